@@ -1,0 +1,210 @@
+#!/usr/bin/env python3
+"""Bench: MoE-layer us/token and HBM GB/s, Qwen3-30B-A3B-shaped Q4_K/Q6_K decode.
+
+One step = one decode token through all 48 stacked MoE layers (router tail,
+grouped expert FFN, combine into the residual, and rms_norm between layers),
+every layer with its own synthetic weights resident in HBM (18.8 GB), the
+activation chain never leaving the device.  Inputs are resident before the
+timed region starts.
+
+Prints ONE JSON line (rank 0).  `value` is microseconds per MoE layer per token
+(lower is better); `roofline` covers the dominant kernel, timed with HIP event
+pairs on its own stream; `cpu_baseline` is the C restatement of ggml-CPU's
+algorithm for the same stage on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--shape", default="qwen3_30b", choices=["qwen3_30b", "qwen3_next", "olmoe"])
+    ap.add_argument("--layers", type=int, default=None, help="stacked layers (default: the shape's)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_bytes(shape, kind: int) -> int:
+    """Algorithmic HBM bytes of one launch of each kernel for one token."""
+    from hoard_amd import KERNEL_DOWN, KERNEL_GATEUP, KERNEL_ROUTER, expert_bytes
+    s = shape
+    n = s.n_embd
+    if kind == KERNEL_ROUTER:
+        return 4 * s.n_expert * n + 4 * n + 4 * n  # W, x in, fx out
+    sh = bool(s.n_ff_shexp)
+    if kind == KERNEL_GATEUP:
+        b = s.n_used * (expert_bytes(s.gate_type, s.n_ff, n) + expert_bytes(s.up_type, s.n_ff, n))
+        if sh:
+            b += expert_bytes(s.sh_gate_type, s.n_ff_shexp, n) + expert_bytes(s.sh_up_type, s.n_ff_shexp, n)
+            b += 4 * n  # shared gate row
+        return b + 4 * n + 4 * (s.n_used * s.n_ff + s.n_ff_shexp)  # fx in, h out
+    if kind == KERNEL_DOWN:
+        b = s.n_used * expert_bytes(s.down_type, n, s.n_ff)
+        if sh:
+            b += expert_bytes(s.sh_down_type, n, s.n_ff_shexp)
+        return b + 4 * (s.n_used * s.n_ff + s.n_ff_shexp) + 8 * n  # h in, res in, out
+    raise ValueError(kind)
+
+
+def cpu_baseline(shape, seed: int, budget_s: float):
+    """The oracle (C restatement of ggml-CPU's algorithm) on host cores."""
+    import oracle
+    from hoard_amd import workloads as W
+    threads = min(16, os.cpu_count() or 1)
+    oracle.lib().orc_set_num_threads(threads)
+    n_host_layers = 4
+    layers = [W.make_layer(shape, seed, l) for l in range(n_host_layers)]
+    toks = [W.make_hidden(shape, seed, 1000 + t % 16, t) for t in range(16)]
+    oracle.moe_layer(layers[0], *toks[0])  # warm
+    done, t0 = 0, time.perf_counter()
+    while True:
+        fx, res = toks[done % len(toks)]
+        oracle.moe_layer(layers[done % n_host_layers], fx, res)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and done >= 8:
+            break
+    us = el / done * 1e6
+    return {
+        "value": round(us, 2), "unit": "us/layer", "cores": threads, "kind": "port",
+        "sample": f"{done} token-layers of the same shape cycling {n_host_layers} distinct layers "
+                  f"({shape.name}, fresh hidden per token), OpenMP over rows, {el:.1f} s",
+        "tokens_per_s_48_layers": round(1e6 / (us * 48), 3),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the MoE stage would shard by expert id; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import hoard_amd as H
+    from hoard_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    lib = H.load_library()
+    shape = W.SHAPES[args.shape]
+    n_layer = args.layers or shape.n_layer
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---- resident weights: 48 independent synthetic layers -------------------
+    t0 = time.perf_counter()
+    cfg = shape.cfg(n_layer)
+    h = ctypes.c_void_p()
+    H.check(lib.hoard_moe_create(ctypes.byref(cfg), ctypes.byref(h)))
+    hl = W.make_layer(shape, args.seed, 0)
+    for l in range(n_layer):
+        if l:
+            W.fill_layer(hl, args.seed, l)
+        w = hl.weights()
+        H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(w)))
+    del hl
+    log(f"[bench] {n_layer} layers of {shape.name} resident ({n_layer * shape.n_expert * shape.expert_bytes() / 1e9:.1f} GB "
+        f"experts) in {time.perf_counter() - t0:.1f} s")
+
+    # ---- one input token per step, already on device --------------------------
+    steps, warm = args.steps, args.warmup
+    xs = torch.stack([torch.from_numpy(W.make_hidden(shape, args.seed, 0, t)[1]) for t in range(steps + warm)]).to(dev)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    eps = ctypes.c_float(W.RMS_EPS)
+
+    def step(i):
+        H.check(lib.hoard_moe_decode(h, 0, n_layer, ctypes.c_void_p(xs[i].data_ptr()), eps, sp))
+
+    for i in range(warm):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(warm, warm + steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = ev0.elapsed_time(ev1) / steps
+    us_layer = ms_per_step * 1000.0 / n_layer
+    assert torch.isfinite(xs).all().item(), "non-finite decode output"
+
+    # ---- per-kernel durations: event pair around every launch ------------------
+    H.check(lib.hoard_moe_profile(h, 1))
+    for i in range(warm, warm + steps):
+        step(i)
+    kt = H.KernelTimes()
+    H.check(lib.hoard_moe_profile_read(h, ctypes.byref(kt)))
+    H.check(lib.hoard_moe_profile(h, 0))
+    kernels = {}
+    for kind, name in H.KERNEL_NAMES.items():
+        n = kt.launches[kind]
+        if n:
+            avg_us = kt.total_ms[kind] / n * 1000.0
+            b = kernel_bytes(shape, kind)
+            kernels[name] = {"launches": int(n), "avg_us": round(avg_us, 3), "bytes": b,
+                             "gbps": round(b / avg_us / 1e3, 1)}
+    dom = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
+    dk = kernels[dom]
+
+    layer_bytes = shape.bytes_per_token_layer()
+    layer_gbps = layer_bytes / (us_layer * 1e3)
+    result = {
+        "metric": "MoE-layer us/token + HBM GB/s (% of peak), Qwen3-30B-A3B-shape Q4_K decode",
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_K/q6_K weights x q8_K activations (int8 dot), f32 router/accumulate",
+        "data": "synthetic (seeded random Q4_K/Q6_K super-blocks, f32 router, N(0,1) hidden)",
+        "config": {"workload": f"{shape.name}: {n_layer} stacked MoE layers, batch-1 decode, "
+                               f"hidden {shape.n_embd}, {shape.n_expert} experts top-{shape.n_used}, "
+                               f"ff {shape.n_ff}, all experts resident in HBM",
+                   "tokens_per_step": 1, "layers": n_layer},
+        "tokens_per_s": round(1000.0 / ms_per_step, 2),
+        "layer_hbm_gbps": round(layer_gbps, 1),
+        "layer_hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
+        "layer_bytes": layer_bytes,
+        "kernels": kernels,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(dk["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    lib.hoard_moe_destroy(h)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

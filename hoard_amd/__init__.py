@@ -1,0 +1,122 @@
+"""hoard_amd -- MI355X-native MoE expert stage of bgallon-dev/hoard.
+
+The product is libhoard_moe.so (C++ orchestrator + HIP kernels for gfx950)
+behind the C ABI in include/hoard_moe.h.  This module is ctypes plumbing for
+tests and the bench: it loads the in-tree library and raises if it has not
+been built -- there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libhoard_moe.so"
+
+TYPE_F32 = 0
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+
+OK = 0
+ERR_INVALID = -1
+ERR_UNSUPPORTED = -2
+ERR_HIP = -3
+ERR_OOM = -4
+ERR_STATE = -5
+
+
+class HoardError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"hoard error {code}: {msg}")
+        self.code = code
+
+
+class MoeCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "n_embd", "n_expert", "n_used", "n_ff", "n_ff_shexp", "n_layer", "renorm", "pool_k",
+        "max_tokens")]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [
+        ("router", ctypes.c_void_p),
+        ("gate_type", ctypes.c_int32), ("up_type", ctypes.c_int32), ("down_type", ctypes.c_int32),
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+        ("sh_gate_type", ctypes.c_int32), ("sh_up_type", ctypes.c_int32), ("sh_down_type", ctypes.c_int32),
+        ("sh_gate", ctypes.c_void_p), ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p),
+        ("sh_gate_inp", ctypes.c_void_p),
+    ]
+
+
+class MoeStats(ctypes.Structure):
+    _fields_ = [
+        ("reqs", ctypes.c_uint64), ("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64),
+        ("bytes_h2d", ctypes.c_uint64), ("tokens", ctypes.c_uint64),
+        ("expert_hist", ctypes.c_uint64 * 1024), ("last_unique", ctypes.c_int32),
+    ]
+
+
+KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN = 0, 1, 2
+KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "down_combine"}
+
+
+class KernelTimes(ctypes.Structure):
+    _fields_ = [("launches", ctypes.c_uint64 * 8), ("total_ms", ctypes.c_double * 8)]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+# name -> (restype, argtypes); every symbol the public headers declare
+ABI = {
+    "hoard_last_error": (ctypes.c_char_p, []),
+    "hoard_moe_create": (_I, [ctypes.POINTER(MoeCfg), ctypes.POINTER(_P)]),
+    "hoard_moe_destroy": (None, [_P]),
+    "hoard_moe_set_layer_weights": (_I, [_P, _I, ctypes.POINTER(LayerWeights)]),
+    "hoard_moe_route": (_I, [_P, _I, _P, _P, _P, _P]),
+    "hoard_moe_ffn_combine": (_I, [_P, _I, _P, _P, _P, _P, _P, _P]),
+    "hoard_moe_layer": (_I, [_P, _I, _P, _P, _P, _P, _P, _P]),
+    "hoard_moe_decode": (_I, [_P, _I, _I, _P, ctypes.c_float, _P]),
+    "hoard_moe_profile": (_I, [_P, _I]),
+    "hoard_moe_profile_read": (_I, [_P, ctypes.POINTER(KernelTimes)]),
+    "hoard_synth_key": (ctypes.c_uint64, [ctypes.c_uint32] * 5),
+    "hoard_synth_fill_blocks": (_I, [_I, ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),
+    "hoard_synth_fill_normal": (None, [ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),
+    "hoard_synth_fill_experts": (_I, [_I, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      ctypes.c_uint32, _I, _I, _I, _P, ctypes.c_float]),
+    "hoard_synth_expert_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+}
+
+_lib = None
+
+
+def load_library(path: Path | None = None) -> ctypes.CDLL:
+    """Load the in-tree libhoard_moe.so; raise if it was never built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise HoardError(ERR_STATE, f"{p} is not built: run __graft_entry__.build() "
+                                    "(or python -m hoard_amd.build) first")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in ABI.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise HoardError(rc, load_library().hoard_last_error().decode())
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    return (cols // 256) * BLOCK_BYTES[qtype]
+
+
+def expert_bytes(qtype: int, rows: int, cols: int) -> int:
+    return rows * row_bytes(qtype, cols)

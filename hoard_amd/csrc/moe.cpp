@@ -1,0 +1,425 @@
+// C++ orchestrator behind the C ABI in include/hoard_moe.h.
+//
+// Mirrors the reference's per-layer stage order (src/run_moe_stream.cpp:
+// router tail :353-373 -> slot fetch :379-421 -> graph B :424-445 -> combine
+// :447) with every step a device launch on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "hoard_moe.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) return fail(HOARD_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr size_t kTailPad = 256;  // kernels read up to 15 bytes past a staged run
+
+bool quant_type_ok(int t) { return t == HOARD_TYPE_Q4_K || t == HOARD_TYPE_Q6_K; }
+
+size_t mat_bytes(int type, int rows, int cols) {
+    return (size_t)rows * (size_t)(cols / 256) * hoard::block_bytes(type);
+}
+
+struct Layer {
+    bool loaded = false;
+    float *router = nullptr;
+    int gate_type = 0, up_type = 0, down_type = 0;
+    size_t gstride = 0, ustride = 0, dstride = 0;
+    uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    int sh_gate_type = 0, sh_up_type = 0, sh_down_type = 0;
+    uint8_t *sh_gate = nullptr, *sh_up = nullptr, *sh_down = nullptr;
+    float *sh_gate_inp = nullptr;
+};
+
+}  // namespace
+
+struct hoard_moe {
+    hoard_moe_cfg cfg{};
+    int device = 0;
+    std::vector<Layer> layers;
+    // per-call device scratch
+    float *fx = nullptr;          // [max_tokens][n_embd]
+    float *logits = nullptr;      // [max_tokens][n_expert]
+    unsigned *counters = nullptr; // [max_tokens]
+    int32_t *sel = nullptr;       // [max_tokens][n_used]
+    float *wsel = nullptr;        // [max_tokens][n_used]
+    float *sgate = nullptr;       // [max_tokens]
+    float *hbuf = nullptr;        // [n_used+1][hstride]
+    int hstride = 0;
+    hoard_moe_stats stats{};
+    // per-launch event pairs while profiling is enabled
+    bool profiling = false;
+    struct Mark {
+        int kind;
+        hipEvent_t a, b;
+    };
+    std::vector<Mark> marks;
+    std::vector<hipEvent_t> event_pool;
+
+    ~hoard_moe() {
+        for (auto &m : marks) {
+            hipEventDestroy(m.a);
+            hipEventDestroy(m.b);
+        }
+        for (auto e : event_pool) hipEventDestroy(e);
+        for (auto &L : layers) free_layer(L);
+        hipFree(fx);
+        hipFree(logits);
+        hipFree(counters);
+        hipFree(sel);
+        hipFree(wsel);
+        hipFree(sgate);
+        hipFree(hbuf);
+    }
+    static void free_layer(Layer &L) {
+        hipFree(L.router);
+        hipFree(L.gate);
+        hipFree(L.up);
+        hipFree(L.down);
+        hipFree(L.sh_gate);
+        hipFree(L.sh_up);
+        hipFree(L.sh_down);
+        hipFree(L.sh_gate_inp);
+        L = Layer{};
+    }
+};
+
+namespace {
+
+int dev_alloc(void **p, size_t n) {
+    hipError_t e = hipMalloc(p, n);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+        return fail(HOARD_ERR_OOM, "hipMalloc(%zu): %s", n, hipGetErrorString(e));
+    }
+    return HOARD_OK;
+}
+
+int upload(void **dst, const void *src, size_t n, size_t alloc) {
+    int rc = dev_alloc(dst, alloc);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpy(*dst, src, n, hipMemcpyHostToDevice));
+    return HOARD_OK;
+}
+
+int check_layer(hoard_moe *h, int layer) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    if (layer < 0 || layer >= h->cfg.n_layer) return fail(HOARD_ERR_INVALID, "layer %d out of range", layer);
+    if (!h->layers[layer].loaded) return fail(HOARD_ERR_STATE, "layer %d has no weights", layer);
+    HIP_TRY(hipSetDevice(h->device));
+    return HOARD_OK;
+}
+
+hoard::MatDesc mat(const uint8_t *base, size_t stride, int type, int rows, int cols, int n_ids) {
+    hoard::MatDesc m;
+    m.base = base;
+    m.stride = stride;
+    m.type = type;
+    m.rows = rows;
+    m.cols = cols;
+    m.n_ids = n_ids;
+    return m;
+}
+
+hipEvent_t take_event(hoard_moe *h) {
+    if (!h->event_pool.empty()) {
+        hipEvent_t e = h->event_pool.back();
+        h->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Brackets one launch with an event pair when profiling; no-op otherwise.
+struct KernelMark {
+    hoard_moe *h;
+    int kind;
+    hipStream_t s;
+    hipEvent_t a = nullptr;
+    KernelMark(hoard_moe *h_, int kind_, hipStream_t s_) : h(h_), kind(kind_), s(s_) {
+        if (h->profiling && (a = take_event(h))) hipEventRecord(a, s);
+    }
+    ~KernelMark() {
+        if (!a) return;
+        hipEvent_t b = take_event(h);
+        if (!b) {
+            h->event_pool.push_back(a);
+            return;
+        }
+        hipEventRecord(b, s);
+        h->marks.push_back({kind, a, b});
+    }
+};
+
+int run_route(hoard_moe *h, const Layer &L, const float *xin, int is_residual, float eps, int32_t *sel,
+              float *w, hipStream_t s) {
+    const hoard_moe_cfg &c = h->cfg;
+    hoard::RouterArgs a{};
+    a.xin = xin;
+    a.fx_out = h->fx;
+    a.eps = eps;
+    a.xin_is_residual = is_residual;
+    a.w = L.router;
+    a.n = c.n_embd;
+    a.E = c.n_expert;
+    a.k = c.n_used;
+    a.renorm = c.renorm;
+    a.M = 1;
+    a.logits = h->logits;
+    a.counters = h->counters;
+    a.sel = sel;
+    a.wsel = w;
+    KernelMark mark(h, HOARD_KERNEL_ROUTER, s);
+    HIP_TRY(hoard::launch_router(a, s));
+    return HOARD_OK;
+}
+
+int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, const float *w,
+            const float *res, float *out, hipStream_t s) {
+    const hoard_moe_cfg &c = h->cfg;
+    const int n_ids = c.n_expert;
+    const bool sh = c.n_ff_shexp > 0;
+    hoard::GateUpArgs g{};
+    g.fx = fx;
+    g.ids = ids;
+    g.gate = mat(L.gate, L.gstride, L.gate_type, c.n_ff, c.n_embd, n_ids);
+    g.up = mat(L.up, L.ustride, L.up_type, c.n_ff, c.n_embd, n_ids);
+    if (sh) {
+        g.sh_gate = mat(L.sh_gate, 0, L.sh_gate_type, c.n_ff_shexp, c.n_embd, 1);
+        g.sh_up = mat(L.sh_up, 0, L.sh_up_type, c.n_ff_shexp, c.n_embd, 1);
+        g.sh_gate_inp = L.sh_gate_inp;
+    }
+    g.sgate = h->sgate;
+    g.n_embd = c.n_embd;
+    g.k = c.n_used;
+    g.h = h->hbuf;
+    g.hstride = h->hstride;
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_GATEUP, s);
+        e = hoard::launch_gateup(g, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "gate/up launch: %s", hipGetErrorString(e));
+
+    hoard::DownArgs d{};
+    d.h = h->hbuf;
+    d.hstride = h->hstride;
+    d.ids = ids;
+    d.w = w;
+    d.down = mat(L.down, L.dstride, L.down_type, c.n_embd, c.n_ff, n_ids);
+    if (sh) d.sh_down = mat(L.sh_down, 0, L.sh_down_type, c.n_embd, c.n_ff_shexp, 1);
+    d.sgate = h->sgate;
+    d.n_embd = c.n_embd;
+    d.k = c.n_used;
+    d.res = res;
+    d.out = out;
+    {
+        KernelMark mark(h, HOARD_KERNEL_DOWN, s);
+        e = hoard::launch_down_combine(d, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "down/combine launch: %s", hipGetErrorString(e));
+    return HOARD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *hoard_last_error(void) { return g_err.c_str(); }
+
+int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
+    g_err.clear();
+    if (!cfg || !out) return fail(HOARD_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const hoard_moe_cfg &c = *cfg;
+    if (c.n_embd <= 0 || c.n_embd % 256) return fail(HOARD_ERR_INVALID, "n_embd %d not a positive multiple of 256", c.n_embd);
+    if (c.n_ff <= 0 || c.n_ff % 256) return fail(HOARD_ERR_INVALID, "n_ff %d not a positive multiple of 256", c.n_ff);
+    if (c.n_ff_shexp < 0 || c.n_ff_shexp % 256) return fail(HOARD_ERR_INVALID, "n_ff_shexp %d not a multiple of 256", c.n_ff_shexp);
+    if (c.n_expert <= 0 || c.n_expert > 1024) return fail(HOARD_ERR_INVALID, "n_expert %d outside 1..1024", c.n_expert);
+    if (c.n_used <= 0 || c.n_used > 16 || c.n_used > c.n_expert)
+        return fail(HOARD_ERR_INVALID, "n_used %d outside 1..min(16, n_expert)", c.n_used);
+    if (c.n_layer <= 0) return fail(HOARD_ERR_INVALID, "n_layer %d", c.n_layer);
+    if (c.max_tokens <= 0) return fail(HOARD_ERR_INVALID, "max_tokens %d", c.max_tokens);
+    if (c.pool_k != 0) return fail(HOARD_ERR_UNSUPPORTED, "pool_k > 0 not available in this build");
+    hoard_moe *h = new (std::nothrow) hoard_moe();
+    if (!h) return fail(HOARD_ERR_OOM, "handle");
+    h->cfg = c;
+    if (hipGetDevice(&h->device) != hipSuccess) {
+        delete h;
+        return fail(HOARD_ERR_HIP, "no HIP device");
+    }
+    h->layers.resize(c.n_layer);
+    h->hstride = c.n_ff > c.n_ff_shexp ? c.n_ff : c.n_ff_shexp;
+    const size_t T = (size_t)c.max_tokens;
+    int rc = 0;
+    rc = rc ? rc : dev_alloc((void **)&h->fx, T * c.n_embd * sizeof(float));
+    rc = rc ? rc : dev_alloc((void **)&h->logits, T * c.n_expert * sizeof(float));
+    rc = rc ? rc : dev_alloc((void **)&h->counters, T * sizeof(unsigned));
+    rc = rc ? rc : dev_alloc((void **)&h->sel, T * c.n_used * sizeof(int32_t));
+    rc = rc ? rc : dev_alloc((void **)&h->wsel, T * c.n_used * sizeof(float));
+    rc = rc ? rc : dev_alloc((void **)&h->sgate, T * sizeof(float));
+    rc = rc ? rc : dev_alloc((void **)&h->hbuf, (size_t)(c.n_used + 1) * h->hstride * sizeof(float));
+    if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
+        rc = fail(HOARD_ERR_HIP, "hipMemset counters");
+    if (rc) {
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return HOARD_OK;
+}
+
+void hoard_moe_destroy(hoard_moe *h) {
+    if (!h) return;
+    hipSetDevice(h->device);
+    hipDeviceSynchronize();
+    delete h;
+}
+
+int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weights *w) {
+    if (!h || !w) return fail(HOARD_ERR_INVALID, "null argument");
+    if (layer < 0 || layer >= h->cfg.n_layer) return fail(HOARD_ERR_INVALID, "layer %d out of range", layer);
+    const hoard_moe_cfg &c = h->cfg;
+    if (!w->router || !w->gate || !w->up || !w->down) return fail(HOARD_ERR_INVALID, "missing tensor");
+    if (!quant_type_ok(w->gate_type) || !quant_type_ok(w->up_type) || !quant_type_ok(w->down_type))
+        return fail(HOARD_ERR_UNSUPPORTED, "expert types %d/%d/%d: only Q4_K (12) and Q6_K (14)", w->gate_type,
+                    w->up_type, w->down_type);
+    const bool sh = c.n_ff_shexp > 0;
+    if (sh) {
+        if (!w->sh_gate || !w->sh_up || !w->sh_down || !w->sh_gate_inp)
+            return fail(HOARD_ERR_INVALID, "n_ff_shexp > 0 but shared-expert tensors missing");
+        if (!quant_type_ok(w->sh_gate_type) || !quant_type_ok(w->sh_up_type) || !quant_type_ok(w->sh_down_type))
+            return fail(HOARD_ERR_UNSUPPORTED, "shared expert types %d/%d/%d", w->sh_gate_type, w->sh_up_type,
+                        w->sh_down_type);
+    }
+    HIP_TRY(hipSetDevice(h->device));
+    Layer &L = h->layers[layer];
+    hoard_moe::free_layer(L);
+    L.gate_type = w->gate_type;
+    L.up_type = w->up_type;
+    L.down_type = w->down_type;
+    L.gstride = mat_bytes(L.gate_type, c.n_ff, c.n_embd);
+    L.ustride = mat_bytes(L.up_type, c.n_ff, c.n_embd);
+    L.dstride = mat_bytes(L.down_type, c.n_embd, c.n_ff);
+    const size_t E = (size_t)c.n_expert;
+    int rc = 0;
+    const size_t rb = (size_t)c.n_expert * c.n_embd * sizeof(float);
+    rc = rc ? rc : upload((void **)&L.router, w->router, rb, rb);
+    rc = rc ? rc : upload((void **)&L.gate, w->gate, E * L.gstride, E * L.gstride + kTailPad);
+    rc = rc ? rc : upload((void **)&L.up, w->up, E * L.ustride, E * L.ustride + kTailPad);
+    rc = rc ? rc : upload((void **)&L.down, w->down, E * L.dstride, E * L.dstride + kTailPad);
+    if (sh && !rc) {
+        L.sh_gate_type = w->sh_gate_type;
+        L.sh_up_type = w->sh_up_type;
+        L.sh_down_type = w->sh_down_type;
+        const size_t sg = mat_bytes(L.sh_gate_type, c.n_ff_shexp, c.n_embd);
+        const size_t su = mat_bytes(L.sh_up_type, c.n_ff_shexp, c.n_embd);
+        const size_t sd = mat_bytes(L.sh_down_type, c.n_embd, c.n_ff_shexp);
+        rc = rc ? rc : upload((void **)&L.sh_gate, w->sh_gate, sg, sg + kTailPad);
+        rc = rc ? rc : upload((void **)&L.sh_up, w->sh_up, su, su + kTailPad);
+        rc = rc ? rc : upload((void **)&L.sh_down, w->sh_down, sd, sd + kTailPad);
+        rc = rc ? rc : upload((void **)&L.sh_gate_inp, w->sh_gate_inp, c.n_embd * sizeof(float), c.n_embd * sizeof(float));
+    }
+    if (rc) {
+        hoard_moe::free_layer(L);
+        return rc;
+    }
+    L.loaded = true;
+    return HOARD_OK;
+}
+
+int hoard_moe_route(hoard_moe *h, int layer, const float *fx_dev, int32_t *sel_dev, float *w_dev,
+                    void *stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    if (!fx_dev || !sel_dev || !w_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
+    return run_route(h, h->layers[layer], fx_dev, 0, 0.0f, sel_dev, w_dev, (hipStream_t)stream);
+}
+
+int hoard_moe_ffn_combine(hoard_moe *h, int layer, const float *fx_dev, const int32_t *ids_dev,
+                          const float *w_dev, const float *res_dev, float *out_dev, void *stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    if (!fx_dev || !ids_dev || !w_dev || !res_dev || !out_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
+    return run_ffn(h, h->layers[layer], fx_dev, ids_dev, w_dev, res_dev, out_dev, (hipStream_t)stream);
+}
+
+int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *res_dev, float *out_dev,
+                    int32_t *sel_dev, float *w_dev, void *stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    if (!fx_dev || !res_dev || !out_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
+    int32_t *sel = sel_dev ? sel_dev : h->sel;
+    float *w = w_dev ? w_dev : h->wsel;
+    const Layer &L = h->layers[layer];
+    rc = run_route(h, L, fx_dev, 0, 0.0f, sel, w, (hipStream_t)stream);
+    if (rc) return rc;
+    return run_ffn(h, L, fx_dev, sel, w, res_dev, out_dev, (hipStream_t)stream);
+}
+
+int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps, void *stream) {
+    if (!h || !x_dev) return fail(HOARD_ERR_INVALID, "null argument");
+    if (layer_begin < 0 || layer_end > h->cfg.n_layer || layer_begin > layer_end)
+        return fail(HOARD_ERR_INVALID, "layer range [%d,%d)", layer_begin, layer_end);
+    hipStream_t s = (hipStream_t)stream;
+    for (int l = layer_begin; l < layer_end; ++l) {
+        int rc = check_layer(h, l);
+        if (rc) return rc;
+        const Layer &L = h->layers[l];
+        rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
+        if (rc) return rc;
+        rc = run_ffn(h, L, h->fx, h->sel, h->wsel, x_dev, x_dev, s);
+        if (rc) return rc;
+    }
+    return HOARD_OK;
+}
+
+int hoard_moe_profile(hoard_moe *h, int enable) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    h->profiling = enable != 0;
+    return HOARD_OK;
+}
+
+int hoard_moe_profile_read(hoard_moe *h, hoard_moe_kernel_times *out) {
+    if (!h || !out) return fail(HOARD_ERR_INVALID, "null argument");
+    std::memset(out, 0, sizeof *out);
+    HIP_TRY(hipSetDevice(h->device));
+    if (!h->marks.empty()) HIP_TRY(hipEventSynchronize(h->marks.back().b));
+    for (auto &m : h->marks) {
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, m.a, m.b));
+        out->launches[m.kind] += 1;
+        out->total_ms[m.kind] += ms;
+        h->event_pool.push_back(m.a);
+        h->event_pool.push_back(m.b);
+    }
+    h->marks.clear();
+    return HOARD_OK;
+}
+
+}  // extern "C"

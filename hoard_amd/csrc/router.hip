@@ -1,0 +1,167 @@
+// Fused router tail (kernel family 1): f32 router GEMV, softmax over all
+// experts, top-k, gather and optional renorm, in one launch.
+//
+// Replaces ggml_mul_mat(ffn_gate_inp, fx) + ggml_soft_max + ggml_top_k +
+// ggml_get_rows (src/run_moe_stream.cpp:353-356, src/run_qwen35.cpp:556-559)
+// and the host renorm (src/run_moe_stream.cpp:371-373).
+//
+// Layout: one 64-lane wave per workgroup computes two router rows; lane l of a
+// row owns elements l, l+32, l+64, ... and keeps one fused multiply-add chain,
+// the same 32 accumulators ggml's x86 f32 dot keeps (4 vectors x 8 lanes), and
+// folds them in that dot's order (16, 8, 4 lanes apart, then pairs), so the
+// logits are the CPU path's bit for bit.  The last workgroup to finish a token
+// (device-scope counter) runs softmax / top-k on one wave.
+#include "kernels.h"
+#include "qblocks.h"
+
+namespace hoard {
+
+namespace {
+
+constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
+constexpr int kMaxK = 16;
+
+__global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
+    const int lane = threadIdx.x;
+    const int half = lane >> 5, l = lane & 31;
+    const int tok = blockIdx.y;
+    const int n = a.n, E = a.E;
+    const float *x = a.xin + (size_t)tok * n;
+    const int row = blockIdx.x * 2 + half;
+
+    float scale = 1.0f;
+    if (a.xin_is_residual) {
+        // rms_norm: mean of x*x accumulated in double, scale = 1/sqrtf(mean + eps)
+        double ss = 0.0;
+        for (int i = lane; i < n; i += 64) {
+            const float v = x[i];
+            ss += (double)(v * v);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        const float mean = (float)(ss / (double)n);
+        scale = 1.0f / sqrtf(mean + a.eps);
+        if (blockIdx.x == 0) {
+            float *fo = a.fx_out + (size_t)tok * n;
+            for (int i = lane; i < n; i += 64) fo[i] = x[i] * scale;
+        }
+    }
+
+    if (row < E) {
+        const float *wr = a.w + (size_t)row * n;
+        float acc = 0.0f;
+        if (a.xin_is_residual) {
+#pragma unroll 8
+            for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l] * scale, acc);
+        } else {
+#pragma unroll 8
+            for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l], acc);
+        }
+        acc = acc + __shfl_xor(acc, 16);
+        acc = acc + __shfl_xor(acc, 8);
+        acc = acc + __shfl_xor(acc, 4);
+        acc = acc + __shfl_xor(acc, 1);
+        acc = acc + __shfl_xor(acc, 2);
+        if (l == 0) a.logits[(size_t)tok * E + row] = acc;
+    }
+
+    // ---- the last workgroup of this token runs the tail ----
+    __shared__ int is_last;
+    __threadfence();
+    if (lane == 0) is_last = atomicAdd(&a.counters[tok], 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+
+    const float *lg = a.logits + (size_t)tok * E;
+    float p[kMaxExpertsPerLane];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kMaxExpertsPerLane; ++t) {
+        const int e = lane + 64 * t;
+        p[t] = e < E ? lg[e] : -INFINITY;
+        mx = p[t] > mx ? p[t] : mx;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(mx, off);
+        mx = o > mx ? o : mx;
+    }
+    // softmax: exp(l - max), sum in double, scale by (float)(1/sum)
+    double sum = 0.0;
+#pragma unroll
+    for (int t = 0; t < kMaxExpertsPerLane; ++t) {
+        const int e = lane + 64 * t;
+        if (e < E) {
+            p[t] = expf(p[t] - mx);
+            sum += (double)p[t];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    const float sc = (float)(1.0 / sum);
+#pragma unroll
+    for (int t = 0; t < kMaxExpertsPerLane; ++t) p[t] = p[t] * sc;
+
+    // top-k: repeated wave argmax, larger probability first, lower index on ties
+    uint32_t taken = 0;
+    int selv[kMaxK];
+    float wv[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j >= a.k) break;
+        float bv = 0.0f;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int t = 0; t < kMaxExpertsPerLane; ++t) {
+            const int e = lane + 64 * t;
+            if (e < E && !((taken >> t) & 1u) && (be == 0x7fffffff || p[t] > bv)) {
+                bv = p[t];
+                be = e;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oe = __shfl_xor(be, off);
+            const bool take = (be == 0x7fffffff) ? (oe != 0x7fffffff)
+                                                 : (oe != 0x7fffffff && (ov > bv || (ov == bv && oe < be)));
+            if (take) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        if ((be & 63) == lane) taken |= 1u << (be >> 6);
+        selv[j] = be;
+        wv[j] = bv;
+    }
+    if (a.renorm) {
+        float ws = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+            if (j < a.k) ws = ws + wv[j];
+        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+            if (j < a.k) wv[j] = wv[j] / ws;
+    }
+    // lane j < k stores entry j (selv/wv are identical on every lane)
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j < a.k && lane == j) {
+            a.sel[(size_t)tok * a.k + j] = selv[j];
+            a.wsel[(size_t)tok * a.k + j] = wv[j];
+        }
+    }
+    if (lane == 0) a.counters[tok] = 0u;
+}
+
+}  // namespace
+
+hipError_t launch_router(const RouterArgs &a, hipStream_t s) {
+    dim3 grid((unsigned)((a.E + 1) / 2), (unsigned)a.M);
+    hipLaunchKernelGGL(router_kernel, grid, dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace hoard

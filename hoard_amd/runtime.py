@@ -1,0 +1,108 @@
+"""Python handle over the C ABI, with torch providing device memory and streams.
+
+torch is plumbing here: it allocates the activation buffers the ABI reads and
+writes and hands over its current HIP stream.  Every computation is a call
+into libhoard_moe.so.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import check, load_library
+
+
+def _torch():
+    import torch  # deferred: the CPU-only tests never need a device
+    return torch
+
+
+class MoEStage:
+    """One hoard_moe handle.  layers: {layer index: workloads.HostLayer}."""
+
+    def __init__(self, shape, n_layer: int | None = None, layers=None, pool_k: int = 0,
+                 max_tokens: int = 1):
+        torch = _torch()
+        if not torch.cuda.is_available():
+            raise RuntimeError("MoEStage needs a HIP device")
+        self.lib = load_library()
+        self.shape = shape
+        self.cfg = shape.cfg(n_layer, pool_k, max_tokens)
+        self.h = ctypes.c_void_p()
+        torch.cuda.init()
+        check(self.lib.hoard_moe_create(ctypes.byref(self.cfg), ctypes.byref(self.h)))
+        for li, hl in (layers or {}).items():
+            self.set_layer(li, hl)
+
+    def close(self):
+        if self.h:
+            self.lib.hoard_moe_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_layer(self, layer: int, hl) -> None:
+        w = hl.weights()
+        check(self.lib.hoard_moe_set_layer_weights(self.h, layer, ctypes.byref(w)))
+
+    # -- device helpers ------------------------------------------------------
+    @staticmethod
+    def stream():
+        return ctypes.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+    @staticmethod
+    def dev(a, dtype=None):
+        torch = _torch()
+        t = torch.as_tensor(np.ascontiguousarray(a))
+        if dtype is not None:
+            t = t.to(dtype)
+        return t.to("cuda")
+
+    @staticmethod
+    def ptr(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    # -- ABI calls (numpy in, numpy out; synchronous) ------------------------
+    def route(self, layer: int, fx: np.ndarray):
+        torch = _torch()
+        s = self.shape
+        fx_d = self.dev(fx)
+        sel = torch.empty(s.n_used, dtype=torch.int32, device="cuda")
+        w = torch.empty(s.n_used, dtype=torch.float32, device="cuda")
+        check(self.lib.hoard_moe_route(self.h, layer, self.ptr(fx_d), self.ptr(sel), self.ptr(w), self.stream()))
+        torch.cuda.synchronize()
+        return sel.cpu().numpy(), w.cpu().numpy()
+
+    def ffn_combine(self, layer: int, fx, ids, w, res):
+        torch = _torch()
+        fx_d, ids_d, w_d, res_d = self.dev(fx), self.dev(ids, torch.int32), self.dev(w), self.dev(res)
+        out = torch.empty_like(res_d)
+        check(self.lib.hoard_moe_ffn_combine(self.h, layer, self.ptr(fx_d), self.ptr(ids_d), self.ptr(w_d),
+                                             self.ptr(res_d), self.ptr(out), self.stream()))
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def layer(self, layer: int, fx, res):
+        torch = _torch()
+        s = self.shape
+        fx_d, res_d = self.dev(fx), self.dev(res)
+        out = torch.empty_like(res_d)
+        sel = torch.empty(s.n_used, dtype=torch.int32, device="cuda")
+        w = torch.empty(s.n_used, dtype=torch.float32, device="cuda")
+        check(self.lib.hoard_moe_layer(self.h, layer, self.ptr(fx_d), self.ptr(res_d), self.ptr(out),
+                                       self.ptr(sel), self.ptr(w), self.stream()))
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
+
+    def decode(self, x, layer_begin: int, layer_end: int, eps: float):
+        torch = _torch()
+        x_d = self.dev(x)
+        check(self.lib.hoard_moe_decode(self.h, layer_begin, layer_end, self.ptr(x_d), ctypes.c_float(eps),
+                                        self.stream()))
+        torch.cuda.synchronize()
+        return x_d.cpu().numpy()

@@ -1,0 +1,149 @@
+/*
+ * hoard_moe.h -- C ABI of the MI355X MoE expert stage.
+ *
+ * Drop-in for the per-layer expert stage of bgallon-dev/hoard: the router tail
+ * of "graph A", the VRAM expert-slot pool, "graph B" (expert FFN over the
+ * selected experts) and the host weighted combine.  Every call is extern "C",
+ * returns 0 on success or a negative HOARD_ERR_* code (hoard_last_error()
+ * then describes it), throws nothing across the boundary and takes the
+ * hipStream_t to run on as a void*.  A handle is not thread-safe: use one
+ * handle per host thread, as the reference keeps all ggml/device calls on one
+ * thread (src/run_moe_stream.cpp:415).
+ *
+ * Weights cross the boundary as raw GGUF-layout bytes (expert e of a
+ * [n_expert] tensor at e*stride, src/run_moe_stream.cpp:177-179); activations
+ * are fp32 device pointers.
+ */
+#ifndef HOARD_MOE_H
+#define HOARD_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define HOARD_OK 0
+#define HOARD_ERR_INVALID (-1)     /* bad argument or shape */
+#define HOARD_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. quant type) */
+#define HOARD_ERR_HIP (-3)         /* HIP runtime error */
+#define HOARD_ERR_OOM (-4)         /* device or pinned host allocation failed */
+#define HOARD_ERR_STATE (-5)       /* call not valid in the handle's state */
+
+/* ggml type ids accepted for expert tensors (ggml.h enum ggml_type). */
+#define HOARD_TYPE_F32 0
+#define HOARD_TYPE_Q4_K 12
+#define HOARD_TYPE_Q6_K 14
+
+typedef struct hoard_moe hoard_moe;
+
+/* Stage shape.  Replaces the hparams the reference reads from GGUF in
+   load_model (src/run_moe_stream.cpp:128-150, src/run_qwen35.cpp:161-172)
+   plus the pool size K (src/run_moe_stream.cpp:232). */
+typedef struct hoard_moe_cfg {
+    int32_t n_embd;     /* hidden size, multiple of 256 */
+    int32_t n_expert;   /* routed experts per layer, <= 1024 */
+    int32_t n_used;     /* experts per token (top-k), 1..16 */
+    int32_t n_ff;       /* routed expert intermediate, multiple of 256 */
+    int32_t n_ff_shexp; /* shared expert intermediate (multiple of 256), 0 = none */
+    int32_t n_layer;
+    int32_t renorm;     /* norm_topk_prob: 1 renormalises the top-k weights (wnorm, :150) */
+    int32_t pool_k;     /* 0: every expert resident in HBM; >0: K HBM slots per layer
+                           filled from pinned host memory (the reference's Slots, :193-203) */
+    int32_t max_tokens; /* largest M accepted by hoard_moe_forward_batched (>= 1) */
+} hoard_moe_cfg;
+
+/* One layer's weights, host pointers to GGUF-layout bytes.  Types are per layer
+   (mixed quantisation across layers, src/run_moe_stream.cpp:177-179). */
+typedef struct hoard_layer_weights {
+    const float *router;  /* ffn_gate_inp [n_expert][n_embd] f32 */
+    int32_t gate_type, up_type, down_type;
+    const void *gate;     /* ffn_gate_exps: n_expert x (n_ff rows of n_embd) */
+    const void *up;       /* ffn_up_exps:   n_expert x (n_ff rows of n_embd) */
+    const void *down;     /* ffn_down_exps: n_expert x (n_embd rows of n_ff) */
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
+    const void *sh_gate;  /* ffn_gate_shexp (n_ff_shexp rows of n_embd), or NULL */
+    const void *sh_up;    /* ffn_up_shexp */
+    const void *sh_down;  /* ffn_down_shexp (n_embd rows of n_ff_shexp) */
+    const float *sh_gate_inp; /* ffn_gate_inp_shexp [n_embd] f32 */
+} hoard_layer_weights;
+
+typedef struct hoard_moe_stats {
+    uint64_t reqs;       /* expert requests seen by the pool (reference `reqs`, :264) */
+    uint64_t hits;       /* requests served from an HBM slot (`vram_hit`) */
+    uint64_t misses;     /* requests that needed an upload (`copies`) */
+    uint64_t bytes_h2d;  /* bytes uploaded host -> HBM */
+    uint64_t tokens;     /* tokens routed through hoard_moe_forward_batched */
+    uint64_t expert_hist[1024]; /* per-expert token count of the last batched call */
+    int32_t last_unique; /* unique experts in the last batched call */
+} hoard_moe_stats;
+
+/* Text of the last error on this host thread ("" if none). */
+const char *hoard_last_error(void);
+
+/* Creates a handle and allocates the device state for cfg: resident expert
+   tensors (pool_k == 0) or K slots per layer plus pinned host masters
+   (pool_k > 0), the router weights and per-call scratch.  Replaces the
+   Slots / KV / weight-buffer set-up of src/run_moe_stream.cpp:237-254. */
+int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out);
+void hoard_moe_destroy(hoard_moe *h);
+
+/* Copies one layer's weights in (synchronously).  Replaces load_model's
+   upload of ffn_gate_inp and the expert byte ranges recorded at
+   src/run_moe_stream.cpp:171-184 (and ggml_backend_tensor_set of the shared
+   expert tensors, src/run_qwen35.cpp:219, 250-253). */
+int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weights *w);
+
+/* Router tail for one token: logits = ffn_gate_inp . fx (f32), softmax over
+   all experts, top-k (descending, ties -> lower index), gather, optional
+   renorm with the 6.103515625e-5 clamp.  Replaces ggml_mul_mat, ggml_soft_max,
+   ggml_top_k, ggml_get_rows at src/run_moe_stream.cpp:353-356 and the host
+   renorm at :371-373.  sel_dev: int32[n_used], w_dev: f32[n_used]. */
+int hoard_moe_route(hoard_moe *h, int layer, const float *fx_dev, int32_t *sel_dev, float *w_dev,
+                    void *stream);
+
+/* Graph B plus the combine for one token: for j in 0..n_used-1 the expert
+   FFN y_j = down(silu(gate x) * up x) of expert ids_dev[j] (an expert id when
+   pool_k == 0, a slot index from hoard_moe_pool_ensure when pool_k > 0), then
+   out[d] = (sum_j w_j*y_j[d]) + shex[d] + res[d], shex being the
+   sigmoid-gated shared expert when n_ff_shexp > 0.  Replaces graph B at
+   src/run_moe_stream.cpp:424-445 (src/run_qwen35.cpp:640-666) and the host
+   combine at :447 (:675-676).  out_dev may alias res_dev. */
+int hoard_moe_ffn_combine(hoard_moe *h, int layer, const float *fx_dev, const int32_t *ids_dev,
+                          const float *w_dev, const float *res_dev, float *out_dev, void *stream);
+
+/* Route + FFN + combine for one token with nothing leaving the device
+   (pool_k == 0).  sel_dev / w_dev receive the selection when non-NULL. */
+int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *res_dev,
+                    float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
+
+/* Stacked decode over layers [layer_begin, layer_end) for one token, in place
+   on x_dev (pool_k == 0): per layer fx = rms_norm(x, eps), x = layer(fx, x).
+   The reference round-trips to the host twice per layer
+   (src/run_moe_stream.cpp:362-370, 441-447); here the chain stays on device. */
+int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps,
+                     void *stream);
+
+/* Per-kernel timing, the device counterpart of the reference's phase timers
+   (tA/tFetch/tB, src/run_moe_stream.cpp:291,311,377,422,448): while enabled,
+   every kernel launch is bracketed by a pair of hipEvents on its stream.
+   hoard_moe_profile_read synchronises on the last event, returns the launch
+   counts and summed durations per kernel kind, and clears them. */
+#define HOARD_KERNEL_ROUTER 0
+#define HOARD_KERNEL_GATEUP 1
+#define HOARD_KERNEL_DOWN 2
+#define HOARD_KERNEL_KINDS 8
+typedef struct hoard_moe_kernel_times {
+    uint64_t launches[HOARD_KERNEL_KINDS];
+    double total_ms[HOARD_KERNEL_KINDS];
+} hoard_moe_kernel_times;
+
+int hoard_moe_profile(hoard_moe *h, int enable);
+int hoard_moe_profile_read(hoard_moe *h, hoard_moe_kernel_times *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
