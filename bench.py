@@ -40,6 +40,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--phases", action="store_true", help="trace one-launch decode phases of one token")
     return ap.parse_args()
 
 
@@ -47,11 +48,13 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_bytes(shape, kind: int) -> int:
+def kernel_bytes(shape, kind: int, n_layer: int) -> int:
     """Algorithmic HBM bytes of one launch of each kernel for one token."""
-    from hoard_amd import KERNEL_DOWN, KERNEL_GATEUP, KERNEL_ROUTER, expert_bytes
+    from hoard_amd import KERNEL_DECODE, KERNEL_DOWN, KERNEL_GATEUP, KERNEL_ROUTER, expert_bytes
     s = shape
     n = s.n_embd
+    if kind == KERNEL_DECODE:  # one launch runs every layer of the token
+        return n_layer * s.bytes_per_token_layer()
     if kind == KERNEL_ROUTER:
         return 4 * s.n_expert * n + 4 * n + 4 * n  # W, x in, fx out
     sh = bool(s.n_ff_shexp)
@@ -67,6 +70,33 @@ def kernel_bytes(shape, kind: int) -> int:
             b += expert_bytes(s.sh_down_type, n, s.n_ff_shexp)
         return b + 4 * (s.n_used * s.n_ff + s.n_ff_shexp) + 8 * n  # h in, res in, out
     raise ValueError(kind)
+
+
+PHASES = ["layer_start", "x_gathered", "router_rows_q8x", "router_rows_q8x_", "logits_gathered_topk",
+          "loads_issued", "gateup_rows_landed", "h_published", "h_gathered_q8h", "down_y_published",
+          "y_gathered_x_published", "y_gathered_x_published_"]
+
+
+def phase_breakdown(lib, h, step, H):
+    """Per-phase time of the one-launch decode: for each boundary, when the slowest
+    workgroup reached it, relative to the previous boundary (median over layers)."""
+    H.check(lib.hoard_moe_phase_trace(h, 1))
+    step()
+    buf = np.zeros(512 * 256 * H.TRACE_PHASES, dtype=np.uint64)
+    nl = ctypes.c_int()
+    H.check(lib.hoard_moe_phase_trace_read(h, ctypes.c_void_p(buf.ctypes.data), buf.size, ctypes.byref(nl)))
+    H.check(lib.hoard_moe_phase_trace(h, 0))
+    if nl.value == 0:
+        return None
+    t = buf[: nl.value * 256 * H.TRACE_PHASES].reshape(nl.value, 256, H.TRACE_PHASES).astype(np.int64)
+    reach = t.max(axis=1)                      # [layer, phase]: slowest workgroup
+    reach[:, 0] = t[:, :, 0].min(axis=1)       # layer start: first workgroup
+    # phases 7..9 are skipped by workgroups without an expert; they hold 0 then
+    d = np.diff(reach, axis=1) * 10e-3         # 100 MHz ticks -> us
+    med = np.median(d[1:] if nl.value > 1 else d, axis=0)
+    out = {f"{PHASES[i]}->{PHASES[i + 1]}": round(float(med[i]), 3) for i in range(len(PHASES) - 1)}
+    out["layer_total"] = round(float(np.median((reach[1:, -1] - reach[1:, 0]) * 10e-3)) if nl.value > 1 else 0.0, 3)
+    return out
 
 
 def cpu_baseline(shape, seed: int, budget_s: float):
@@ -167,7 +197,7 @@ def main():
         n = kt.launches[kind]
         if n:
             avg_us = kt.total_ms[kind] / n * 1000.0
-            b = kernel_bytes(shape, kind)
+            b = kernel_bytes(shape, kind, n_layer)
             kernels[name] = {"launches": int(n), "avg_us": round(avg_us, 3), "bytes": b,
                              "gbps": round(b / avg_us / 1e3, 1)}
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
@@ -200,6 +230,16 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbps"], "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(dk["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
     }
+    if args.phases:
+        ph = phase_breakdown(lib, h, lambda: step(warm), H)
+        if ph:
+            result["phases_us"] = ph
+            for k_, v_ in ph.items():
+                log(f"[phase] {k_:40s} {v_:8.3f} us")
+    persistent = ctypes.c_int()
+    H.check(lib.hoard_moe_get_option(h, H.OPT_PERSISTENT_AVAILABLE, ctypes.byref(persistent)))
+    result["config"]["decode_path"] = ("one cooperative launch per token" if persistent.value
+                                       else "router, gate/up and down+combine launches per layer")
     lib.hoard_moe_destroy(h)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds)

@@ -57,8 +57,12 @@ class MoeStats(ctypes.Structure):
     ]
 
 
-KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN = 0, 1, 2
-KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "down_combine"}
+KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN, KERNEL_DECODE = 0, 1, 2, 3
+KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "down_combine",
+                KERNEL_DECODE: "decode_persistent"}
+TRACE_PHASES = 12
+OPT_PERSISTENT_DECODE = 1
+OPT_PERSISTENT_AVAILABLE = 2
 
 
 class KernelTimes(ctypes.Structure):
@@ -79,6 +83,11 @@ ABI = {
     "hoard_moe_decode": (_I, [_P, _I, _I, _P, ctypes.c_float, _P]),
     "hoard_moe_profile": (_I, [_P, _I]),
     "hoard_moe_profile_read": (_I, [_P, ctypes.POINTER(KernelTimes)]),
+    "hoard_moe_set_option": (_I, [_P, _I, _I]),
+    "hoard_moe_get_option": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int)]),
+    "hoard_moe_sync_check": (_I, [_P]),
+    "hoard_moe_phase_trace": (_I, [_P, _I]),
+    "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
     "hoard_synth_key": (ctypes.c_uint64, [ctypes.c_uint32] * 5),
     "hoard_synth_fill_blocks": (_I, [_I, ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),
     "hoard_synth_fill_normal": (None, [ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),
@@ -96,6 +105,13 @@ def load_library(path: Path | None = None) -> ctypes.CDLL:
     if _lib is not None and path is None:
         return _lib
     p = Path(path) if path else LIB_PATH
+    try:
+        # torch bundles its own libamdhip64 and finds it by a name that does not
+        # match the one this library links; loading torch first keeps a single
+        # HIP runtime in the process whichever module the caller imports first.
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not p.exists():
         raise HoardError(ERR_STATE, f"{p} is not built: run __graft_entry__.build() "
                                     "(or python -m hoard_amd.build) first")

@@ -63,6 +63,36 @@ struct DownArgs {
 };
 hipError_t launch_down_combine(const DownArgs &a, hipStream_t s);
 
+// Persistent stacked decode (one cooperative launch per token).
+struct DecodeLayer {
+    const float *router;
+    const uint8_t *gate, *up, *down;
+    size_t gstride, ustride, dstride;
+    int gate_type, up_type, down_type;
+};
+struct PersistentArgs {
+    const DecodeLayer *layers;  // device array, indexed by layer
+    int l0, l1;
+    float *x;                   // [n_embd] in/out
+    float eps;
+    int n_embd, E, k, n_ff, renorm;
+    int rows_gu, rows_d;        // n_ff/32 and n_embd/32 rows per workgroup
+    int max_rb_gu, max_rb_d;    // largest gate/up and down row bytes over the layers
+    // exchanged values carry their sequence number: {float bits, seq} per 64-bit word
+    uint64_t *X;                // [2][8][n_embd]  per-XCD copies of x
+    uint64_t *LG;               // [8][E]          per-XCD router logits
+    uint64_t *H;                // [8][n_ff]       per-XCD h
+    uint64_t *Y;                // [2][8][n_embd]  expert outputs by slot
+    unsigned *tickets;          // [8] counters, 128 B apart
+    int *err;
+    unsigned seq0;
+    unsigned long long *trace;  // optional [layer][256 workgroups][kTracePhases] wall-clock stamps
+};
+constexpr int kTracePhases = 12;
+constexpr size_t kPersistentMaxLds = 163840 - 1024;
+size_t persistent_lds_bytes(const PersistentArgs &a);
+hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s);
+
 size_t block_bytes(int type);
 
 }  // namespace hoard

@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -34,7 +35,7 @@ int fail(int code, const char *fmt, ...) {
         if (e_ != hipSuccess) return fail(HOARD_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
 
-constexpr size_t kTailPad = 256;  // kernels read up to 15 bytes past a staged run
+constexpr size_t kTailPad = 4096;  // kernels read whole 1 KB chunks past the end of a staged run
 
 bool quant_type_ok(int t) { return t == HOARD_TYPE_Q4_K || t == HOARD_TYPE_Q6_K; }
 
@@ -77,6 +78,19 @@ struct hoard_moe {
     };
     std::vector<Mark> marks;
     std::vector<hipEvent_t> event_pool;
+    // persistent stacked decode
+    bool persistent_shape_ok = false;  // shape/device admit the one-launch decode
+    int persistent_mode = 1;           // HOARD_OPT_PERSISTENT_DECODE value
+    bool table_dirty = true;
+    hoard::DecodeLayer *d_table = nullptr;
+    uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
+    unsigned *pflags = nullptr;        // tickets
+    int *perr = nullptr;
+    unsigned seq = 1;
+    unsigned long long *ptrace = nullptr;  // phase stamps of the last traced decode
+    size_t trace_layers = 0;
+    bool tracing = false;
+    int trace_last = 0;  // layers covered by the last traced decode
 
     ~hoard_moe() {
         for (auto &m : marks) {
@@ -92,6 +106,14 @@ struct hoard_moe {
         hipFree(wsel);
         hipFree(sgate);
         hipFree(hbuf);
+        hipFree(d_table);
+        hipFree(pX);
+        hipFree(pLG);
+        hipFree(pH);
+        hipFree(pY);
+        hipFree(pflags);
+        hipFree(perr);
+        hipFree(ptrace);
     }
     static void free_layer(Layer &L) {
         hipFree(L.router);
@@ -246,6 +268,115 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
     return HOARD_OK;
 }
 
+// The one-launch decode needs 8 XCDs x 32 CUs (one workgroup per CU), one
+// expert slot per XCD, a router small enough to prefetch into LDS and no shared
+// expert; otherwise hoard_moe_decode launches the per-layer kernels.
+constexpr int kPersistentCus = 256;
+
+int persistent_setup(hoard_moe *h) {
+    const hoard_moe_cfg &c = h->cfg;
+    int cus = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, h->device) != hipSuccess) return fail(HOARD_ERR_HIP, "device properties");
+    cus = prop.multiProcessorCount;
+    const bool arch_ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    h->persistent_shape_ok = arch_ok && cus == kPersistentCus && c.n_embd == 2048 && c.n_used == 8 &&
+                             c.n_expert % 32 == 0 && c.n_expert <= 128 && c.n_ff % 256 == 0 && c.n_ff <= 1024 &&
+                             c.n_ff_shexp == 0 && c.pool_k == 0;
+    if (!h->persistent_shape_ok) return HOARD_OK;
+    int rc = 0;
+    rc = rc ? rc : dev_alloc((void **)&h->d_table, sizeof(hoard::DecodeLayer) * c.n_layer);
+    const size_t nX = (size_t)2 * 8 * c.n_embd, nLG = (size_t)8 * c.n_expert, nH = (size_t)8 * c.n_ff;
+    rc = rc ? rc : dev_alloc((void **)&h->pX, sizeof(uint64_t) * nX);
+    rc = rc ? rc : dev_alloc((void **)&h->pLG, sizeof(uint64_t) * nLG);
+    rc = rc ? rc : dev_alloc((void **)&h->pH, sizeof(uint64_t) * nH);
+    rc = rc ? rc : dev_alloc((void **)&h->pY, sizeof(uint64_t) * nX);
+    const size_t flag_words = (size_t)8 * 32;
+    rc = rc ? rc : dev_alloc((void **)&h->pflags, flag_words * sizeof(unsigned));
+    rc = rc ? rc : dev_alloc((void **)&h->perr, sizeof(int));
+    if (rc) return rc;
+    // sequence tags start at 1, so zeroed words never read as current
+    HIP_TRY(hipMemset(h->pX, 0, sizeof(uint64_t) * nX));
+    HIP_TRY(hipMemset(h->pLG, 0, sizeof(uint64_t) * nLG));
+    HIP_TRY(hipMemset(h->pH, 0, sizeof(uint64_t) * nH));
+    HIP_TRY(hipMemset(h->pY, 0, sizeof(uint64_t) * nX));
+    HIP_TRY(hipMemset(h->pflags, 0, flag_words * sizeof(unsigned)));
+    HIP_TRY(hipMemset(h->perr, 0, sizeof(int)));
+    return HOARD_OK;
+}
+
+// Launches the one-launch decode when it applies; *used reports whether it did.
+int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t s, bool *used) {
+    *used = false;
+    if (!h->persistent_shape_ok || h->persistent_mode == 0 || l0 >= l1) return HOARD_OK;
+    const hoard_moe_cfg &c = h->cfg;
+    int max_rb_gu = 0, max_rb_d = 0;
+    for (int l = l0; l < l1; ++l) {
+        const Layer &L = h->layers[l];
+        const int g = (int)(mat_bytes(L.gate_type, 1, c.n_embd)), u = (int)(mat_bytes(L.up_type, 1, c.n_embd));
+        const int d = (int)(mat_bytes(L.down_type, 1, c.n_ff));
+        max_rb_gu = std::max(max_rb_gu, std::max(g, u));
+        max_rb_d = std::max(max_rb_d, d);
+    }
+    hoard::PersistentArgs a{};
+    a.l0 = l0;
+    a.l1 = l1;
+    a.x = x;
+    a.eps = eps;
+    a.n_embd = c.n_embd;
+    a.E = c.n_expert;
+    a.k = c.n_used;
+    a.n_ff = c.n_ff;
+    a.renorm = c.renorm;
+    a.rows_gu = c.n_ff / 32;
+    a.rows_d = c.n_embd / 32;
+    a.max_rb_gu = max_rb_gu;
+    a.max_rb_d = max_rb_d;
+    if (hoard::persistent_lds_bytes(a) > hoard::kPersistentMaxLds) return HOARD_OK;  // falls back
+    if (h->table_dirty) {
+        std::vector<hoard::DecodeLayer> t(c.n_layer);
+        for (int l = 0; l < c.n_layer; ++l) {
+            const Layer &L = h->layers[l];
+            t[l] = hoard::DecodeLayer{L.router, L.gate, L.up, L.down, L.gstride, L.ustride, L.dstride,
+                                      L.gate_type, L.up_type, L.down_type};
+        }
+        HIP_TRY(hipMemcpy(h->d_table, t.data(), sizeof(hoard::DecodeLayer) * t.size(), hipMemcpyHostToDevice));
+        h->table_dirty = false;
+    }
+    a.layers = h->d_table;
+    a.X = h->pX;
+    a.LG = h->pLG;
+    a.H = h->pH;
+    a.Y = h->pY;
+    a.tickets = h->pflags;
+    a.err = h->perr;
+    a.seq0 = h->seq;
+    if (h->tracing) {
+        if (h->trace_layers < (size_t)c.n_layer) {
+            hipFree(h->ptrace);
+            h->ptrace = nullptr;
+            int rc = dev_alloc((void **)&h->ptrace, sizeof(unsigned long long) * c.n_layer * 256 * hoard::kTracePhases);
+            if (rc) return rc;
+            h->trace_layers = c.n_layer;
+        }
+        a.trace = h->ptrace;
+        h->trace_last = l1 - l0;
+    }
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_DECODE, s);
+        e = hoard::launch_persistent_decode(a, s);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        if (h->persistent_mode == 2) return fail(HOARD_ERR_HIP, "persistent decode launch: %s", hipGetErrorString(e));
+        return HOARD_OK;  // auto mode: fall back to the per-layer kernels
+    }
+    h->seq += 4u * (unsigned)(l1 - l0) + 4u;
+    *used = true;
+    return HOARD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -286,6 +417,7 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     rc = rc ? rc : dev_alloc((void **)&h->hbuf, (size_t)(c.n_used + 1) * h->hstride * sizeof(float));
     if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
+    if (!rc) rc = persistent_setup(h);
     if (rc) {
         delete h;
         return rc;
@@ -350,6 +482,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
         return rc;
     }
     L.loaded = true;
+    h->table_dirty = true;
     return HOARD_OK;
 }
 
@@ -390,12 +523,80 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
     for (int l = layer_begin; l < layer_end; ++l) {
         int rc = check_layer(h, l);
         if (rc) return rc;
+    }
+    bool used = false;
+    int rc0 = persistent_decode(h, layer_begin, layer_end, x_dev, eps, s, &used);
+    if (rc0 || used) return rc0;
+    for (int l = layer_begin; l < layer_end; ++l) {
+        int rc = 0;
         const Layer &L = h->layers[l];
         rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
         if (rc) return rc;
         rc = run_ffn(h, L, h->fx, h->sel, h->wsel, x_dev, x_dev, s);
         if (rc) return rc;
     }
+    return HOARD_OK;
+}
+
+int hoard_moe_set_option(hoard_moe *h, int option, int value) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    switch (option) {
+    case HOARD_OPT_PERSISTENT_DECODE:
+        if (value < 0 || value > 2) return fail(HOARD_ERR_INVALID, "persistent decode mode %d", value);
+        if (value == 2 && !h->persistent_shape_ok)
+            return fail(HOARD_ERR_UNSUPPORTED, "shape or device does not admit the persistent decode");
+        h->persistent_mode = value;
+        return HOARD_OK;
+    default:
+        return fail(HOARD_ERR_INVALID, "unknown option %d", option);
+    }
+}
+
+int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
+    if (!h || !value) return fail(HOARD_ERR_INVALID, "null argument");
+    switch (option) {
+    case HOARD_OPT_PERSISTENT_DECODE:
+        *value = h->persistent_mode;
+        return HOARD_OK;
+    case HOARD_OPT_PERSISTENT_AVAILABLE:
+        *value = h->persistent_shape_ok ? 1 : 0;
+        return HOARD_OK;
+    default:
+        return fail(HOARD_ERR_INVALID, "unknown option %d", option);
+    }
+}
+
+int hoard_moe_sync_check(hoard_moe *h) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipDeviceSynchronize());
+    if (h->perr) {
+        int err = 0;
+        HIP_TRY(hipMemcpy(&err, h->perr, sizeof(int), hipMemcpyDeviceToHost));
+        if (err) {
+            HIP_TRY(hipMemset(h->perr, 0, sizeof(int)));
+            return fail(HOARD_ERR_HIP, "persistent decode: a cross-workgroup wait timed out (output poisoned)");
+        }
+    }
+    return HOARD_OK;
+}
+
+int hoard_moe_phase_trace(hoard_moe *h, int enable) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    h->tracing = enable != 0;
+    return HOARD_OK;
+}
+
+int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, int *n_layers) {
+    if (!h || !out || !n_layers) return fail(HOARD_ERR_INVALID, "null argument");
+    *n_layers = 0;
+    if (!h->ptrace || h->trace_last <= 0) return HOARD_OK;
+    const size_t words = (size_t)h->trace_last * 256 * hoard::kTracePhases;
+    if (max_words < words) return fail(HOARD_ERR_INVALID, "trace needs %zu words", words);
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, h->ptrace, words * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    *n_layers = h->trace_last;
     return HOARD_OK;
 }
 

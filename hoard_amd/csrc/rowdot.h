@@ -1,0 +1,219 @@
+// Row dot products for K-quant rows staged in LDS, computed by an aligned
+// group of 8 lanes per row.  Each lane takes 1/8 of every super-block with
+// 16-byte LDS reads (the 8 lanes of a group read one contiguous 128-byte span,
+// so a wave's reads are bank-conflict free), forms exact integer partial sums
+// with v_dot4_i32_i8, and the group adds them with a 3-step DPP butterfly.
+// The fp32 block terms are then accumulated over super-blocks in block order,
+// exactly as the CPU path does, so the row value is bit-identical to it.
+#pragma once
+
+#include "qblocks.h"
+#include "wave.h"
+
+namespace hoard {
+
+// Q8_K activation block as staged in LDS: quants first so every 16-byte read
+// of them is 16-byte aligned (same fields as ggml's block_q8_K).
+struct Q8L {
+    int32_t qs[64];
+    int16_t bsums[16];
+    float d;
+    int32_t pad[3];
+};
+static_assert(sizeof(Q8L) == 304, "Q8L is 19 x 16 bytes");
+
+// Wave quantisation of 256 floats to Q8_K (ggml quantize_row_q8_K semantics:
+// largest |x| with its sign, first index on ties; iscale = -127/max;
+// q = min(127, nearest_int(iscale*x)); d = 1/iscale; all-zero block -> 0).
+__device__ __forceinline__ void wave_quantize_q8l(const float *x, Q8L *out) {
+    const int lane = threadIdx.x & 63;
+    const float4 v4 = *reinterpret_cast<const float4 *>(x + 4 * lane);
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    float amax = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > amax) {
+            amax = a;
+            idx = 4 * lane + i;
+        }
+    }
+    wave_argmax(amax, idx);
+    if (idx == 0x7fffffff) {
+        out->qs[lane] = 0;
+        if (lane < 16) out->bsums[lane] = 0;
+        if (lane == 0) out->d = 0.0f;
+        return;
+    }
+    const float mval = x[idx];
+    const float iscale = -127.0f / mval;
+    uint32_t packed = 0;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int q = nearest_int(iscale * v[i]);
+        q = q < 127 ? q : 127;
+        s += q;
+        packed |= ((uint32_t)(q & 0xff)) << (8 * i);
+    }
+    out->qs[lane] = (int32_t)packed;
+    s = group4_sum(s);
+    if ((lane & 3) == 0) out->bsums[lane >> 2] = (int16_t)s;
+    if (lane == 0) out->d = 1.0f / iscale;
+}
+
+// One Q4_K row of nb super-blocks (16-byte aligned in LDS) dotted with x.
+// t = lane & 7.  Lane t covers quant bytes [16t, 16t+16) of every block, i.e.
+// 16 elements of sub-block 2*(t/2) (low nibbles) and of 2*(t/2)+1 (high).
+__device__ __forceinline__ float g8_row_q4k(const uint8_t *row, const Q8L *x, int nb, int t) {
+    const int c = t >> 1, h = t & 1;
+    float acc = 0.0f, accm = 0.0f;
+#pragma unroll
+    for (int b = 0; b < nb; ++b) {
+        const uint8_t *blk = row + b * kQ4KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 q = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * t);
+        const Q8L &xb = x[b];
+        const uint4 xl = *reinterpret_cast<const uint4 *>(&xb.qs[16 * c + 4 * h]);
+        const uint4 xh = *reinterpret_cast<const uint4 *>(&xb.qs[16 * c + 8 + 4 * h]);
+        int lo = 0, hi = 0;
+        lo = sdot4(q.x & 0x0f0f0f0fu, xl.x, lo);
+        lo = sdot4(q.y & 0x0f0f0f0fu, xl.y, lo);
+        lo = sdot4(q.z & 0x0f0f0f0fu, xl.z, lo);
+        lo = sdot4(q.w & 0x0f0f0f0fu, xl.w, lo);
+        hi = sdot4((q.x >> 4) & 0x0f0f0f0fu, xh.x, hi);
+        hi = sdot4((q.y >> 4) & 0x0f0f0f0fu, xh.y, hi);
+        hi = sdot4((q.z >> 4) & 0x0f0f0f0fu, xh.z, hi);
+        hi = sdot4((q.w >> 4) & 0x0f0f0f0fu, xh.w, hi);
+        int sc0, m0, sc1, m1;
+        q4k_scale_min(2 * c, hd.y, hd.z, hd.w, sc0, m0);
+        q4k_scale_min(2 * c + 1, hd.y, hd.z, hd.w, sc1, m1);
+        int isum = sc0 * lo + sc1 * hi;
+        int msum = h ? 0
+                     : m0 * ((int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
+                           m1 * ((int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
+        isum = group8_sum(isum);
+        msum = group8_sum(msum);
+        const float d = half_bits_to_float(hd.x & 0xffffu) * xb.d;
+        const float dm = half_bits_to_float(hd.x >> 16) * xb.d;
+        acc = acc + d * (float)isum;
+        accm = accm + dm * (float)msum;
+    }
+    return acc - accm;
+}
+
+// One Q6_K row of nb super-blocks (2-byte aligned in LDS) dotted with x.
+// Lane t covers positions l in [8*(t&3), +8) of half t>>2 for all four
+// 32-element quarters: 32 of the block's 256 elements.
+__device__ __forceinline__ float g8_row_q6k(const uint8_t *row, const Q8L *x, int nb, int t) {
+    const int n = t >> 2, lh = t & 3;
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < nb; ++b) {
+        const uint8_t *blk = row + b * kQ6KBytes;
+        const Q8L &xb = x[b];
+        int s[4] = {0, 0, 0, 0}, z[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t A = lds_u32(blk + 64 * n + 8 * lh + 4 * w);
+            const uint32_t B = lds_u32(blk + 64 * n + 32 + 8 * lh + 4 * w);
+            const uint32_t C = lds_u32(blk + 128 + 32 * n + 8 * lh + 4 * w);
+            const uint32_t q[4] = {
+                (A & 0x0f0f0f0fu) | ((C & 0x03030303u) << 4),
+                (B & 0x0f0f0f0fu) | (((C >> 2) & 0x03030303u) << 4),
+                ((A >> 4) & 0x0f0f0f0fu) | (((C >> 4) & 0x03030303u) << 4),
+                ((B >> 4) & 0x0f0f0f0fu) | (((C >> 6) & 0x03030303u) << 4),
+            };
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t xw = (uint32_t)xb.qs[32 * n + 8 * i + 2 * lh + w];
+                s[i] = sdot4(q[i], xw, s[i]);
+                z[i] = sdot4(0x01010101u, xw, z[i]);
+            }
+        }
+        int isum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int g = 8 * n + 2 * i + (lh >> 1);
+            isum += (int)(int8_t)blk[192 + g] * (s[i] - 32 * z[i]);
+        }
+        isum = group8_sum(isum);
+        const uint32_t dbits = (uint32_t)blk[208] | ((uint32_t)blk[209] << 8);
+        acc = acc + (half_bits_to_float(dbits) * xb.d) * (float)isum;
+    }
+    return acc;
+}
+
+// Fully unrolled variants for a compile-time block count, so every LDS read of
+// the row is issued before the first dot product needs it.
+template <int NB>
+__device__ __forceinline__ float g8_row_q4k_n(const uint8_t *row, const Q8L *x, int t) {
+    return g8_row_q4k(row, x, NB, t);
+}
+template <int NB>
+__device__ __forceinline__ float g8_row_q6k_n(const uint8_t *row, const Q8L *x, int t) {
+    return g8_row_q6k(row, x, NB, t);
+}
+
+__device__ __forceinline__ float g8_row(int type, const uint8_t *row, const Q8L *x, int nb, int t) {
+    if (type == kTypeQ4K) {
+        switch (nb) {
+        case 8: return g8_row_q4k_n<8>(row, x, t);
+        case 4: return g8_row_q4k_n<4>(row, x, t);
+        case 3: return g8_row_q4k_n<3>(row, x, t);
+        case 2: return g8_row_q4k_n<2>(row, x, t);
+        default: return g8_row_q4k(row, x, nb, t);
+        }
+    }
+    switch (nb) {
+    case 8: return g8_row_q6k_n<8>(row, x, t);
+    case 4: return g8_row_q6k_n<4>(row, x, t);
+    case 3: return g8_row_q6k_n<3>(row, x, t);
+    case 2: return g8_row_q6k_n<2>(row, x, t);
+    default: return g8_row_q6k(row, x, nb, t);
+    }
+}
+
+// Q8_K quantisation of 256 values held 4 per lane (lane l: elements 4l..4l+3).
+__device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out) {
+    const int lane = threadIdx.x & 63;
+    float amax = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > amax) {
+            amax = a;
+            idx = 4 * lane + i;
+        }
+    }
+    wave_argmax(amax, idx);
+    if (idx == 0x7fffffff) {
+        out->qs[lane] = 0;
+        if (lane < 16) out->bsums[lane] = 0;
+        if (lane == 0) out->d = 0.0f;
+        return;
+    }
+    // the signed value at idx: lane idx/4, component idx%4
+    const int src = idx >> 2, comp = idx & 3;
+    const float c0 = readlane_f(v[0], src), c1 = readlane_f(v[1], src), c2 = readlane_f(v[2], src),
+                c3 = readlane_f(v[3], src);
+    const float mval = comp == 0 ? c0 : (comp == 1 ? c1 : (comp == 2 ? c2 : c3));
+    const float iscale = -127.0f / mval;
+    uint32_t packed = 0;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int q = nearest_int(iscale * v[i]);
+        q = q < 127 ? q : 127;
+        s += q;
+        packed |= ((uint32_t)(q & 0xff)) << (8 * i);
+    }
+    out->qs[lane] = (int32_t)packed;
+    s = group4_sum(s);
+    if ((lane & 3) == 0) out->bsums[lane >> 2] = (int16_t)s;
+    if (lane == 0) out->d = 1.0f / iscale;
+}
+
+}  // namespace hoard

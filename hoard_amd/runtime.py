@@ -99,6 +99,17 @@ class MoEStage:
         torch.cuda.synchronize()
         return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
 
+    def set_option(self, option: int, value: int) -> None:
+        check(self.lib.hoard_moe_set_option(self.h, option, value))
+
+    def get_option(self, option: int) -> int:
+        v = ctypes.c_int()
+        check(self.lib.hoard_moe_get_option(self.h, option, ctypes.byref(v)))
+        return v.value
+
+    def sync_check(self) -> None:
+        check(self.lib.hoard_moe_sync_check(self.h))
+
     def decode(self, x, layer_begin: int, layer_end: int, eps: float):
         torch = _torch()
         x_d = self.dev(x)

@@ -134,6 +134,7 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
 #define HOARD_KERNEL_ROUTER 0
 #define HOARD_KERNEL_GATEUP 1
 #define HOARD_KERNEL_DOWN 2
+#define HOARD_KERNEL_DECODE 3
 #define HOARD_KERNEL_KINDS 8
 typedef struct hoard_moe_kernel_times {
     uint64_t launches[HOARD_KERNEL_KINDS];
@@ -141,6 +142,27 @@ typedef struct hoard_moe_kernel_times {
 } hoard_moe_kernel_times;
 
 int hoard_moe_profile(hoard_moe *h, int enable);
+
+/* Phase trace of the one-launch decode, the counterpart of the reference's
+   DECODE BREAKDOWN (src/run_moe_stream.cpp:551-554): while enabled, every
+   workgroup stamps the 100 MHz device wall clock at 12 phase boundaries of every
+   layer.  hoard_moe_phase_trace_read synchronises and copies the stamps of the
+   last traced call as [layer][256 workgroups (xcd*32 + rank)][12]. */
+int hoard_moe_phase_trace(hoard_moe *h, int enable);
+int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, int *n_layers);
+
+/* Options.  HOARD_OPT_PERSISTENT_DECODE selects how hoard_moe_decode runs:
+   0 = one launch per kernel per layer, 1 = one cooperative launch per call
+   when the shape and device admit it (default), 2 = require that launch.
+   HOARD_OPT_PERSISTENT_AVAILABLE (read-only) reports whether they admit it. */
+#define HOARD_OPT_PERSISTENT_DECODE 1
+#define HOARD_OPT_PERSISTENT_AVAILABLE 2
+int hoard_moe_set_option(hoard_moe *h, int option, int value);
+int hoard_moe_get_option(hoard_moe *h, int option, int *value);
+
+/* Synchronises the device and reports a cross-workgroup wait that timed out
+   in the one-launch decode (its output rows are then NaN). */
+int hoard_moe_sync_check(hoard_moe *h);
 int hoard_moe_profile_read(hoard_moe *h, hoard_moe_kernel_times *out);
 
 #ifdef __cplusplus

@@ -150,3 +150,50 @@ def test_decode_chain_per_layer(orc):
         assert np.array_equal(whole.view(np.uint32), xs[-1].view(np.uint32))
     finally:
         st.close()
+
+
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE], ids=lambda s: s.name)
+def test_persistent_decode_matches_oracle_and_launch_path(orc, shape):
+    """One-launch stacked decode (router, experts per XCD, combine, rms_norm) against the
+    oracle layer by layer, and against the per-layer launch path on the same input."""
+    import hoard_amd as H
+    nl = 4
+    layers = {l: W.make_layer(shape, 1, l) for l in range(nl)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_PERSISTENT_AVAILABLE) == 1
+        st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+        for tok in range(3):
+            _, x = W.make_hidden(shape, 1, 0, tok)
+            xs = [x]
+            for l in range(nl):
+                print(f"persistent {shape.name} token {tok} layer {l}", flush=True)
+                xs.append(st.decode(xs[-1], l, l + 1, W.RMS_EPS))
+                st.sync_check()
+            for l in range(nl):
+                fx = orc.rms_norm(xs[l], W.RMS_EPS)
+                ref, _, _ = orc.moe_layer(layers[l], fx, xs[l])
+                m = parity.assert_parity(xs[l + 1], ref, f"persistent {shape.name} tok {tok} layer {l}")
+                print("  ", m, flush=True)
+            print(f"persistent {shape.name} token {tok} all layers", flush=True)
+            whole = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.sync_check()
+            assert np.array_equal(whole.view(np.uint32), xs[-1].view(np.uint32))
+            st.set_option(H.OPT_PERSISTENT_DECODE, 0)
+            launched = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+            parity.assert_parity(whole, launched, "persistent vs per-layer launches")
+    finally:
+        st.close()
+
+
+def test_persistent_decode_unavailable_shape_falls_back():
+    import hoard_amd as H
+    shape = W.QWEN3_NEXT  # shared expert + 512 experts: per-layer launches
+    st = _stage(shape, {0: W.make_layer(shape, 0, 0, experts=[])})
+    try:
+        assert st.get_option(H.OPT_PERSISTENT_AVAILABLE) == 0
+        with pytest.raises(H.HoardError):
+            st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+    finally:
+        st.close()
