@@ -81,10 +81,6 @@ __device__ __forceinline__ int issue_lds_copy(uint8_t *dst, const uint8_t *src, 
 
 __host__ __device__ __forceinline__ size_t chunk_region(size_t nbytes) { return ((nbytes + 15 + 1023) >> 10) << 10; }
 
-__device__ __forceinline__ size_t row_bytes_dev(int type, int cols) {
-    return (size_t)(cols / QK) * (type == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
-}
-
 struct Smem {
     // byte offsets into dynamic LDS
     int xs, fxs, w, gate, up, down, q8x, q8h, gu, ys, ps;
@@ -159,6 +155,10 @@ __device__ __forceinline__ bool poll(F ready, int *err) {
     }
 }
 
+// TGU/NB: gate and up type and super-blocks per row (n_embd / 256);
+// TD/NBH: down type and super-blocks per row (n_ff / 256).  Compile-time
+// shapes keep the code of one instantiation well inside the instruction cache.
+template <int TGU, int NB, int TD, int NBH>
 __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sh_rank, sh_fail;
@@ -189,7 +189,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
 
     const int n = a.n_embd, E = a.E, k = a.k;
     const int rw = E / kPerXcd;  // router rows per workgroup
-    const int nb = n / QK, nbh = a.n_ff / QK;
+    constexpr int nb = NB, nbh = NBH;
+    constexpr int kEmbd = NB * QK;
+    static_assert(TGU == kTypeQ4K, "gate/up rows are Q4_K");
+    static_assert(2 * (NBH * QK / kPerXcd) <= kThreads / 8, "one 8-lane group per gate/up row");
     const int R = a.rows_gu, RD = a.rows_d;
     const bool has_expert = (int)xcc < k;
     uint64_t *LGx = a.LG + (size_t)xcc * E;
@@ -268,17 +271,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         if (wave == 0) {
             const int row = lane >> 3, m = lane & 7;
             if (row < rw) {
-                const float *wr = wl + (size_t)row * n + 4 * m;
+                const float *wr = wl + (size_t)row * kEmbd + 4 * m;
                 const float *fr = fxs + 4 * m;
                 float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll 8
-                for (int i = 0; i < n; i += 32) {
-                    const float4 wv = *reinterpret_cast<const float4 *>(wr + i);
-                    const float4 fv = *reinterpret_cast<const float4 *>(fr + i);
-                    a0 = fmaf(wv.x, fv.x, a0);
-                    a1 = fmaf(wv.y, fv.y, a1);
-                    a2 = fmaf(wv.z, fv.z, a2);
-                    a3 = fmaf(wv.w, fv.w, a3);
+                // batches of 8 steps: all 16 LDS reads are issued before the first FMA waits
+                for (int i0 = 0; i0 < kEmbd; i0 += 32 * 8) {
+                    float4 wv[8], fv[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        wv[j] = *reinterpret_cast<const float4 *>(wr + i0 + 32 * j);
+                        fv[j] = *reinterpret_cast<const float4 *>(fr + i0 + 32 * j);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        a0 = fmaf(wv[j].x, fv[j].x, a0);
+                        a1 = fmaf(wv[j].y, fv[j].y, a1);
+                        a2 = fmaf(wv[j].z, fv[j].z, a2);
+                        a3 = fmaf(wv[j].w, fv[j].w, a3);
+                    }
                 }
                 const float r = group8_ggml_fold(a0, a1, a2, a3);
                 if (m == 0) st_l2(LGx + rank * rw + row, tag(r, seq));
@@ -288,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 2);
         stamp(l, 3);
 
-        // -- P2 (wave 0): softmax over all experts, top-k by rank, renorm --
+        // -- P2: softmax over all experts (wave 0), ranks (all threads), renorm (wave 0) --
         if (wave == 0) {
             uint64_t w0 = 0, w1 = 0;
             const bool got = poll(
@@ -314,48 +324,56 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             }
             sum = wave_sum_d(sum);
             const float sc = (float)(1.0 / sum);
-            p0 = p0 * sc;
-            p1 = p1 * sc;
-            if (lane < E) ps[lane] = p0;
-            if (lane + 64 < E) ps[lane + 64] = p1;
+            if (lane < E) ps[lane] = p0 * sc;
+            if (lane + 64 < E) ps[lane + 64] = p1 * sc;
             if (lane < 16) sel_s[lane] = -1;
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are visible to it
-            __builtin_amdgcn_wave_barrier();
-            // rank = experts ahead in (probability desc, index asc) order
-            int r0 = 0, r1 = 0;
-            for (int e4 = 0; e4 < E; e4 += 4) {
-                const float4 pv = *reinterpret_cast<const float4 *>(ps + e4);
-                const float pe[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int e2 = e4 + c;
-                    r0 += (pe[c] > p0 || (pe[c] == p0 && e2 < lane)) ? 1 : 0;
-                    r1 += (pe[c] > p1 || (pe[c] == p1 && e2 < lane + 64)) ? 1 : 0;
+        }
+        lds_barrier();
+        {
+            // rank of expert e = experts ahead of it in (probability desc, index asc)
+            // order; four lanes split the comparisons and add their counts
+            const int e = tid >> 2, q = tid & 3;
+            const int span = E >> 2;
+            int r = 0;
+            float pe = 0.0f;
+            if (e < E) {
+                pe = ps[e];
+                for (int e4 = q * span; e4 < q * span + span; e4 += 4) {
+                    const float4 pv = *reinterpret_cast<const float4 *>(ps + e4);
+                    r += (pv.x > pe || (pv.x == pe && e4 < e)) ? 1 : 0;
+                    r += (pv.y > pe || (pv.y == pe && e4 + 1 < e)) ? 1 : 0;
+                    r += (pv.z > pe || (pv.z == pe && e4 + 2 < e)) ? 1 : 0;
+                    r += (pv.w > pe || (pv.w == pe && e4 + 3 < e)) ? 1 : 0;
                 }
             }
-            if (lane < E && r0 < k) {
-                sel_s[r0] = lane;
-                w_s[r0] = p0;
+            r = group4_sum(r);
+            if (e < E && q == 0 && r < k) {
+                sel_s[r] = e;
+                w_s[r] = pe;
             }
-            if (lane + 64 < E && r1 < k) {
-                sel_s[r1] = lane + 64;
-                w_s[r1] = p1;
+        }
+        lds_barrier();
+        if (wave == 0) {
+            // every lane forms the same left-to-right sum; lane j normalises weight j
+            float ws = 0.0f;
+            for (int j = 0; j < k; ++j) {
+                const int sj = sel_s[j];
+                ws = ws + ((sj < 0 || sj >= E) ? __builtin_nanf("") : w_s[j]);  // NaN logits only
             }
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            __builtin_amdgcn_wave_barrier();
-            if (lane == 0) {
-                float ws = 0.0f;
-                for (int j = 0; j < k; ++j) {
-                    if (sel_s[j] < 0 || sel_s[j] >= E) {  // only reachable with NaN logits
-                        sel_s[j] = 0;
-                        w_s[j] = __builtin_nanf("");
-                    }
-                    ws = ws + w_s[j];
-                }
-                if (a.renorm) {
-                    if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
-                    for (int j = 0; j < k; ++j) w_s[j] = w_s[j] / ws;
-                }
+            int sj = lane < k ? sel_s[lane] : 0;
+            float wj = lane < k ? w_s[lane] : 0.0f;
+            if (sj < 0 || sj >= E) {
+                sj = 0;
+                wj = __builtin_nanf("");
+            }
+            if (a.renorm) {
+                if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+                wj = wj / ws;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads above precede the writes
+            if (lane < k) {
+                sel_s[lane] = sj;
+                w_s[lane] = wj;
             }
         }
         __syncthreads();
@@ -367,8 +385,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
 
         // -- P3: waves 0-3 stream gate/up rows, waves 4-7 stream down rows --
         const int e = has_expert ? sel_s[xcc] : 0;
-        const size_t rbg = row_bytes_dev(L.gate_type, n), rbu = row_bytes_dev(L.up_type, n);
-        const size_t rbd = row_bytes_dev(L.down_type, a.n_ff);
+        constexpr size_t rbg = (size_t)NB * QType<TGU>::bytes, rbu = rbg;
+        constexpr size_t rbd = (size_t)NBH * QType<TD>::bytes;
         const uint8_t *gsrc = L.gate + (size_t)e * L.gstride + (size_t)rank * R * rbg;
         const uint8_t *usrc = L.up + (size_t)e * L.ustride + (size_t)rank * R * rbu;
         const uint8_t *dsrc = L.down + (size_t)e * L.dstride + (size_t)rank * RD * rbd;
@@ -383,21 +401,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 5);
 
         if (has_expert) {
-            // -- P4: gate/up rows on waves 0-3 while the down rows still stream --
-            if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);
+            // -- P4: gate/up rows on every wave while the down rows still stream --
+            if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // the gate/up rows these waves issued
             lds_barrier();
             stamp(l, 6);
-            if (wave < kWaves / 2) {
-                for (int pr = grp; pr < 2 * R; pr += kThreads / 16) {
+            {
+                // one 8-lane group per row (2R <= 64), lane t holding Q8_K(x) block t
+                Q8Reg xr;
+                if (t8 < NB) load_q8reg(q8x[t8], xr);
+                const int pr = grp;
+                if (pr < 2 * R) {
                     const int mat = pr >= R, row = pr - mat * R;
-                    const float v = mat ? g8_row(L.up_type, smem + S.up + ou + row * rbu, q8x, nb, t8)
-                                        : g8_row(L.gate_type, smem + S.gate + og + row * rbg, q8x, nb, t8);
-                    if (t8 == 0) gu[pr] = v;
+                    const uint8_t *rp = mat ? smem + S.up + ou + row * rbu : smem + S.gate + og + row * rbg;
+                    const float v = lpb_row_q4k<NB>(rp, xr, t8);
+                    if (t8 == NB - 1) gu[pr] = v;
                 }
-            } else {
-                __builtin_amdgcn_s_waitcnt(0);  // down rows landed
             }
-            __syncthreads();
+            lds_barrier();
             if (tid < R) {
                 const float g = gu[tid], uu = gu[R + tid];
                 st_l2(Hx + rank * R + tid, tag(g / (1.0f + expf(-g)) * uu, seq + 1u));
@@ -423,17 +443,31 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
                 wave_quantize_q8l_regs(v, &q8h[wave]);
             }
-            __syncthreads();
+            __builtin_amdgcn_s_waitcnt(0);  // down rows landed (issued by waves 4-7)
+            lds_barrier();
             if (sh_fail) {
                 ok = false;
                 break;
             }
             stamp(l, 8);
-            for (int row = grp; row < RD; row += kThreads / 8) {
-                const float y = g8_row(L.down_type, smem + S.down + od + row * rbd, q8h, nbh, t8);
-                if (t8 == 0) ys[row] = y;
+            if constexpr (TD == kTypeQ6K) {
+                // 8 lanes per row; a wave takes rows of one parity so that its rows
+                // share their 4-byte alignment when the row size is 2 mod 4
+                const int row = 16 * (wave >> 1) + 2 * (grp & 7) + (wave & 1);
+                if (row < RD) {
+                    const float y = g8_row_q6k_u<NBH>(smem + S.down + od + row * rbd, q8h, t8);
+                    if (t8 == 0) ys[row] = y;
+                }
+            } else {
+                Q8Reg hr;
+                if (t8 < NBH) load_q8reg(q8h[t8], hr);
+                const int row = grp;
+                if (row < RD) {
+                    const float y = lpb_row_q4k<NBH>(smem + S.down + od + row * rbd, hr, t8);
+                    if (t8 == NBH - 1) ys[row] = y;
+                }
             }
-            __syncthreads();
+            lds_barrier();
             if (wave == 0) {
                 uint64_t *Y = a.Y + ((size_t)cur * kXcds + xcc) * n + rank * RD;
                 for (int i = lane; i < RD; i += 64) st_dev64(Y + i, tag(ys[i], seq + 2u));
@@ -493,19 +527,46 @@ size_t persistent_lds_bytes(const PersistentArgs &a) {
     return total;
 }
 
+// The shapes with an instantiated kernel: {gate/up type, n_embd, down type, n_ff}.
+#define HOARD_PERSISTENT_SHAPES(X)      \
+    X(kTypeQ4K, 2048, kTypeQ6K, 768)    \
+    X(kTypeQ4K, 2048, kTypeQ4K, 1024)   \
+    X(kTypeQ4K, 2048, kTypeQ6K, 512)    \
+    X(kTypeQ4K, 2048, kTypeQ6K, 1024)
+
+using KernelFn = void (*)(PersistentArgs);
+
+static KernelFn persistent_kernel(int gu_type, int n_embd, int d_type, int n_ff) {
+#define HOARD_PICK(TG, N, TD, F) \
+    if (gu_type == TG && n_embd == N && d_type == TD && n_ff == F) return decode_kernel<TG, N / QK, TD, F / QK>;
+    HOARD_PERSISTENT_SHAPES(HOARD_PICK)
+#undef HOARD_PICK
+    return nullptr;
+}
+
+bool persistent_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff) {
+    return persistent_kernel(gu_type, n_embd, d_type, n_ff) != nullptr;
+}
+
 hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s) {
+    const KernelFn fn = persistent_kernel(a.gu_type, a.n_embd, a.d_type, a.n_ff);
+    if (!fn) return hipErrorInvalidConfiguration;
     const size_t lds = persistent_lds_bytes(a);
     if (lds > kPersistentMaxLds) return hipErrorInvalidConfiguration;
-    static int attr_bytes = -1;
-    if (attr_bytes != (int)lds) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    static struct {
+        KernelFn fn;
+        size_t lds;
+    } set_attr[8] = {};  // dynamic-LDS limit already applied per instantiation
+    int slot = 0;
+    while (slot < 8 && set_attr[slot].fn && set_attr[slot].fn != fn) ++slot;
+    if (slot == 8 || set_attr[slot].fn != fn || set_attr[slot].lds != lds) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        attr_bytes = (int)lds;
+        if (slot < 8) set_attr[slot] = {fn, lds};
     }
     PersistentArgs args = a;
     void *params[] = {&args};
-    return hipLaunchCooperativeKernel((const void *)decode_kernel, dim3(kXcds * kPerXcd), dim3(kThreads), params,
-                                      (unsigned)lds, s);
+    return hipLaunchCooperativeKernel((const void *)fn, dim3(kXcds * kPerXcd), dim3(kThreads), params, (unsigned)lds, s);
 }
 
 }  // namespace hoard

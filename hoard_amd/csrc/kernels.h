@@ -78,6 +78,7 @@ struct PersistentArgs {
     int n_embd, E, k, n_ff, renorm;
     int rows_gu, rows_d;        // n_ff/32 and n_embd/32 rows per workgroup
     int max_rb_gu, max_rb_d;    // largest gate/up and down row bytes over the layers
+    int gu_type, d_type;        // gate/up and down types, the same in every layer of [l0, l1)
     // exchanged values carry their sequence number: {float bits, seq} per 64-bit word
     uint64_t *X;                // [2][8][n_embd]  per-XCD copies of x
     uint64_t *LG;               // [8][E]          per-XCD router logits
@@ -92,6 +93,7 @@ constexpr int kTracePhases = 12;
 constexpr size_t kPersistentMaxLds = 163840 - 1024;
 size_t persistent_lds_bytes(const PersistentArgs &a);
 hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s);
+bool persistent_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
 
 size_t block_bytes(int type);
 

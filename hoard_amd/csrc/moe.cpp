@@ -310,14 +310,26 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     *used = false;
     if (!h->persistent_shape_ok || h->persistent_mode == 0 || l0 >= l1) return HOARD_OK;
     const hoard_moe_cfg &c = h->cfg;
-    int max_rb_gu = 0, max_rb_d = 0;
+    // Forced mode reports why the range cannot take the one-launch path; auto
+    // mode falls back to the per-layer kernels.
+    auto skip = [&](const char *why) {
+        return h->persistent_mode == 2 ? fail(HOARD_ERR_UNSUPPORTED, "persistent decode: %s", why) : HOARD_OK;
+    };
+    // one kernel instantiation serves the whole range: uniform types, gate = up
+    const int gu_type = h->layers[l0].gate_type, d_type = h->layers[l0].down_type;
     for (int l = l0; l < l1; ++l) {
         const Layer &L = h->layers[l];
-        const int g = (int)(mat_bytes(L.gate_type, 1, c.n_embd)), u = (int)(mat_bytes(L.up_type, 1, c.n_embd));
-        const int d = (int)(mat_bytes(L.down_type, 1, c.n_ff));
-        max_rb_gu = std::max(max_rb_gu, std::max(g, u));
-        max_rb_d = std::max(max_rb_d, d);
+        if (L.gate_type != gu_type || L.up_type != gu_type || L.down_type != d_type)
+            return skip("layer types differ within the range");
+        // rows are staged into LDS at their source offset modulo 16; the kernel's
+        // row reads need that offset to be 0
+        const uintptr_t al = reinterpret_cast<uintptr_t>(L.gate) | reinterpret_cast<uintptr_t>(L.up) |
+                             reinterpret_cast<uintptr_t>(L.down) | L.gstride | L.ustride | L.dstride;
+        if (al & 15) return skip("expert tensors are not 16-byte aligned");
     }
+    if (!hoard::persistent_shape_compiled(gu_type, c.n_embd, d_type, c.n_ff))
+        return skip("no kernel instantiated for these types and sizes");
+    const int max_rb_gu = (int)mat_bytes(gu_type, 1, c.n_embd), max_rb_d = (int)mat_bytes(d_type, 1, c.n_ff);
     hoard::PersistentArgs a{};
     a.l0 = l0;
     a.l1 = l1;
@@ -332,7 +344,9 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     a.rows_d = c.n_embd / 32;
     a.max_rb_gu = max_rb_gu;
     a.max_rb_d = max_rb_d;
-    if (hoard::persistent_lds_bytes(a) > hoard::kPersistentMaxLds) return HOARD_OK;  // falls back
+    a.gu_type = gu_type;
+    a.d_type = d_type;
+    if (hoard::persistent_lds_bytes(a) > hoard::kPersistentMaxLds) return skip("LDS footprint too large");
     if (h->table_dirty) {
         std::vector<hoard::DecodeLayer> t(c.n_layer);
         for (int l = 0; l < c.n_layer; ++l) {

@@ -145,34 +145,188 @@ __device__ __forceinline__ float g8_row_q6k(const uint8_t *row, const Q8L *x, in
     return acc;
 }
 
-// Fully unrolled variants for a compile-time block count, so every LDS read of
-// the row is issued before the first dot product needs it.
-template <int NB>
-__device__ __forceinline__ float g8_row_q4k_n(const uint8_t *row, const Q8L *x, int t) {
-    return g8_row_q4k(row, x, NB, t);
-}
-template <int NB>
-__device__ __forceinline__ float g8_row_q6k_n(const uint8_t *row, const Q8L *x, int t) {
-    return g8_row_q6k(row, x, NB, t);
+// Q6_K rows whose start has the same 4-byte alignment (0 or 2) in every lane
+// of the wave: 210-byte blocks alternate between the two, so each block takes
+// one scalar branch to a body with a compile-time shift instead of per-lane
+// alignment tests.
+template <int SH>
+__device__ __forceinline__ uint32_t lds_u32_c(const uint8_t *p) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - SH);
+    if constexpr (SH == 0)
+        return w[0];
+    else
+        return __builtin_amdgcn_alignbyte(w[1], w[0], SH);
 }
 
-__device__ __forceinline__ float g8_row(int type, const uint8_t *row, const Q8L *x, int nb, int t) {
-    if (type == kTypeQ4K) {
-        switch (nb) {
-        case 8: return g8_row_q4k_n<8>(row, x, t);
-        case 4: return g8_row_q4k_n<4>(row, x, t);
-        case 3: return g8_row_q4k_n<3>(row, x, t);
-        case 2: return g8_row_q4k_n<2>(row, x, t);
-        default: return g8_row_q4k(row, x, nb, t);
+template <int SH>
+__device__ __forceinline__ int q6k_block_isum_g8(const uint8_t *blk, const Q8L &xb, int n, int lh) {
+    int s[4] = {0, 0, 0, 0}, z[4] = {0, 0, 0, 0};
+    uint32_t A[2], B[2], C[2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        A[w] = lds_u32_c<SH>(blk + 64 * n + 8 * lh + 4 * w);
+        B[w] = lds_u32_c<SH>(blk + 64 * n + 32 + 8 * lh + 4 * w);
+        C[w] = lds_u32_c<SH>(blk + 128 + 32 * n + 8 * lh + 4 * w);
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t q[4] = {
+            (A[w] & 0x0f0f0f0fu) | ((C[w] & 0x03030303u) << 4),
+            (B[w] & 0x0f0f0f0fu) | (((C[w] >> 2) & 0x03030303u) << 4),
+            ((A[w] >> 4) & 0x0f0f0f0fu) | (((C[w] >> 4) & 0x03030303u) << 4),
+            ((B[w] >> 4) & 0x0f0f0f0fu) | (((C[w] >> 6) & 0x03030303u) << 4),
+        };
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t xw = (uint32_t)xb.qs[32 * n + 8 * i + 2 * lh + w];
+            s[i] = sdot4(q[i], xw, s[i]);
+            z[i] = sdot4(0x01010101u, xw, z[i]);
         }
     }
-    switch (nb) {
-    case 8: return g8_row_q6k_n<8>(row, x, t);
-    case 4: return g8_row_q6k_n<4>(row, x, t);
-    case 3: return g8_row_q6k_n<3>(row, x, t);
-    case 2: return g8_row_q6k_n<2>(row, x, t);
-    default: return g8_row_q6k(row, x, nb, t);
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = 8 * n + 2 * i + (lh >> 1);
+        isum += (int)(int8_t)blk[192 + g] * (s[i] - 32 * z[i]);
     }
+    return isum;
+}
+
+template <int NB>
+__device__ __forceinline__ float g8_row_q6k_u(const uint8_t *row, const Q8L *x, int t) {
+    const int n = t >> 2, lh = t & 3;
+    const uint32_t al = (uint32_t)__builtin_amdgcn_readfirstlane((int)(reinterpret_cast<uintptr_t>(row) & 3u));
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint8_t *blk = row + b * kQ6KBytes;
+        int isum;
+        if (((al + 2u * b) & 3u) == 0u)
+            isum = q6k_block_isum_g8<0>(blk, x[b], n, lh);
+        else
+            isum = q6k_block_isum_g8<2>(blk, x[b], n, lh);
+        isum = group8_sum(isum);
+        const uint32_t dbits = (uint32_t)blk[208] | ((uint32_t)blk[209] << 8);
+        acc = acc + (half_bits_to_float(dbits) * x[b].d) * (float)isum;
+    }
+    return acc;
+}
+
+// Row dot for a compile-time type and block count: the block loop unrolls
+// fully, so every LDS read of the row is issued before the first dot product
+// needs it, and a kernel instantiates only the bodies it uses.
+template <int TYPE, int NB>
+__device__ __forceinline__ float g8_row(const uint8_t *row, const Q8L *x, int t) {
+    static_assert(TYPE == kTypeQ4K || TYPE == kTypeQ6K, "Q4_K or Q6_K rows");
+    if constexpr (TYPE == kTypeQ4K)
+        return g8_row_q4k(row, x, NB, t);
+    else
+        return g8_row_q6k(row, x, NB, t);
+}
+
+// ---------------------------------------------------------------------------
+// One lane per super-block.  A row of NB <= G super-blocks is handled by an
+// aligned group of G lanes, lane t taking block t whole: its integer sums are
+// complete in-lane, and the fp32 block terms are then added in block order by
+// a chain through the group's lanes (row_shr:1 makes lane i read lane i - 1).
+// The activation block a lane needs is the same for every row, so it is held
+// in registers across rows.
+
+// Q8_K activation block held in registers by the lane that owns it.
+struct Q8Reg {
+    uint4 q[16];  // 256 int8 quants
+    int bs[8];    // bsums[2s] + bsums[2s+1]: sum of the 32 quants of sub-block s
+    float d;
+};
+
+__device__ __forceinline__ void load_q8reg(const Q8L &x, Q8Reg &r) {
+    const uint4 *q = reinterpret_cast<const uint4 *>(x.qs);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r.q[i] = q[i];
+    const uint4 b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
+    const uint4 b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
+    const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) r.bs[s] = (int)(int16_t)(w[s] & 0xffffu) + (int)(int16_t)(w[s] >> 16);
+    r.d = x.d;
+}
+
+constexpr int kDppRowShr1 = 0x111;  // lane i reads lane i - 1 of its row
+
+// Ordered fp32 sum over lanes 0..nb-1 of each aligned group: lane t holds v.
+// Returns 0 + v0 + v1 + ... (left to right) in lane nb-1 of the group.
+template <int NB>
+__device__ __forceinline__ float group_chain_sum(float v, int t) {
+    float acc = 0.0f + v;
+#pragma unroll
+    for (int s = 1; s < NB; ++s) {
+        const float prev = dpp_f<kDppRowShr1>(acc);
+        acc = t == s ? prev + v : acc;
+    }
+    return acc;
+}
+
+// Q4_K super-block (16-byte aligned) against the lane's activation block:
+// the integer sums isum = sum_s sc_s * dot_s and msum = sum_s m_s * bsum_s.
+__device__ __forceinline__ void q4k_block_sums(const uint8_t *blk, const Q8Reg &x, uint32_t &dm_bits, int &isum,
+                                               int &msum) {
+    const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+    uint4 q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * i);
+    dm_bits = hd.x;
+    const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+    auto byte = [&](int i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+    isum = 0;
+    msum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // 64-element chunk j: sub-blocks 2j (low nibbles) and 2j+1 (high)
+        const uint32_t qw[8] = {q[2 * j].x, q[2 * j].y, q[2 * j].z, q[2 * j].w,
+                                q[2 * j + 1].x, q[2 * j + 1].y, q[2 * j + 1].z, q[2 * j + 1].w};
+        const uint32_t xl[8] = {x.q[4 * j].x, x.q[4 * j].y, x.q[4 * j].z, x.q[4 * j].w,
+                                x.q[4 * j + 1].x, x.q[4 * j + 1].y, x.q[4 * j + 1].z, x.q[4 * j + 1].w};
+        const uint32_t xh[8] = {x.q[4 * j + 2].x, x.q[4 * j + 2].y, x.q[4 * j + 2].z, x.q[4 * j + 2].w,
+                                x.q[4 * j + 3].x, x.q[4 * j + 3].y, x.q[4 * j + 3].z, x.q[4 * j + 3].w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            lo = sdot4(qw[k] & 0x0f0f0f0fu, xl[k], lo);
+            hi = sdot4((qw[k] >> 4) & 0x0f0f0f0fu, xh[k], hi);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int s = 2 * j + h;
+            int sc, mn;
+            if (s < 4) {
+                sc = byte(s) & 63;
+                mn = byte(s + 4) & 63;
+            } else {
+                sc = (byte(s + 4) & 0x0f) | ((byte(s - 4) >> 6) << 4);
+                mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+            }
+            isum += sc * (h ? hi : lo);
+            msum += mn * x.bs[s];
+        }
+    }
+}
+
+// One Q4_K row of NB super-blocks (16-byte aligned) dotted with the
+// activation; valid in lane NB-1 of the lane's group.
+template <int NB>
+__device__ __forceinline__ float lpb_row_q4k(const uint8_t *row, const Q8Reg &x, int t) {
+    float p = 0.0f, pm = 0.0f;
+    if (t < NB) {
+        uint32_t dm;
+        int isum, msum;
+        q4k_block_sums(row + t * kQ4KBytes, x, dm, isum, msum);
+        const float d = half_bits_to_float(dm & 0xffffu) * x.d;
+        const float dmin = half_bits_to_float(dm >> 16) * x.d;
+        p = d * (float)isum;
+        pm = dmin * (float)msum;
+    }
+    const float acc = group_chain_sum<NB>(p, t);
+    const float accm = group_chain_sum<NB>(pm, t);
+    return acc - accm;
 }
 
 // Q8_K quantisation of 256 values held 4 per lane (lane l: elements 4l..4l+3).
