@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--phases", action="store_true", help="trace one-launch decode phases of one token")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 5 device-to-device copies of BYTES (HBM counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -99,6 +101,32 @@ def phase_breakdown(lib, h, step, H):
     return out
 
 
+def copy_probe(nbytes: int):
+    """A plain copy kernel of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters of the decode kernel to bytes."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "copies": 5}), flush=True)
+
+
+def measured_traffic(shape, kernel: str, n_layer: int):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-probe factor), or
+    None when no summary covers this kernel and workload."""
+    f = ROOT / "profiles" / f"traffic_{kernel}_{shape.name}.json"
+    if not f.exists():
+        return None
+    t = json.loads(f.read_text())
+    if t.get("kernel") != kernel or t.get("layers") != n_layer:
+        return None
+    return int(t["hbm_bytes_per_launch"])
+
+
 def cpu_baseline(shape, seed: int, budget_s: float):
     """The oracle (C restatement of ggml-CPU's algorithm) on host cores."""
     import oracle
@@ -134,6 +162,10 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     import hoard_amd as H
     from hoard_amd import workloads as W
@@ -228,7 +260,9 @@ def main():
         "layer_bytes": layer_bytes,
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbps"], "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(dk["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(dk["gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(shape, dom, n_layer),
+                     "algorithmic_bytes": dk["bytes"]},
     }
     if args.phases:
         ph = phase_breakdown(lib, h, lambda: step(warm), H)
