@@ -63,6 +63,7 @@ KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "
 TRACE_PHASES = 12
 OPT_PERSISTENT_DECODE = 1
 OPT_PERSISTENT_AVAILABLE = 2
+OPT_POOL_NAIVE = 3
 
 
 class KernelTimes(ctypes.Structure):
@@ -88,6 +89,12 @@ ABI = {
     "hoard_moe_sync_check": (_I, [_P]),
     "hoard_moe_phase_trace": (_I, [_P, _I]),
     "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
+    "hoard_moe_pool_ensure": (_I, [_P, _I, _P, _P, _P, _P, _P]),
+    "hoard_moe_get_stats": (_I, [_P, ctypes.POINTER(MoeStats)]),
+    "hoard_moe_reset_stats": (_I, [_P]),
+    "hoard_slot_lru_create": (_I, [_I, _I, _I, _I, ctypes.POINTER(_P)]),
+    "hoard_slot_lru_access": (_I, [_P, _I, _P, _I, _P, _P]),
+    "hoard_slot_lru_destroy": (None, [_P]),
     "hoard_synth_key": (ctypes.c_uint64, [ctypes.c_uint32] * 5),
     "hoard_synth_fill_blocks": (_I, [_I, ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),
     "hoard_synth_fill_normal": (None, [ctypes.c_uint64, _P, ctypes.c_size_t, ctypes.c_float]),

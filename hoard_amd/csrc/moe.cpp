@@ -14,6 +14,7 @@
 
 #include "hoard_moe.h"
 #include "kernels.h"
+#include "slot_lru.h"
 
 namespace {
 
@@ -47,11 +48,25 @@ struct Layer {
     bool loaded = false;
     float *router = nullptr;
     int gate_type = 0, up_type = 0, down_type = 0;
-    size_t gstride = 0, ustride = 0, dstride = 0;
+    size_t gstride = 0, ustride = 0, dstride = 0;  // bytes between consecutive experts (or slots)
+    size_t gbytes = 0, ubytes = 0, dbytes = 0;     // bytes of one expert's matrix
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int sh_gate_type = 0, sh_up_type = 0, sh_down_type = 0;
     uint8_t *sh_gate = nullptr, *sh_up = nullptr, *sh_down = nullptr;
     float *sh_gate_inp = nullptr;
+    // pool_k > 0: gate/up/down above point into K slots of one record
+    // [gate | up | down] each (stride = record size), so a miss is one copy from
+    // the pinned host masters, laid out the same way per expert (the
+    // reference's RAM tier, here never evicted)
+    uint8_t *slots = nullptr;
+    uint8_t *host_experts = nullptr;
+    hipEvent_t copied = nullptr;    // last uploads into this layer's slots (copy stream)
+    hipEvent_t copied2 = nullptr;   // the same on the second copy stream
+    hipEvent_t last_use = nullptr;  // last FFN reading this layer's slots (compute stream)
+    bool used = false;              // last_use has been recorded
+    int32_t *slot_stage = nullptr;  // pinned staging of the slot ids handed to the device
+    hipEvent_t staged = nullptr;    // the staging copy has been consumed
+    bool stage_pending = false;
 };
 
 }  // namespace
@@ -88,6 +103,12 @@ struct hoard_moe {
     int *perr = nullptr;
     unsigned seq = 1;
     unsigned long long *ptrace = nullptr;  // phase stamps of the last traced decode
+    // expert slot pool (pool_k > 0)
+    hoard::SlotLru lru;
+    bool pool_naive = false;
+    int32_t *pin_sel = nullptr;     // pinned [n_used]: device-routed ids read back on the on-demand path
+    int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
+    hipStream_t copy2 = nullptr;    // second upload stream: two copies in flight hide per-copy set-up
     size_t trace_layers = 0;
     bool tracing = false;
     int trace_last = 0;  // layers covered by the last traced decode
@@ -114,8 +135,21 @@ struct hoard_moe {
         hipFree(pflags);
         hipFree(perr);
         hipFree(ptrace);
+        hipHostFree(pin_sel);
+        hipFree(slot_ids);
+        if (copy2) hipStreamDestroy(copy2);
     }
     static void free_layer(Layer &L) {
+        if (L.copied) hipEventDestroy(L.copied);
+        if (L.copied2) hipEventDestroy(L.copied2);
+        if (L.last_use) hipEventDestroy(L.last_use);
+        if (L.staged) hipEventDestroy(L.staged);
+        hipHostFree(L.host_experts);
+        hipHostFree(L.slot_stage);
+        if (L.slots) {
+            hipFree(L.slots);
+            L.gate = L.up = L.down = nullptr;  // views into slots
+        }
         hipFree(L.router);
         hipFree(L.gate);
         hipFree(L.up);
@@ -224,7 +258,7 @@ int run_route(hoard_moe *h, const Layer &L, const float *xin, int is_residual, f
 int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, const float *w,
             const float *res, float *out, hipStream_t s) {
     const hoard_moe_cfg &c = h->cfg;
-    const int n_ids = c.n_expert;
+    const int n_ids = c.pool_k > 0 ? c.pool_k : c.n_expert;  // ids are slots in pool mode
     const bool sh = c.n_ff_shexp > 0;
     hoard::GateUpArgs g{};
     g.fx = fx;
@@ -266,6 +300,75 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
     }
     if (e != hipSuccess) return fail(HOARD_ERR_HIP, "down/combine launch: %s", hipGetErrorString(e));
     return HOARD_OK;
+}
+
+// Slot pool step for one layer: LRU bookkeeping on the host, uploads of the
+// missed experts on copy_stream (after the previous FFN that read this layer's
+// slots), and `stream` made to wait for them.  slot_dev (optional) receives
+// the slot ids through a pinned staging copy on `stream`.
+int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host, int32_t *slot_dev,
+                hipStream_t s, hipStream_t cs) {
+    const hoard_moe_cfg &c = h->cfg;
+    Layer &L = h->layers[layer];
+    const int n = c.n_used;
+    for (int j = 0; j < n; ++j)
+        if (sel[j] < 0 || sel[j] >= c.n_expert) return fail(HOARD_ERR_INVALID, "expert id %d out of range", sel[j]);
+    int32_t slots[16];
+    uint8_t miss[16];
+    h->lru.access(layer, sel, n, h->pool_naive, slots, miss);
+    int n_miss = 0;
+    for (int j = 0; j < n; ++j) n_miss += miss[j];
+    // misses alternate between the caller's copy stream and a second one; both
+    // first wait until the last FFN reading this layer's slots is done
+    hipStream_t up[2] = {cs, h->copy2};
+    const int n_up = n_miss > 1 ? 2 : 1;
+    if (n_miss && L.used)
+        for (int i = 0; i < n_up; ++i) HIP_TRY(hipStreamWaitEvent(up[i], L.last_use, 0));
+    int m = 0;
+    for (int j = 0; j < n; ++j) {
+        h->stats.reqs += 1;
+        if (!miss[j]) {
+            h->stats.hits += 1;
+            continue;
+        }
+        const size_t e = (size_t)sel[j], sl = (size_t)slots[j], rec = L.gstride;  // one [g|u|d] record
+        HIP_TRY(hipMemcpyAsync(L.slots + sl * rec, L.host_experts + e * rec, rec, hipMemcpyHostToDevice, up[m++ % n_up]));
+        h->stats.misses += 1;
+        h->stats.bytes_h2d += rec;
+    }
+    if (n_miss) {
+        hipEvent_t ev[2] = {L.copied, L.copied2};
+        for (int i = 0; i < n_up; ++i) {
+            HIP_TRY(hipEventRecord(ev[i], up[i]));
+            HIP_TRY(hipStreamWaitEvent(s, ev[i], 0));
+        }
+    }
+    if (slot_host) std::memcpy(slot_host, slots, sizeof(int32_t) * n);
+    if (slot_dev) {
+        if (L.stage_pending) HIP_TRY(hipEventSynchronize(L.staged));  // previous ids consumed
+        std::memcpy(L.slot_stage, slots, sizeof(int32_t) * n);
+        HIP_TRY(hipMemcpyAsync(slot_dev, L.slot_stage, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+        HIP_TRY(hipEventRecord(L.staged, s));
+        L.stage_pending = true;
+    }
+    return HOARD_OK;
+}
+
+// Marks the end of an FFN that read `layer`'s slots (pool mode).
+int pool_mark_use(hoard_moe *h, int layer, hipStream_t s) {
+    if (h->cfg.pool_k == 0) return HOARD_OK;
+    Layer &L = h->layers[layer];
+    HIP_TRY(hipEventRecord(L.last_use, s));
+    L.used = true;
+    return HOARD_OK;
+}
+
+// On-demand pool step after a device-side route: the selection is read back
+// (the reference's D2H of sel, :367), then the slots are ensured.
+int pool_after_route(hoard_moe *h, int layer, const int32_t *sel_dev, int32_t *slot_dev, hipStream_t s) {
+    HIP_TRY(hipMemcpyAsync(h->pin_sel, sel_dev, sizeof(int32_t) * h->cfg.n_used, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return pool_ensure(h, layer, h->pin_sel, nullptr, slot_dev, s, s);
 }
 
 // The one-launch decode needs 8 XCDs x 32 CUs (one workgroup per CU), one
@@ -410,7 +513,8 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
         return fail(HOARD_ERR_INVALID, "n_used %d outside 1..min(16, n_expert)", c.n_used);
     if (c.n_layer <= 0) return fail(HOARD_ERR_INVALID, "n_layer %d", c.n_layer);
     if (c.max_tokens <= 0) return fail(HOARD_ERR_INVALID, "max_tokens %d", c.max_tokens);
-    if (c.pool_k != 0) return fail(HOARD_ERR_UNSUPPORTED, "pool_k > 0 not available in this build");
+    if (c.pool_k < 0 || (c.pool_k > 0 && (c.pool_k < c.n_used || c.pool_k > c.n_expert)))
+        return fail(HOARD_ERR_INVALID, "pool_k %d outside n_used..n_expert (or 0 for all resident)", c.pool_k);
     hoard_moe *h = new (std::nothrow) hoard_moe();
     if (!h) return fail(HOARD_ERR_OOM, "handle");
     h->cfg = c;
@@ -431,6 +535,14 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     rc = rc ? rc : dev_alloc((void **)&h->hbuf, (size_t)(c.n_used + 1) * h->hstride * sizeof(float));
     if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
+    if (!rc && c.pool_k > 0) {
+        h->lru.reset(c.n_layer, c.n_expert, c.pool_k);
+        if (hipHostMalloc((void **)&h->pin_sel, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
+            rc = fail(HOARD_ERR_OOM, "pinned selection buffer");
+        rc = rc ? rc : dev_alloc((void **)&h->slot_ids, sizeof(int32_t) * c.n_used);
+        if (!rc && hipStreamCreateWithFlags(&h->copy2, hipStreamNonBlocking) != hipSuccess)
+            rc = fail(HOARD_ERR_HIP, "second copy stream");
+    }
     if (!rc) rc = persistent_setup(h);
     if (rc) {
         delete h;
@@ -469,16 +581,50 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
     L.gate_type = w->gate_type;
     L.up_type = w->up_type;
     L.down_type = w->down_type;
-    L.gstride = mat_bytes(L.gate_type, c.n_ff, c.n_embd);
-    L.ustride = mat_bytes(L.up_type, c.n_ff, c.n_embd);
-    L.dstride = mat_bytes(L.down_type, c.n_embd, c.n_ff);
+    L.gbytes = L.gstride = mat_bytes(L.gate_type, c.n_ff, c.n_embd);
+    L.ubytes = L.ustride = mat_bytes(L.up_type, c.n_ff, c.n_embd);
+    L.dbytes = L.dstride = mat_bytes(L.down_type, c.n_embd, c.n_ff);
     const size_t E = (size_t)c.n_expert;
     int rc = 0;
     const size_t rb = (size_t)c.n_expert * c.n_embd * sizeof(float);
     rc = rc ? rc : upload((void **)&L.router, w->router, rb, rb);
-    rc = rc ? rc : upload((void **)&L.gate, w->gate, E * L.gstride, E * L.gstride + kTailPad);
-    rc = rc ? rc : upload((void **)&L.up, w->up, E * L.ustride, E * L.ustride + kTailPad);
-    rc = rc ? rc : upload((void **)&L.down, w->down, E * L.dstride, E * L.dstride + kTailPad);
+    if (c.pool_k == 0) {
+        rc = rc ? rc : upload((void **)&L.gate, w->gate, E * L.gstride, E * L.gstride + kTailPad);
+        rc = rc ? rc : upload((void **)&L.up, w->up, E * L.ustride, E * L.ustride + kTailPad);
+        rc = rc ? rc : upload((void **)&L.down, w->down, E * L.dstride, E * L.dstride + kTailPad);
+    } else {
+        const size_t K = (size_t)c.pool_k, rec = L.gbytes + L.ubytes + L.dbytes;
+        rc = rc ? rc : dev_alloc((void **)&L.slots, K * rec + kTailPad);
+        if (!rc) {
+            L.gate = L.slots;
+            L.up = L.slots + L.gbytes;
+            L.down = L.slots + L.gbytes + L.ubytes;
+            L.gstride = L.ustride = L.dstride = rec;
+        }
+        if (!rc && hipHostMalloc((void **)&L.host_experts, E * rec, hipHostMallocDefault) != hipSuccess) {
+            L.host_experts = nullptr;
+            (void)hipGetLastError();
+            rc = fail(HOARD_ERR_OOM, "hipHostMalloc(%zu) for the expert masters", E * rec);
+        }
+        if (!rc) {
+            const uint8_t *g = static_cast<const uint8_t *>(w->gate), *u = static_cast<const uint8_t *>(w->up),
+                          *d = static_cast<const uint8_t *>(w->down);
+            for (size_t e = 0; e < E; ++e) {
+                uint8_t *r = L.host_experts + e * rec;
+                std::memcpy(r, g + e * L.gbytes, L.gbytes);
+                std::memcpy(r + L.gbytes, u + e * L.ubytes, L.ubytes);
+                std::memcpy(r + L.gbytes + L.ubytes, d + e * L.dbytes, L.dbytes);
+            }
+        }
+        if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
+            rc = fail(HOARD_ERR_OOM, "pinned slot staging");
+        if (!rc && (hipEventCreateWithFlags(&L.copied, hipEventDisableTiming) != hipSuccess ||
+                    hipEventCreateWithFlags(&L.copied2, hipEventDisableTiming) != hipSuccess ||
+                    hipEventCreateWithFlags(&L.last_use, hipEventDisableTiming) != hipSuccess ||
+                    hipEventCreateWithFlags(&L.staged, hipEventDisableTiming) != hipSuccess))
+            rc = fail(HOARD_ERR_HIP, "pool events");
+        if (!rc) h->lru.reset_layer(layer);  // the slots no longer hold this layer's experts
+    }
     if (sh && !rc) {
         L.sh_gate_type = w->sh_gate_type;
         L.sh_up_type = w->sh_up_type;
@@ -513,7 +659,9 @@ int hoard_moe_ffn_combine(hoard_moe *h, int layer, const float *fx_dev, const in
     int rc = check_layer(h, layer);
     if (rc) return rc;
     if (!fx_dev || !ids_dev || !w_dev || !res_dev || !out_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
-    return run_ffn(h, h->layers[layer], fx_dev, ids_dev, w_dev, res_dev, out_dev, (hipStream_t)stream);
+    rc = run_ffn(h, h->layers[layer], fx_dev, ids_dev, w_dev, res_dev, out_dev, (hipStream_t)stream);
+    if (rc) return rc;
+    return pool_mark_use(h, layer, (hipStream_t)stream);
 }
 
 int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *res_dev, float *out_dev,
@@ -524,9 +672,18 @@ int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *r
     int32_t *sel = sel_dev ? sel_dev : h->sel;
     float *w = w_dev ? w_dev : h->wsel;
     const Layer &L = h->layers[layer];
-    rc = run_route(h, L, fx_dev, 0, 0.0f, sel, w, (hipStream_t)stream);
+    hipStream_t s = (hipStream_t)stream;
+    rc = run_route(h, L, fx_dev, 0, 0.0f, sel, w, s);
     if (rc) return rc;
-    return run_ffn(h, L, fx_dev, sel, w, res_dev, out_dev, (hipStream_t)stream);
+    const int32_t *ids = sel;
+    if (h->cfg.pool_k > 0) {
+        rc = pool_after_route(h, layer, sel, h->slot_ids, s);
+        if (rc) return rc;
+        ids = h->slot_ids;
+    }
+    rc = run_ffn(h, L, fx_dev, ids, w, res_dev, out_dev, s);
+    if (rc) return rc;
+    return pool_mark_use(h, layer, s);
 }
 
 int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps, void *stream) {
@@ -546,9 +703,39 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
         const Layer &L = h->layers[l];
         rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
         if (rc) return rc;
-        rc = run_ffn(h, L, h->fx, h->sel, h->wsel, x_dev, x_dev, s);
+        const int32_t *ids = h->sel;
+        if (h->cfg.pool_k > 0) {
+            rc = pool_after_route(h, l, h->sel, h->slot_ids, s);
+            if (rc) return rc;
+            ids = h->slot_ids;
+        }
+        rc = run_ffn(h, L, h->fx, ids, h->wsel, x_dev, x_dev, s);
+        if (rc) return rc;
+        rc = pool_mark_use(h, l, s);
         if (rc) return rc;
     }
+    return HOARD_OK;
+}
+
+int hoard_moe_pool_ensure(hoard_moe *h, int layer, const int32_t *sel_host, int32_t *slot_host,
+                          int32_t *slot_dev, void *stream, void *copy_stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    if (h->cfg.pool_k == 0) return fail(HOARD_ERR_STATE, "handle has no slot pool (pool_k == 0)");
+    if (!sel_host || (!slot_host && !slot_dev)) return fail(HOARD_ERR_INVALID, "null argument");
+    return pool_ensure(h, layer, sel_host, slot_host, slot_dev, (hipStream_t)stream,
+                       copy_stream ? (hipStream_t)copy_stream : (hipStream_t)stream);
+}
+
+int hoard_moe_get_stats(hoard_moe *h, hoard_moe_stats *out) {
+    if (!h || !out) return fail(HOARD_ERR_INVALID, "null argument");
+    *out = h->stats;
+    return HOARD_OK;
+}
+
+int hoard_moe_reset_stats(hoard_moe *h) {
+    if (!h) return fail(HOARD_ERR_INVALID, "null handle");
+    h->stats = hoard_moe_stats{};
     return HOARD_OK;
 }
 
@@ -560,6 +747,14 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
         if (value == 2 && !h->persistent_shape_ok)
             return fail(HOARD_ERR_UNSUPPORTED, "shape or device does not admit the persistent decode");
         h->persistent_mode = value;
+        return HOARD_OK;
+    case HOARD_OPT_POOL_NAIVE:
+        if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "pool naive flag %d", value);
+        if (value && h->cfg.pool_k > 0) {
+            // naive mode places request j in slot j; residency restarts empty
+            for (int l = 0; l < h->cfg.n_layer; ++l) h->lru.reset_layer(l);
+        }
+        h->pool_naive = value != 0;
         return HOARD_OK;
     default:
         return fail(HOARD_ERR_INVALID, "unknown option %d", option);
@@ -574,6 +769,9 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
         return HOARD_OK;
     case HOARD_OPT_PERSISTENT_AVAILABLE:
         *value = h->persistent_shape_ok ? 1 : 0;
+        return HOARD_OK;
+    case HOARD_OPT_POOL_NAIVE:
+        *value = h->pool_naive ? 1 : 0;
         return HOARD_OK;
     default:
         return fail(HOARD_ERR_INVALID, "unknown option %d", option);

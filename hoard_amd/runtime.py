@@ -99,6 +99,32 @@ class MoEStage:
         torch.cuda.synchronize()
         return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
 
+    def pool_ensure(self, layer: int, sel, copy_stream=None):
+        """Makes the experts sel resident in this layer's slots; returns the slots
+        (host) and a device tensor holding them, ordered on the current stream."""
+        torch = _torch()
+        sel_h = np.ascontiguousarray(sel, dtype=np.int32)
+        slots_h = np.zeros(self.shape.n_used, dtype=np.int32)
+        slots_d = torch.empty(self.shape.n_used, dtype=torch.int32, device="cuda")
+        cs = ctypes.c_void_p(copy_stream.cuda_stream) if copy_stream is not None else None
+        check(self.lib.hoard_moe_pool_ensure(self.h, layer, sel_h.ctypes.data, slots_h.ctypes.data,
+                                             self.ptr(slots_d), self.stream(), cs))
+        return slots_h, slots_d
+
+    def ffn_combine_dev(self, layer: int, fx_d, ids_d, w_d, res_d, out_d) -> None:
+        """hoard_moe_ffn_combine on device tensors, asynchronous on the current stream."""
+        check(self.lib.hoard_moe_ffn_combine(self.h, layer, self.ptr(fx_d), self.ptr(ids_d), self.ptr(w_d),
+                                             self.ptr(res_d), self.ptr(out_d), self.stream()))
+
+    def stats(self):
+        from . import MoeStats
+        st = MoeStats()
+        check(self.lib.hoard_moe_get_stats(self.h, ctypes.byref(st)))
+        return st
+
+    def reset_stats(self) -> None:
+        check(self.lib.hoard_moe_reset_stats(self.h))
+
     def set_option(self, option: int, value: int) -> None:
         check(self.lib.hoard_moe_set_option(self.h, option, value))
 

@@ -213,3 +213,43 @@ def make_hidden(shape: Shape, seed: int, layer: int, token: int = 0) -> tuple[np
 
 def as_ptr(a: np.ndarray) -> ctypes.c_void_p:
     return ctypes.c_void_p(a.ctypes.data)
+
+
+@dataclass
+class RoutingTrace:
+    """Per (token, layer): the n_used selected experts and their weights."""
+    sel: np.ndarray  # int32 [tokens, n_layer, n_used]
+    w: np.ndarray    # float32 [tokens, n_layer, n_used], each row sums to 1
+
+
+def routing_trace(shape: Shape, seed: int, tokens: int = 512, n_layer: int | None = None,
+                  zipf_s: float = 0.8, reuse_p: float = 0.4, window: int = 4) -> RoutingTrace:
+    """Seeded synthetic routing for the slot-pool workload: per layer, expert
+    popularity follows Zipf(zipf_s) over a random ranking of the experts; each
+    of a token's picks instead reuses, with probability reuse_p, an expert the
+    same layer selected in the previous `window` tokens.  Picks are distinct
+    within a token.  Weights are normalised Exp(1) draws."""
+    n_layer = n_layer or shape.n_layer
+    E, k = shape.n_expert, shape.n_used
+    rng = np.random.Generator(np.random.PCG64(0x7A1F0000 + seed))
+    ranks = [rng.permutation(E) for _ in range(n_layer)]
+    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** zipf_s
+    cdf = np.cumsum(p / p.sum())
+    sel = np.zeros((tokens, n_layer, k), dtype=np.int32)
+    for t in range(tokens):
+        for layer in range(n_layer):
+            recent = sorted(set(sel[max(0, t - window):t, layer].ravel().tolist())) if t else []
+            picked: list[int] = []
+            while len(picked) < k:
+                pool = [e for e in recent if e not in picked]
+                if pool and rng.random() < reuse_p:
+                    e = pool[int(rng.integers(len(pool)))]
+                else:
+                    e = int(ranks[layer][min(int(np.searchsorted(cdf, rng.random(), side="right")), E - 1)])
+                    if e in picked:
+                        continue
+                picked.append(e)
+            sel[t, layer] = picked
+    w = rng.exponential(1.0, size=(tokens, n_layer, k)).astype(np.float32)
+    w /= w.sum(axis=2, keepdims=True)
+    return RoutingTrace(sel, w.astype(np.float32))

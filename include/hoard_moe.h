@@ -114,13 +114,15 @@ int hoard_moe_route(hoard_moe *h, int layer, const float *fx_dev, int32_t *sel_d
 int hoard_moe_ffn_combine(hoard_moe *h, int layer, const float *fx_dev, const int32_t *ids_dev,
                           const float *w_dev, const float *res_dev, float *out_dev, void *stream);
 
-/* Route + FFN + combine for one token with nothing leaving the device
-   (pool_k == 0).  sel_dev / w_dev receive the selection when non-NULL. */
+/* Route + FFN + combine for one token with nothing leaving the device when
+   pool_k == 0 (with a slot pool the selection is read back to ensure the
+   slots, see hoard_moe_pool_ensure).  sel_dev / w_dev receive the selection
+   when non-NULL. */
 int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *res_dev,
                     float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 
 /* Stacked decode over layers [layer_begin, layer_end) for one token, in place
-   on x_dev (pool_k == 0): per layer fx = rms_norm(x, eps), x = layer(fx, x).
+   on x_dev: per layer fx = rms_norm(x, eps), x = layer(fx, x).
    The reference round-trips to the host twice per layer
    (src/run_moe_stream.cpp:362-370, 441-447); here the chain stays on device. */
 int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps,
@@ -157,8 +159,47 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
    HOARD_OPT_PERSISTENT_AVAILABLE (read-only) reports whether they admit it. */
 #define HOARD_OPT_PERSISTENT_DECODE 1
 #define HOARD_OPT_PERSISTENT_AVAILABLE 2
+/* HOARD_OPT_POOL_NAIVE: 1 = the reference's "naive" mode (every selected
+   expert is uploaded into slot j on every call, :417), 0 = LRU (default). */
+#define HOARD_OPT_POOL_NAIVE 3
 int hoard_moe_set_option(hoard_moe *h, int option, int value);
 int hoard_moe_get_option(hoard_moe *h, int option, int *value);
+
+/* Expert slot pool (pool_k > 0), the reference's Slots
+   (src/run_moe_stream.cpp:193-203): K HBM slots per layer, filled from the
+   full expert set kept in pinned host memory.
+
+   hoard_moe_pool_ensure makes the n_used experts sel_host[] of `layer`
+   resident, as the fetch step at :379-420 does: hits are classified first
+   and move to the front of the layer's LRU list (:385-387), then each miss
+   takes the least recently used slot, evicts its expert and is uploaded with
+   hipMemcpyAsync on copy_stream (:416-419; to_vram, :279-284).  copy_stream
+   first waits for the last FFN that read this layer's slots, and `stream` is
+   made to wait for the uploads, so an FFN launched on `stream` afterwards reads
+   them; with copy_stream distinct from `stream` the uploads of layer l+1 overlap
+   the FFN of layer l.  The slots go to slot_host and/or slot_dev (int32[n_used]),
+   to be passed as ids to hoard_moe_ffn_combine.  hoard_moe_layer and
+   hoard_moe_decode on a pool handle read the device-routed selection back
+   (a synchronisation, as the reference's D2H at :367) and call the same step. */
+int hoard_moe_pool_ensure(hoard_moe *h, int layer, const int32_t *sel_host, int32_t *slot_host,
+                          int32_t *slot_dev, void *stream, void *copy_stream);
+
+/* Counters since creation or the last reset: pool requests, hits, misses and
+   bytes uploaded (the reference's reqs / vram_hit / copies, :264), and the
+   batched path's token histogram. */
+int hoard_moe_get_stats(hoard_moe *h, hoard_moe_stats *out);
+int hoard_moe_reset_stats(hoard_moe *h);
+
+/* Host replay of the slot pool's LRU bookkeeping, with no device: the same
+   placement decisions hoard_moe_pool_ensure makes, for trace studies (the
+   reference's simulators, bench/profiler.py:65-91).  naive != 0 reproduces the
+   reference's "naive" mode (:417): request j goes to slot j, always a miss.
+   slot_out[n] receives the slots, miss_out[n] (optional) 1 per miss. */
+typedef struct hoard_slot_lru hoard_slot_lru;
+int hoard_slot_lru_create(int n_layer, int n_expert, int k, int naive, hoard_slot_lru **out);
+int hoard_slot_lru_access(hoard_slot_lru *p, int layer, const int32_t *sel, int n, int32_t *slot_out,
+                          uint8_t *miss_out);
+void hoard_slot_lru_destroy(hoard_slot_lru *p);
 
 /* Synchronises the device and reports a cross-workgroup wait that timed out
    in the one-launch decode (its output rows are then NaN). */
