@@ -57,9 +57,9 @@ class MoeStats(ctypes.Structure):
     ]
 
 
-KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN, KERNEL_DECODE = 0, 1, 2, 3
+KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN, KERNEL_DECODE, KERNEL_BATCHED = 0, 1, 2, 3, 4
 KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "down_combine",
-                KERNEL_DECODE: "decode_persistent"}
+                KERNEL_DECODE: "decode_persistent", KERNEL_BATCHED: "batched_experts"}
 TRACE_PHASES = 12
 OPT_PERSISTENT_DECODE = 1
 OPT_PERSISTENT_AVAILABLE = 2
@@ -90,6 +90,7 @@ ABI = {
     "hoard_moe_phase_trace": (_I, [_P, _I]),
     "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
     "hoard_moe_pool_ensure": (_I, [_P, _I, _P, _P, _P, _P, _P]),
+    "hoard_moe_forward_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "hoard_moe_get_stats": (_I, [_P, ctypes.POINTER(MoeStats)]),
     "hoard_moe_reset_stats": (_I, [_P]),
     "hoard_slot_lru_create": (_I, [_I, _I, _I, _I, ctypes.POINTER(_P)]),

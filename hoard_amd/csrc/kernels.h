@@ -63,6 +63,33 @@ struct DownArgs {
 };
 hipError_t launch_down_combine(const DownArgs &a, hipStream_t s);
 
+// Batched expert stage for M <= 16 tokens: grouping by expert, int8-MFMA
+// gate/up (+SwiGLU) and down tiles, ordered combine.
+struct BatchedArgs {
+    int M, n_embd, n_ff, E, k;
+    int gu_type, d_type;
+    const float *fx;        // [M][n_embd] normalised inputs
+    const float *res;       // [M][n_embd]
+    float *out;             // [M][n_embd] (may alias res)
+    const int32_t *sel;     // [M][k] from the router
+    const float *wsel;      // [M][k]
+    const uint8_t *gate, *up, *down;
+    size_t gstride, ustride, dstride;
+    uint8_t *q8x;           // Q8_K(fx): [M][n_embd/256] blocks of 304 bytes
+    uint8_t *q8h;           // Q8_K(h):  [umax][16][n_ff/256] blocks
+    float *hbuf;            // [umax][16][n_ff]
+    float *ybuf;            // [M][k][n_embd]
+    int *n_unique;          // [1]
+    int *slot_of;           // [E] scratch
+    int *uexp, *ucount;     // [umax] expert of each group, tokens in it
+    int *utok, *uslot;      // [umax][16] token and slot of each member
+    unsigned *hist;         // [E] tokens per expert in the call
+};
+constexpr int kBatchedMaxTokens = 16;
+constexpr size_t kQ8LBytes = 304;
+hipError_t launch_batched(const BatchedArgs &a, hipStream_t s);
+bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
+
 // Persistent stacked decode (one cooperative launch per token).
 struct DecodeLayer {
     const float *router;

@@ -109,6 +109,12 @@ struct hoard_moe {
     int32_t *pin_sel = nullptr;     // pinned [n_used]: device-routed ids read back on the on-demand path
     int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
     hipStream_t copy2 = nullptr;    // second upload stream: two copies in flight hide per-copy set-up
+    // batched path (allocated on first use)
+    uint8_t *b_q8x = nullptr, *b_q8h = nullptr;
+    float *b_h = nullptr, *b_y = nullptr;
+    int *b_ints = nullptr;          // n_unique, slot_of[E], uexp, ucount, utok, uslot
+    unsigned *b_hist = nullptr;     // [E]
+    bool hist_pending = false;      // a batched call ran since the histogram was last read
     size_t trace_layers = 0;
     bool tracing = false;
     int trace_last = 0;  // layers covered by the last traced decode
@@ -138,6 +144,12 @@ struct hoard_moe {
         hipHostFree(pin_sel);
         hipFree(slot_ids);
         if (copy2) hipStreamDestroy(copy2);
+        hipFree(b_q8x);
+        hipFree(b_q8h);
+        hipFree(b_h);
+        hipFree(b_y);
+        hipFree(b_ints);
+        hipFree(b_hist);
     }
     static void free_layer(Layer &L) {
         if (L.copied) hipEventDestroy(L.copied);
@@ -727,8 +739,111 @@ int hoard_moe_pool_ensure(hoard_moe *h, int layer, const int32_t *sel_host, int3
                        copy_stream ? (hipStream_t)copy_stream : (hipStream_t)stream);
 }
 
+int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
+                              float *out_dev, int32_t *sel_dev, float *w_dev, void *stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    const hoard_moe_cfg &c = h->cfg;
+    if (!fx_dev || !res_dev || !out_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
+    if (M < 1 || M > c.max_tokens || M > hoard::kBatchedMaxTokens)
+        return fail(HOARD_ERR_INVALID, "M %d outside 1..min(max_tokens %d, %d)", M, c.max_tokens,
+                    hoard::kBatchedMaxTokens);
+    if (c.pool_k > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path needs every expert resident (pool_k 0)");
+    if (c.n_ff_shexp > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path has no shared expert");
+    const Layer &L = h->layers[layer];
+    if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
+        return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
+                    L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
+    const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
+    const int umax = std::min(c.n_expert, T * c.n_used);
+    const int nb = c.n_embd / 256, nbh = c.n_ff / 256;
+    if (!h->b_q8x) {
+        rc = rc ? rc : dev_alloc((void **)&h->b_q8x, (size_t)T * nb * hoard::kQ8LBytes);
+        rc = rc ? rc : dev_alloc((void **)&h->b_q8h, (size_t)umax * hoard::kBatchedMaxTokens * nbh * hoard::kQ8LBytes);
+        rc = rc ? rc : dev_alloc((void **)&h->b_h, (size_t)umax * hoard::kBatchedMaxTokens * c.n_ff * sizeof(float));
+        rc = rc ? rc : dev_alloc((void **)&h->b_y, (size_t)T * c.n_used * c.n_embd * sizeof(float));
+        rc = rc ? rc : dev_alloc((void **)&h->b_ints,
+                                 sizeof(int) * (1 + c.n_expert + 2 * umax + 2 * umax * hoard::kBatchedMaxTokens));
+        rc = rc ? rc : dev_alloc((void **)&h->b_hist, sizeof(unsigned) * c.n_expert);
+        if (rc) return rc;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    int32_t *sel = sel_dev ? sel_dev : h->sel;
+    float *w = w_dev ? w_dev : h->wsel;
+    hoard::RouterArgs ra{};
+    ra.xin = fx_dev;
+    ra.fx_out = h->fx;
+    ra.w = L.router;
+    ra.n = c.n_embd;
+    ra.E = c.n_expert;
+    ra.k = c.n_used;
+    ra.renorm = c.renorm;
+    ra.M = M;
+    ra.logits = h->logits;
+    ra.counters = h->counters;
+    ra.sel = sel;
+    ra.wsel = w;
+    {
+        KernelMark mark(h, HOARD_KERNEL_ROUTER, s);
+        HIP_TRY(hoard::launch_router(ra, s));
+    }
+    hoard::BatchedArgs a{};
+    a.M = M;
+    a.n_embd = c.n_embd;
+    a.n_ff = c.n_ff;
+    a.E = c.n_expert;
+    a.k = c.n_used;
+    a.gu_type = L.gate_type;
+    a.d_type = L.down_type;
+    a.fx = fx_dev;
+    a.res = res_dev;
+    a.out = out_dev;
+    a.sel = sel;
+    a.wsel = w;
+    a.gate = L.gate;
+    a.up = L.up;
+    a.down = L.down;
+    a.gstride = L.gstride;
+    a.ustride = L.ustride;
+    a.dstride = L.dstride;
+    a.q8x = h->b_q8x;
+    a.q8h = h->b_q8h;
+    a.hbuf = h->b_h;
+    a.ybuf = h->b_y;
+    int *ip = h->b_ints;
+    a.n_unique = ip;
+    a.slot_of = ip + 1;
+    a.uexp = a.slot_of + c.n_expert;
+    a.ucount = a.uexp + umax;
+    a.utok = a.ucount + umax;
+    a.uslot = a.utok + umax * hoard::kBatchedMaxTokens;
+    a.hist = h->b_hist;
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_BATCHED, s);
+        e = hoard::launch_batched(a, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "batched launch: %s", hipGetErrorString(e));
+    h->stats.tokens += (uint64_t)M;
+    h->hist_pending = true;
+    return HOARD_OK;
+}
+
 int hoard_moe_get_stats(hoard_moe *h, hoard_moe_stats *out) {
     if (!h || !out) return fail(HOARD_ERR_INVALID, "null argument");
+    if (h->hist_pending) {
+        // histogram of the last batched call (synchronises with the device)
+        const int E = h->cfg.n_expert;
+        std::vector<unsigned> hist(E);
+        int nu = 0;
+        HIP_TRY(hipSetDevice(h->device));
+        HIP_TRY(hipDeviceSynchronize());
+        HIP_TRY(hipMemcpy(hist.data(), h->b_hist, sizeof(unsigned) * E, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(&nu, h->b_ints, sizeof(int), hipMemcpyDeviceToHost));
+        for (int e = 0; e < E && e < 1024; ++e) h->stats.expert_hist[e] = hist[e];
+        h->stats.last_unique = nu;
+        h->hist_pending = false;
+    }
     *out = h->stats;
     return HOARD_OK;
 }

@@ -99,6 +99,19 @@ class MoEStage:
         torch.cuda.synchronize()
         return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
 
+    def forward_batched(self, layer: int, fx, res):
+        """M tokens at once: fx, res [M][n_embd] -> out [M][n_embd], sel, w [M][n_used]."""
+        torch = _torch()
+        fx_d, res_d = self.dev(fx), self.dev(res)
+        M = fx_d.shape[0]
+        out = torch.empty_like(res_d)
+        sel = torch.empty((M, self.shape.n_used), dtype=torch.int32, device="cuda")
+        w = torch.empty((M, self.shape.n_used), dtype=torch.float32, device="cuda")
+        check(self.lib.hoard_moe_forward_batched(self.h, layer, M, self.ptr(fx_d), self.ptr(res_d), self.ptr(out),
+                                                 self.ptr(sel), self.ptr(w), self.stream()))
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
+
     def pool_ensure(self, layer: int, sel, copy_stream=None):
         """Makes the experts sel resident in this layer's slots; returns the slots
         (host) and a device tensor holding them, ordered on the current stream."""

@@ -128,6 +128,20 @@ int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *r
 int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps,
                      void *stream);
 
+/* Batched expert stage for M tokens (1 <= M <= min(max_tokens, 16)), every
+   token routed independently: the counterpart of ggml_mul_mat_id over the
+   experts with per-token ids and the weighted sum over them
+   (src/run_specloop.cpp:126-139, src/run_m1.cpp:97-108).  The (token, slot)
+   pairs are grouped by expert so each selected expert's weights are read once
+   per call, and the expert products run on int8 MFMA; each token's result is
+   the single-token hoard_moe_layer's bit for bit.  fx_dev, res_dev, out_dev:
+   [M][n_embd] (out may alias res); sel_dev / w_dev ([M][n_used]) receive the
+   routing when non-NULL.  The call's per-expert token histogram and unique
+   expert count are reported by hoard_moe_get_stats.  Needs pool_k == 0 and no
+   shared expert. */
+int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
+                              float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
+
 /* Per-kernel timing, the device counterpart of the reference's phase timers
    (tA/tFetch/tB, src/run_moe_stream.cpp:291,311,377,422,448): while enabled,
    every kernel launch is bracketed by a pair of hipEvents on its stream.
@@ -137,6 +151,7 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
 #define HOARD_KERNEL_GATEUP 1
 #define HOARD_KERNEL_DOWN 2
 #define HOARD_KERNEL_DECODE 3
+#define HOARD_KERNEL_BATCHED 4 /* the batched path's grouping, MFMA and combine launches together */
 #define HOARD_KERNEL_KINDS 8
 typedef struct hoard_moe_kernel_times {
     uint64_t launches[HOARD_KERNEL_KINDS];
