@@ -29,6 +29,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;                   // weight rows per MFMA tile
 constexpr int kMaxTok = kBatchedMaxTokens;  // token columns per MFMA tile
+constexpr int kMaxExperts = 1024;
 static_assert(sizeof(Q8L) == kQ8LBytes, "Q8_K block size shared with the host");
 
 __device__ __forceinline__ Q8L *q8(uint8_t *p) { return reinterpret_cast<Q8L *>(p); }
@@ -197,31 +198,53 @@ __global__ __launch_bounds__(64) void prep_kernel(BatchedArgs a) {
         wave_quantize_q8l(a.fx + (size_t)t * a.n_embd + (size_t)b * QK, q8(a.q8x) + (size_t)t * nb + b);
         return;
     }
-    // last workgroup: experts in order of first use (token-major, slot order)
-    if (threadIdx.x == 0) {
-        for (int e = 0; e < a.E; ++e) a.slot_of[e] = -1;
-        int U = 0;
-        for (int t = 0; t < a.M; ++t) {
-            for (int j = 0; j < a.k; ++j) {
-                int e = a.sel[t * a.k + j];
-                if (e < 0 || e >= a.E) e = 0;  // the router maps NaN logits to expert 0 with a NaN weight
-                int u = a.slot_of[e];
-                if (u < 0) {
-                    u = U++;
-                    a.slot_of[e] = u;
-                    a.uexp[u] = e;
-                    a.ucount[u] = 0;
-                }
-                const int c = a.ucount[u]++;
-                if (c < kMaxTok) {
-                    a.utok[u * kMaxTok + c] = t;
-                    a.uslot[u * kMaxTok + c] = j;
-                }
-            }
-        }
-        a.n_unique[0] = U;
-        for (int e = 0; e < a.E; ++e) a.hist[e] = a.slot_of[e] >= 0 ? (unsigned)a.ucount[a.slot_of[e]] : 0u;
+    // last workgroup: group the (token, slot) pairs by expert.  A token selects
+    // an expert at most once, so a per-expert bitmask of tokens orders each
+    // group by token; groups are numbered in ascending expert id.
+    __shared__ unsigned mask[kMaxExperts];
+    __shared__ int uidx[kMaxExperts];
+    __shared__ int wave_total;
+    const int lane = threadIdx.x, E = a.E, P = a.M * a.k;
+    for (int e = lane; e < E; e += 64) mask[e] = 0u;
+    __syncthreads();
+    for (int p = lane; p < P; p += 64) {
+        int e = a.sel[p];
+        if (e < 0 || e >= E) e = 0;  // the router maps NaN logits to expert 0 with a NaN weight
+        atomicOr(&mask[e], 1u << (p / a.k));
     }
+    __syncthreads();
+    // ascending prefix count of used experts: lane owns a contiguous run of experts
+    const int per = (E + 63) / 64, e0 = lane * per;
+    int cnt = 0;
+    for (int e = e0; e < e0 + per && e < E; ++e) cnt += mask[e] ? 1 : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+    }
+    int u = incl - cnt;
+    for (int e = e0; e < e0 + per && e < E; ++e) {
+        const unsigned m = mask[e];
+        a.hist[e] = (unsigned)__popc(m);
+        if (m) {
+            uidx[e] = u;
+            a.uexp[u] = e;
+            a.ucount[u] = __popc(m);
+            ++u;
+        }
+    }
+    if (lane == 63) wave_total = incl;
+    __syncthreads();
+    for (int p = lane; p < P; p += 64) {
+        const int t = p / a.k, j = p % a.k;
+        int e = a.sel[p];
+        if (e < 0 || e >= E) e = 0;
+        const int g = uidx[e], c = __popc(mask[e] & ((1u << t) - 1u));
+        a.utok[g * kMaxTok + c] = t;
+        a.uslot[g * kMaxTok + c] = j;
+    }
+    if (lane == 0) a.n_unique[0] = wave_total;
 }
 
 // -- gate/up: one 16-row tile of gate (wave 0) and up (wave 1) of one expert --

@@ -38,6 +38,7 @@ constexpr int kXcds = 8;
 constexpr int kPerXcd = 32;
 constexpr int kFlagStride = 32;             // words: one 128-byte line per flag
 constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
+constexpr int kDecodeK = 8;                     // experts per token: one per XCD
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned v;
@@ -65,18 +66,32 @@ __device__ __forceinline__ bool reached(unsigned v, unsigned target) { return (i
 // 1 KB chunks (64 lanes x 16 B) spread over waves [w0, w0+nw).  Rounds the
 // source down to 16 bytes (returned offset) and reads whole chunks, i.e. up to
 // 1 KB + 15 bytes past the end, which device allocations keep as padding.
+__device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src);
 __device__ __forceinline__ int issue_lds_copy(uint8_t *dst, const uint8_t *src, size_t nbytes, int w0, int nw) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(src);
     const uintptr_t a0 = a & ~(uintptr_t)15;
     const int off = (int)(a - a0);
     const int nchunks = (int)((off + nbytes + 1023) >> 10);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     if (wave >= w0 && wave < w0 + nw) {
         for (int c = wave - w0; c < nchunks; c += nw)
-            __builtin_amdgcn_global_load_lds((const void *)(a0 + (size_t)c * 1024 + lane * 16),
-                                             (lds_void *)(dst + c * 1024), 16, 0, 0);
+            dma_chunk(dst + c * 1024, reinterpret_cast<const uint8_t *>(a0) + (size_t)c * 1024);
     }
     return off;
+}
+
+// One 1 KB chunk (64 lanes x 16 bytes) from global memory into LDS, issued
+// from inline assembly: the compiler then does not know the wave has LDS DMA
+// in flight and does not make its next LDS read wait for it.  Every wave that
+// issues chunks waits for them itself (s_waitcnt vmcnt) before the barrier
+// after which other waves read them.
+__device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src) {
+    const int lane = threadIdx.x & 63;
+    const lds_void *lp = (const lds_void *)dst;  // generic -> LDS address space: the 32-bit LDS offset
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lp);
+    const uint8_t *g = src + lane * 16;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
 }
 
 __host__ __device__ __forceinline__ size_t chunk_region(size_t nbytes) { return ((nbytes + 15 + 1023) >> 10) << 10; }
@@ -249,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         }
         stamp(l, 1);
 
-        // -- P1: rms_norm scale, fx, router rows (8 lanes each), Q8_K(fx) --
+        // -- P1: rms_norm scale, fx, router rows (32 lanes each) --
         {
             double ss = 0.0;
             for (int i = tid; i < n; i += kThreads) {
@@ -263,38 +278,35 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         {
             double tot = 0.0;
             for (int w = 0; w < kWaves; ++w) tot += red_d[w];
-            const float mean = (float)(tot / (double)n);
+            static_assert((kEmbd & (kEmbd - 1)) == 0, "n_embd a power of two: the mean is an exact multiply");
+            const float mean = (float)(tot * (1.0 / (double)kEmbd));
             const float scale = 1.0f / sqrtf(mean + a.eps);
             for (int i = tid; i < n; i += kThreads) fxs[i] = xs[i] * scale;
         }
         __syncthreads();
-        if (wave == 0) {
-            const int row = lane >> 3, m = lane & 7;
+        {
+            // lane l of a 32-lane half-wave holds accumulator l of ggml's x86 f32
+            // dot (elements 32i + l, i ascending); rows 2w and 2w+1 on wave w
+            const int row = 2 * wave + (lane >> 5), l32 = lane & 31;
             if (row < rw) {
-                const float *wr = wl + (size_t)row * kEmbd + 4 * m;
-                const float *fr = fxs + 4 * m;
-                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-                // batches of 8 steps: all 16 LDS reads are issued before the first FMA waits
-                for (int i0 = 0; i0 < kEmbd; i0 += 32 * 8) {
-                    float4 wv[8], fv[8];
+                const float *wr = wl + (size_t)row * kEmbd + l32;
+                const float *fr = fxs + l32;
+                float acc = 0.0f;
+                for (int i0 = 0; i0 < kEmbd; i0 += 32 * 16) {
+                    float wv[16], fv[16];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        wv[j] = *reinterpret_cast<const float4 *>(wr + i0 + 32 * j);
-                        fv[j] = *reinterpret_cast<const float4 *>(fr + i0 + 32 * j);
+                    for (int j = 0; j < 16; ++j) {
+                        wv[j] = wr[i0 + 32 * j];
+                        fv[j] = fr[i0 + 32 * j];
                     }
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        a0 = fmaf(wv[j].x, fv[j].x, a0);
-                        a1 = fmaf(wv[j].y, fv[j].y, a1);
-                        a2 = fmaf(wv[j].z, fv[j].z, a2);
-                        a3 = fmaf(wv[j].w, fv[j].w, a3);
-                    }
+                    for (int j = 0; j < 16; ++j) acc = fmaf(wv[j], fv[j], acc);
                 }
-                const float r = group8_ggml_fold(a0, a1, a2, a3);
-                if (m == 0) st_l2(LGx + rank * rw + row, tag(r, seq));
+                acc = acc + __shfl_xor(acc, 16);  // accumulators a and a+16
+                const float r = row16_ggml_fold(acc);
+                if (l32 == 0) st_l2(LGx + rank * rw + row, tag(r, seq));
             }
         }
-        for (int b = wave; b < nb; b += kWaves) wave_quantize_q8l(fxs + b * QK, &q8x[b]);
         stamp(l, 2);
         stamp(l, 3);
 
@@ -333,17 +345,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             // rank of expert e = experts ahead of it in (probability desc, index asc)
             // order; four lanes split the comparisons and add their counts
             const int e = tid >> 2, q = tid & 3;
-            const int span = E >> 2;
+            const int span = E >> 2;  // a multiple of 8, at most 32
             int r = 0;
             float pe = 0.0f;
             if (e < E) {
                 pe = ps[e];
-                for (int e4 = q * span; e4 < q * span + span; e4 += 4) {
-                    const float4 pv = *reinterpret_cast<const float4 *>(ps + e4);
-                    r += (pv.x > pe || (pv.x == pe && e4 < e)) ? 1 : 0;
-                    r += (pv.y > pe || (pv.y == pe && e4 + 1 < e)) ? 1 : 0;
-                    r += (pv.z > pe || (pv.z == pe && e4 + 2 < e)) ? 1 : 0;
-                    r += (pv.w > pe || (pv.w == pe && e4 + 3 < e)) ? 1 : 0;
+                float4 pv[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    if (4 * c < span) pv[c] = *reinterpret_cast<const float4 *>(ps + q * span + 4 * c);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    if (4 * c < span) {
+                        const int e4 = q * span + 4 * c;
+                        r += (pv[c].x > pe || (pv[c].x == pe && e4 < e)) ? 1 : 0;
+                        r += (pv[c].y > pe || (pv[c].y == pe && e4 + 1 < e)) ? 1 : 0;
+                        r += (pv[c].z > pe || (pv[c].z == pe && e4 + 2 < e)) ? 1 : 0;
+                        r += (pv[c].w > pe || (pv[c].w == pe && e4 + 3 < e)) ? 1 : 0;
+                    }
                 }
             }
             r = group4_sum(r);
@@ -355,11 +374,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         lds_barrier();
         if (wave == 0) {
             // every lane forms the same left-to-right sum; lane j normalises weight j
-            float ws = 0.0f;
-            for (int j = 0; j < k; ++j) {
-                const int sj = sel_s[j];
-                ws = ws + ((sj < 0 || sj >= E) ? __builtin_nanf("") : w_s[j]);  // NaN logits only
+            int sv[kDecodeK];
+            float wv[kDecodeK];
+#pragma unroll
+            for (int j = 0; j < kDecodeK; ++j) {
+                sv[j] = sel_s[j];
+                wv[j] = w_s[j];
             }
+            float ws = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDecodeK; ++j)
+                ws = ws + ((sv[j] < 0 || sv[j] >= E) ? __builtin_nanf("") : wv[j]);  // NaN logits only
             int sj = lane < k ? sel_s[lane] : 0;
             float wj = lane < k ? w_s[lane] : 0.0f;
             if (sj < 0 || sj >= E) {
@@ -383,36 +408,50 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         }
         stamp(l, 4);
 
-        // -- P3: waves 0-3 stream gate/up rows, waves 4-7 stream down rows --
+        // -- P3: waves 0-3 stream the gate/up rows, waves 4-7 the down rows, into LDS --
         const int e = has_expert ? sel_s[xcc] : 0;
         constexpr size_t rbg = (size_t)NB * QType<TGU>::bytes, rbu = rbg;
         constexpr size_t rbd = (size_t)NBH * QType<TD>::bytes;
-        const uint8_t *gsrc = L.gate + (size_t)e * L.gstride + (size_t)rank * R * rbg;
-        const uint8_t *usrc = L.up + (size_t)e * L.ustride + (size_t)rank * R * rbu;
-        const uint8_t *dsrc = L.down + (size_t)e * L.dstride + (size_t)rank * RD * rbd;
-        const int og = (int)(reinterpret_cast<uintptr_t>(gsrc) & 15);
-        const int ou = (int)(reinterpret_cast<uintptr_t>(usrc) & 15);
-        const int od = (int)(reinterpret_cast<uintptr_t>(dsrc) & 15);
+        constexpr int kR = NBH * QK / kPerXcd, kRD = kEmbd / kPerXcd;  // rows per workgroup
+        constexpr int kGuChunks = (int)((kR * rbg + 1023) / 1024);
+        constexpr int kDownChunks = (int)((kRD * rbd + 1023) / 1024);
+        static_assert(2 * kR <= kThreads / 8, "one 8-lane group per gate/up row");
+        // sources are 16-byte aligned (checked on the host), so rows start at the staged offset 0
+        const uint8_t *gsrc = L.gate + (size_t)e * L.gstride + (size_t)rank * kR * rbg;
+        const uint8_t *usrc = L.up + (size_t)e * L.ustride + (size_t)rank * kR * rbu;
+        const uint8_t *dsrc = L.down + (size_t)e * L.dstride + (size_t)rank * kRD * rbd;
+        // Drain this wave's ordinary loads first: the compiler's waits for them
+        // count outstanding operations, and the chunks issued below would
+        // otherwise be counted in front of them.
+        __builtin_amdgcn_s_waitcnt(0);
         if (has_expert) {
-            issue_lds_copy(smem + S.gate, gsrc, (size_t)R * rbg, 0, kWaves / 2);
-            issue_lds_copy(smem + S.up, usrc, (size_t)R * rbu, 0, kWaves / 2);
-            issue_lds_copy(smem + S.down, dsrc, (size_t)RD * rbd, kWaves / 2, kWaves / 2);
+            if (wave < kWaves / 2) {
+                for (int c = wave; c < kGuChunks; c += kWaves / 2) {
+                    dma_chunk(smem + S.gate + c * 1024, gsrc + (size_t)c * 1024);
+                    dma_chunk(smem + S.up + c * 1024, usrc + (size_t)c * 1024);
+                }
+            } else {
+                for (int c = wave - kWaves / 2; c < kDownChunks; c += kWaves / 2)
+                    dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+            }
         }
+        // Q8_K(fx) while the rows are in flight
+        for (int b = wave; b < nb; b += kWaves) wave_quantize_q8l(fxs + b * QK, &q8x[b]);
         stamp(l, 5);
 
         if (has_expert) {
             // -- P4: gate/up rows on every wave while the down rows still stream --
-            if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // the gate/up rows these waves issued
+            if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // the gate/up chunks these waves issued
             lds_barrier();
             stamp(l, 6);
             {
-                // one 8-lane group per row (2R <= 64), lane t holding Q8_K(x) block t
+                // one 8-lane group per row, lane t holding Q8_K(x) block t
                 Q8Reg xr;
                 if (t8 < NB) load_q8reg(q8x[t8], xr);
                 const int pr = grp;
-                if (pr < 2 * R) {
-                    const int mat = pr >= R, row = pr - mat * R;
-                    const uint8_t *rp = mat ? smem + S.up + ou + row * rbu : smem + S.gate + og + row * rbg;
+                if (pr < 2 * kR) {
+                    const int mat = pr >= kR, row = pr - mat * kR;
+                    const uint8_t *rp = mat ? smem + S.up + row * rbu : smem + S.gate + row * rbg;
                     const float v = lpb_row_q4k<NB>(rp, xr, t8);
                     if (t8 == NB - 1) gu[pr] = v;
                 }
@@ -455,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 // share their 4-byte alignment when the row size is 2 mod 4
                 const int row = 16 * (wave >> 1) + 2 * (grp & 7) + (wave & 1);
                 if (row < RD) {
-                    const float y = g8_row_q6k_u<NBH>(smem + S.down + od + row * rbd, q8h, t8);
+                    const float y = g8_row_q6k_u<NBH>(smem + S.down + row * rbd, q8h, t8);
                     if (t8 == 0) ys[row] = y;
                 }
             } else {
@@ -463,7 +502,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 if (t8 < NBH) load_q8reg(q8h[t8], hr);
                 const int row = grp;
                 if (row < RD) {
-                    const float y = lpb_row_q4k<NBH>(smem + S.down + od + row * rbd, hr, t8);
+                    const float y = lpb_row_q4k<NBH>(smem + S.down + row * rbd, hr, t8);
                     if (t8 == NBH - 1) ys[row] = y;
                 }
             }

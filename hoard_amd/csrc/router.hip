@@ -20,6 +20,9 @@ namespace {
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 constexpr int kMaxK = 16;
+constexpr int kMaxRouterTokens = 16;    // tokens per call of the multi-token logits kernel
+
+__device__ void router_tail(const RouterArgs &a, int tok);
 
 __global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
     const int lane = threadIdx.x;
@@ -72,7 +75,68 @@ __global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
     __syncthreads();
     if (!is_last) return;
     __threadfence();
+    router_tail(a, tok);
+    if (lane == 0) a.counters[tok] = 0u;
+}
 
+// Logits for M > 1 tokens (xin = fx): a workgroup of 4 waves takes 8 rows
+// (32 lanes per row) against 4 tokens staged in LDS, so the router weight is
+// read M/4 times per call instead of M times.  Per token the accumulation
+// order is the single-token kernel's.
+constexpr int kRowsPerWg = 8;
+constexpr int kTokPerWg = 4;
+
+__global__ __launch_bounds__(256) void router_rows_m_kernel(RouterArgs a) {
+    extern __shared__ float xs[];  // [kTokPerWg][n]
+    const int n = a.n, E = a.E;
+    const int t0 = blockIdx.y * kTokPerWg;
+    const int nt = min(kTokPerWg, a.M - t0);
+    const float4 *src = reinterpret_cast<const float4 *>(a.xin + (size_t)t0 * n);
+    for (int i = threadIdx.x; i < nt * n / 4; i += blockDim.x) reinterpret_cast<float4 *>(xs)[i] = src[i];
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
+    const int row = blockIdx.x * kRowsPerWg + wave * 2 + (lane >> 5);
+    if (row >= E) return;
+    const float *wr = a.w + (size_t)row * n;
+    float acc[kTokPerWg] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < n; i0 += 32 * 16) {
+        float w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = i0 + 32 * i < n ? wr[i0 + 32 * i + l] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kTokPerWg; ++t) {
+            if (t < nt) {
+                const float *x = xs + t * n + i0 + l;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (i0 + 32 * i < n) acc[t] = fmaf(w[i], x[32 * i], acc[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kTokPerWg; ++t) {
+        if (t < nt) {
+            float v = acc[t];
+            v = v + __shfl_xor(v, 16);
+            v = v + __shfl_xor(v, 8);
+            v = v + __shfl_xor(v, 4);
+            v = v + __shfl_xor(v, 1);
+            v = v + __shfl_xor(v, 2);
+            if (l == 0) a.logits[(size_t)(t0 + t) * E + row] = v;
+        }
+    }
+}
+
+// Softmax, top-k and renorm of one token per workgroup (M > 1).
+__global__ __launch_bounds__(64) void router_tail_kernel(RouterArgs a) { router_tail(a, blockIdx.x); }
+
+}  // namespace
+
+namespace {
+
+__device__ void router_tail(const RouterArgs &a, int tok) {
+    const int lane = threadIdx.x;
+    const int E = a.E;
     const float *lg = a.logits + (size_t)tok * E;
     float p[kMaxExpertsPerLane];
     float mx = -INFINITY;
@@ -153,12 +217,19 @@ __global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
             a.wsel[(size_t)tok * a.k + j] = wv[j];
         }
     }
-    if (lane == 0) a.counters[tok] = 0u;
 }
 
 }  // namespace
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t s) {
+    if (a.M > 1 && !a.xin_is_residual && a.M <= kMaxRouterTokens) {
+        const dim3 grid((unsigned)((a.E + kRowsPerWg - 1) / kRowsPerWg), (unsigned)((a.M + kTokPerWg - 1) / kTokPerWg));
+        const size_t lds = sizeof(float) * kTokPerWg * (size_t)a.n;
+        if (lds > 65536) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(router_rows_m_kernel, grid, dim3(256), lds, s, a);
+        hipLaunchKernelGGL(router_tail_kernel, dim3((unsigned)a.M), dim3(64), 0, s, a);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((a.E + 1) / 2), (unsigned)a.M);
     hipLaunchKernelGGL(router_kernel, grid, dim3(64), 0, s, a);
     return hipGetLastError();
