@@ -39,6 +39,8 @@ constexpr int kPerXcd = 32;
 constexpr int kFlagStride = 32;             // words: one 128-byte line per flag
 constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
 constexpr int kDecodeK = 8;                     // experts per token: one per XCD
+constexpr int kTopkWave = 2;                    // polls the logits, softmax, renorm
+constexpr int kPublishWave = 7;                 // stores h and y
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned v;
@@ -124,8 +126,10 @@ __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, si
     return s;
 }
 
-// Raw workgroup barrier: LDS writes of every wave are done, global and LDS-DMA
-// loads may stay in flight (a __syncthreads fence would wait for those too).
+// Raw workgroup barrier: LDS writes of every wave are done; global loads,
+// stores and LDS DMA may stay in flight (the fence of __syncthreads would wait
+// for them).  Waves exchange data only through LDS inside the layer loop, and
+// every wave that issued LDS DMA waits for it itself before such a barrier.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // {value, seq} words: the value travels with the sequence number of the step that
@@ -236,11 +240,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         const int cur = (l - a.l0) & 1;
         const bool last = l + 1 == a.l1;
         stamp(l, 0);
-        __builtin_amdgcn_s_waitcnt(0);  // router rows in flight since the previous layer
-        if (l > a.l0) {
-            // x of this layer: the XCD's 32 workgroups published 64 rows each
+        // A wave's vmcnt counts its stores too and retires in order, so a wave that
+        // polls must not have stores of its own in flight: each exchange below is
+        // published by one set of waves and polled by another.
+        if (wave >= kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // router rows these waves prefetched
+        if (l > a.l0 && wave >= kWaves / 2) {
+            // x of this layer: the XCD's 32 workgroups published 64 rows each; gathered
+            // by waves 4-7 (wave 0 has just stored its combined rows)
             const uint64_t *xsrc = a.X + ((size_t)cur * kXcds + xcc) * n;
-            for (int i0 = 4 * tid; i0 < n; i0 += 4 * kThreads) {
+            for (int i0 = 4 * (tid - kThreads / 2); i0 < n; i0 += 4 * (kThreads / 2)) {
                 uint64_t w[4];
                 const bool got = poll(
                     [&]() {
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 *reinterpret_cast<float4 *>(xs + i0) = make_float4(tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3]));
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (sh_fail) {
             ok = false;
             break;
@@ -274,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             ss = wave_sum_d(ss);
             if (lane == 0) red_d[wave] = ss;
         }
-        __syncthreads();
+        lds_barrier();
         {
             double tot = 0.0;
             for (int w = 0; w < kWaves; ++w) tot += red_d[w];
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             const float scale = 1.0f / sqrtf(mean + a.eps);
             for (int i = tid; i < n; i += kThreads) fxs[i] = xs[i] * scale;
         }
-        __syncthreads();
+        lds_barrier();
         {
             // lane l of a 32-lane half-wave holds accumulator l of ggml's x86 f32
             // dot (elements 32i + l, i ascending); rows 2w and 2w+1 on wave w
@@ -310,8 +318,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 2);
         stamp(l, 3);
 
-        // -- P2: softmax over all experts (wave 0), ranks (all threads), renorm (wave 0) --
-        if (wave == 0) {
+        // -- P2: softmax (wave 2: waves 0-1 stored the logits), ranks (all threads), renorm (wave 2) --
+        if (wave == kTopkWave) {
             uint64_t w0 = 0, w1 = 0;
             const bool got = poll(
                 [&]() {
@@ -372,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             }
         }
         lds_barrier();
-        if (wave == 0) {
+        if (wave == kTopkWave) {
             // every lane forms the same left-to-right sum; lane j normalises weight j
             int sv[kDecodeK];
             float wv[kDecodeK];
@@ -401,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 w_s[lane] = wj;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (sh_fail) {
             ok = false;
             break;
@@ -457,9 +465,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 }
             }
             lds_barrier();
-            if (tid < R) {
-                const float g = gu[tid], uu = gu[R + tid];
-                st_l2(Hx + rank * R + tid, tag(g / (1.0f + expf(-g)) * uu, seq + 1u));
+            if (wave == kPublishWave && lane < R) {  // not a wave that polls h
+                const float g = gu[lane], uu = gu[R + lane];
+                st_l2(Hx + rank * R + lane, tag(g / (1.0f + expf(-g)) * uu, seq + 1u));
             }
             stamp(l, 7);
 
@@ -507,13 +515,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 }
             }
             lds_barrier();
-            if (wave == 0) {
+            if (wave == kPublishWave) {  // wave 0 polls y next
                 uint64_t *Y = a.Y + ((size_t)cur * kXcds + xcc) * n + rank * RD;
                 for (int i = lane; i < RD; i += 64) st_dev64(Y + i, tag(ys[i], seq + 2u));
             }
             stamp(l, 9);
         }
-        // next layer's router rows, from waves that touch no other memory before then
+        // next layer's router rows, from the waves that gather x next
         if (!last && wave >= kWaves / 2) prefetch_router(l + 1, kWaves / 2, kWaves / 2);
 
         // -- P6 (wave 0): combine rows [RD*rank, RD*rank+RD) over every expert slot --
