@@ -416,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         }
         stamp(l, 4);
 
-        // -- P3: waves 0-3 stream the gate/up rows, waves 4-7 the down rows, into LDS --
+        // -- P3: waves 0-3 stream the gate/up rows into LDS (waves 6-7 the down rows, in P4) --
         const int e = has_expert ? sel_s[xcc] : 0;
         constexpr size_t rbg = (size_t)NB * QType<TGU>::bytes, rbu = rbg;
         constexpr size_t rbd = (size_t)NBH * QType<TD>::bytes;
@@ -432,15 +432,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         // count outstanding operations, and the chunks issued below would
         // otherwise be counted in front of them.
         __builtin_amdgcn_s_waitcnt(0);
-        if (has_expert) {
-            if (wave < kWaves / 2) {
-                for (int c = wave; c < kGuChunks; c += kWaves / 2) {
-                    dma_chunk(smem + S.gate + c * 1024, gsrc + (size_t)c * 1024);
-                    dma_chunk(smem + S.up + c * 1024, usrc + (size_t)c * 1024);
-                }
-            } else {
-                for (int c = wave - kWaves / 2; c < kDownChunks; c += kWaves / 2)
-                    dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+        if (has_expert && wave < kWaves / 2) {
+            for (int c = wave; c < kGuChunks; c += kWaves / 2) {
+                dma_chunk(smem + S.gate + c * 1024, gsrc + (size_t)c * 1024);
+                dma_chunk(smem + S.up + c * 1024, usrc + (size_t)c * 1024);
             }
         }
         // Q8_K(fx) while the rows are in flight
@@ -452,6 +447,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // the gate/up chunks these waves issued
             lds_barrier();
             stamp(l, 6);
+            // the down rows are needed only after the h exchange: fetched now, after
+            // the gate/up rows, so that those did not share the bandwidth; issued by
+            // waves 6-7, which have no gate/up row when 2R <= 48
+            if (wave >= kWaves - 2)
+                for (int c = wave - (kWaves - 2); c < kDownChunks; c += 2)
+                    dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
             {
                 // one 8-lane group per row, lane t holding Q8_K(x) block t
                 Q8Reg xr;
