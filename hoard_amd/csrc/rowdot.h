@@ -25,42 +25,12 @@ static_assert(sizeof(Q8L) == 304, "Q8L is 19 x 16 bytes");
 // Wave quantisation of 256 floats to Q8_K (ggml quantize_row_q8_K semantics:
 // largest |x| with its sign, first index on ties; iscale = -127/max;
 // q = min(127, nearest_int(iscale*x)); d = 1/iscale; all-zero block -> 0).
+__device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out);
 __device__ __forceinline__ void wave_quantize_q8l(const float *x, Q8L *out) {
     const int lane = threadIdx.x & 63;
     const float4 v4 = *reinterpret_cast<const float4 *>(x + 4 * lane);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    float amax = 0.0f;
-    int idx = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > amax) {
-            amax = a;
-            idx = 4 * lane + i;
-        }
-    }
-    wave_argmax(amax, idx);
-    if (idx == 0x7fffffff) {
-        out->qs[lane] = 0;
-        if (lane < 16) out->bsums[lane] = 0;
-        if (lane == 0) out->d = 0.0f;
-        return;
-    }
-    const float mval = x[idx];
-    const float iscale = -127.0f / mval;
-    uint32_t packed = 0;
-    int s = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int q = nearest_int(iscale * v[i]);
-        q = q < 127 ? q : 127;
-        s += q;
-        packed |= ((uint32_t)(q & 0xff)) << (8 * i);
-    }
-    out->qs[lane] = (int32_t)packed;
-    s = group4_sum(s);
-    if ((lane & 3) == 0) out->bsums[lane >> 2] = (int16_t)s;
-    if (lane == 0) out->d = 1.0f / iscale;
+    wave_quantize_q8l_regs(v, out);
 }
 
 // One Q4_K row of nb super-blocks (16-byte aligned in LDS) dotted with x.
@@ -330,30 +300,24 @@ __device__ __forceinline__ float lpb_row_q4k(const uint8_t *row, const Q8Reg &x,
 }
 
 // Q8_K quantisation of 256 values held 4 per lane (lane l: elements 4l..4l+3).
+// The scale comes from the first element (lowest index) of largest magnitude:
+// a wave max of |x|, then the lowest lane holding it and its first component.
 __device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out) {
     const int lane = threadIdx.x & 63;
-    float amax = 0.0f;
-    int idx = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > amax) {
-            amax = a;
-            idx = 4 * lane + i;
-        }
-    }
-    wave_argmax(amax, idx);
-    if (idx == 0x7fffffff) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    if (!(amax >= 0.0f)) amax = 0.0f;  // NaN elements never set the scale
+    amax = wave_max_f(amax);
+    if (!(amax > 0.0f)) {  // all zero (or NaN): d = 0, q = 0
         out->qs[lane] = 0;
         if (lane < 16) out->bsums[lane] = 0;
         if (lane == 0) out->d = 0.0f;
         return;
     }
-    // the signed value at idx: lane idx/4, component idx%4
-    const int src = idx >> 2, comp = idx & 3;
+    const bool has = fabsf(v[0]) == amax || fabsf(v[1]) == amax || fabsf(v[2]) == amax || fabsf(v[3]) == amax;
+    const int src = __ffsll((unsigned long long)__builtin_amdgcn_ballot_w64(has)) - 1;
     const float c0 = readlane_f(v[0], src), c1 = readlane_f(v[1], src), c2 = readlane_f(v[2], src),
                 c3 = readlane_f(v[3], src);
-    const float mval = comp == 0 ? c0 : (comp == 1 ? c1 : (comp == 2 ? c2 : c3));
+    const float mval = fabsf(c0) == amax ? c0 : (fabsf(c1) == amax ? c1 : (fabsf(c2) == amax ? c2 : c3));
     const float iscale = -127.0f / mval;
     uint32_t packed = 0;
     int s = 0;
