@@ -244,7 +244,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         // polls must not have stores of its own in flight: each exchange below is
         // published by one set of waves and polled by another.
         if (wave >= kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // router rows these waves prefetched
-        if (l > a.l0 && wave >= kWaves / 2) {
+        double ss = 0.0;  // this thread's part of sum(x*x), for rms_norm
+        if (l == a.l0) {
+            for (int i = tid; i < n; i += kThreads) {
+                const float v = xs[i];
+                ss += (double)(v * v);
+            }
+        } else if (wave >= kWaves / 2) {
             // x of this layer: the XCD's 32 workgroups published 64 rows each; gathered
             // by waves 4-7 (wave 0 has just stored its combined rows)
             const uint64_t *xsrc = a.X + ((size_t)cur * kXcds + xcc) * n;
@@ -262,9 +268,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                     },
                     a.err);
                 if (!got) sh_fail = 1;
-                *reinterpret_cast<float4 *>(xs + i0) = make_float4(tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3]));
+                const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
+                *reinterpret_cast<float4 *>(xs + i0) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) ss += (double)(v[c] * v[c]);
             }
         }
+        ss = wave_sum_d(ss);
+        if (lane == 0) red_d[wave] = ss;
         lds_barrier();
         if (sh_fail) {
             ok = false;
@@ -273,16 +284,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 1);
 
         // -- P1: rms_norm scale, fx, router rows (32 lanes each) --
-        {
-            double ss = 0.0;
-            for (int i = tid; i < n; i += kThreads) {
-                const float v = xs[i];
-                ss += (double)(v * v);
-            }
-            ss = wave_sum_d(ss);
-            if (lane == 0) red_d[wave] = ss;
-        }
-        lds_barrier();
         {
             double tot = 0.0;
             for (int w = 0; w < kWaves; ++w) tot += red_d[w];
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 2);
         stamp(l, 3);
 
-        // -- P2: softmax (wave 2: waves 0-1 stored the logits), ranks (all threads), renorm (wave 2) --
+        // -- P2: softmax (wave 2: waves 0-1 stored the logits), ranks (all threads) --
         if (wave == kTopkWave) {
             uint64_t w0 = 0, w1 = 0;
             const bool got = poll(
@@ -380,36 +381,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             }
         }
         lds_barrier();
-        if (wave == kTopkWave) {
-            // every lane forms the same left-to-right sum; lane j normalises weight j
-            int sv[kDecodeK];
-            float wv[kDecodeK];
-#pragma unroll
-            for (int j = 0; j < kDecodeK; ++j) {
-                sv[j] = sel_s[j];
-                wv[j] = w_s[j];
-            }
-            float ws = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kDecodeK; ++j)
-                ws = ws + ((sv[j] < 0 || sv[j] >= E) ? __builtin_nanf("") : wv[j]);  // NaN logits only
-            int sj = lane < k ? sel_s[lane] : 0;
-            float wj = lane < k ? w_s[lane] : 0.0f;
-            if (sj < 0 || sj >= E) {
-                sj = 0;
-                wj = __builtin_nanf("");
-            }
-            if (a.renorm) {
-                if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
-                wj = wj / ws;
-            }
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads above precede the writes
-            if (lane < k) {
-                sel_s[lane] = sj;
-                w_s[lane] = wj;
-            }
-        }
-        lds_barrier();
         if (sh_fail) {
             ok = false;
             break;
@@ -417,7 +388,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         stamp(l, 4);
 
         // -- P3: waves 0-3 stream the gate/up rows into LDS (waves 6-7 the down rows, in P4) --
-        const int e = has_expert ? sel_s[xcc] : 0;
+        int e = has_expert ? sel_s[xcc] : 0;
+        if (e < 0 || e >= E) e = 0;  // only with NaN logits; their weights poison the output
         constexpr size_t rbg = (size_t)NB * QType<TGU>::bytes, rbu = rbg;
         constexpr size_t rbd = (size_t)NBH * QType<TD>::bytes;
         constexpr int kR = NBH * QK / kPerXcd, kRD = kEmbd / kPerXcd;  // rows per workgroup
@@ -440,6 +412,31 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         }
         // Q8_K(fx) while the rows are in flight
         for (int b = wave; b < nb; b += kWaves) wave_quantize_q8l(fxs + b * QK, &q8x[b]);
+        if (wave == 0) {
+            // renormalise the weights (only the combine, on this wave, reads them): every
+            // lane forms the same left-to-right sum; lane j normalises weight j
+            int sv[kDecodeK];
+            float wv[kDecodeK];
+#pragma unroll
+            for (int j = 0; j < kDecodeK; ++j) {
+                sv[j] = sel_s[j];
+                wv[j] = w_s[j];
+            }
+            float ws = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDecodeK; ++j)
+                ws = ws + ((sv[j] < 0 || sv[j] >= E) ? __builtin_nanf("") : wv[j]);  // NaN logits only
+            float wj = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kDecodeK; ++j)
+                if (lane == j) wj = (sv[j] < 0 || sv[j] >= E) ? __builtin_nanf("") : wv[j];
+            if (a.renorm) {
+                if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+                wj = wj / ws;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads above precede the writes
+            if (lane < k) w_s[lane] = wj;
+        }
         stamp(l, 5);
 
         if (has_expert) {
