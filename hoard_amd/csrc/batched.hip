@@ -18,6 +18,7 @@
 // (8 int8 of row l % 16) and B[8 (l / 16) .. +7][l % 16] (8 int8 of token
 // column l % 16), and receives D[4 (l / 16) + i][l % 16], i = 0..3.
 #include "kernels.h"
+#include "lds_dma.h"
 #include "qblocks.h"
 #include "rowdot.h"
 
@@ -29,6 +30,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;                   // weight rows per MFMA tile
 constexpr int kMaxTok = kBatchedMaxTokens;  // token columns per MFMA tile
+constexpr int kMfmaMinTokens = 12;          // smallest expert group computed on MFMA
+constexpr int kXChunk = 4;                  // tokens of Q8_K x staged in LDS at a time
 constexpr int kMaxExperts = 1024;
 static_assert(sizeof(Q8L) == kQ8LBytes, "Q8_K block size shared with the host");
 
@@ -46,76 +49,89 @@ __device__ __forceinline__ long hi_nibbles(uint2 w) {
     return (long)(((unsigned long)((w.y >> 4) & 0x0f0f0f0fu) << 32) | ((w.x >> 4) & 0x0f0f0f0fu));
 }
 
-// Q4_K sub-block scale and min for sub-block s from a super-block header.
-__device__ __forceinline__ void q4k_sm(const uint4 &hd, int s, int &sc, int &mn) {
-    const uint32_t sw[3] = {hd.y, hd.z, hd.w};
-    auto byte = [&](int i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
-    if (s < 4) {
-        sc = byte(s) & 63;
-        mn = byte(s + 4) & 63;
-    } else {
-        sc = (byte(s + 4) & 0x0f) | ((byte(s - 4) >> 6) << 4);
-        mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+// Operands of one super-block for one lane: its row's quants for the four
+// 64-element chunks, the headers of the four rows whose results it receives,
+// and its token's Q8_K quants, 16-element sums and scale.
+struct Q4Ops {
+    uint2 qa[4];
+    uint4 hd[4];
+    long xb[8];
+    uint4 b0, b1;
+    float xd;
+};
+
+// Rows of a tile of fewer than 16 rows repeat (row index & RM); the repeated
+// rows' results are not used.
+template <int RM>
+__device__ __forceinline__ void q4_load(const uint8_t *W, size_t rb, const Q8L *xq, int b, Q4Ops &o) {
+    const int lane = threadIdx.x & 63, r = lane & 15 & RM, q = lane >> 4;
+    const uint8_t *blk_r = W + (size_t)r * rb + (size_t)b * kQ4KBytes;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) o.qa[jc] = *reinterpret_cast<const uint2 *>(blk_r + 16 + 32 * jc + 8 * q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o.hd[i] = *reinterpret_cast<const uint4 *>(W + (size_t)((4 * q + i) & RM) * rb + (size_t)b * kQ4KBytes);
+    const Q8L &x = xq[b];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) o.xb[s] = *reinterpret_cast<const long *>(&x.qs[8 * s + 2 * q]);
+    o.b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
+    o.b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
+    o.xd = x.d;
+}
+
+// The 6-bit scales (sc) and mins (mn) of a Q4_K header, four per word: byte
+// s of sc[0] / mn[0] belongs to sub-block s, byte s of sc[1] / mn[1] to s + 4.
+__device__ __forceinline__ void q4k_scales_packed(const uint4 &hd, uint32_t sc[2], uint32_t mn[2]) {
+    sc[0] = hd.y & 0x3f3f3f3fu;
+    mn[0] = hd.z & 0x3f3f3f3fu;
+    sc[1] = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+    mn[1] = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
+
+__device__ __forceinline__ void q4_compute(const Q4Ops &o, float acc[4], float accm[4]) {
+    const uint32_t bw[8] = {o.b0.x, o.b0.y, o.b0.z, o.b0.w, o.b1.x, o.b1.y, o.b1.z, o.b1.w};
+    int bs[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) bs[s] = (int)(int16_t)(bw[s] & 0xffffu) + (int)(int16_t)(bw[s] >> 16);
+    uint32_t sc[4][2], mn[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q4k_scales_packed(o.hd[i], sc[i], mn[i]);
+    int isum[4] = {0, 0, 0, 0}, msum[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const long a = (s & 1) ? hi_nibbles(o.qa[s >> 1]) : lo_nibbles(o.qa[s >> 1]);
+        const v4i d = mfma_16x16x32(a, o.xb[s]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            isum[i] += byte_of(sc[i][s >> 2], s & 3) * d[i];
+            msum[i] += byte_of(mn[i][s >> 2], s & 3) * bs[s];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float dd = half_bits_to_float(o.hd[i].x & 0xffffu) * o.xd;
+        const float dm = half_bits_to_float(o.hd[i].x >> 16) * o.xd;
+        acc[i] = acc[i] + dd * (float)isum[i];
+        accm[i] = accm[i] + dm * (float)msum[i];
     }
 }
 
-// One 16-row Q4_K tile (row r at W + r*rb, NBLK super-blocks) against the
-// lane's token column.  xq: the token's Q8_K blocks, or null for an empty
-// column.  Returns, for rows 4(l/16)+i, acc_i - accm_i as the per-token path
-// forms them.
-template <int NBLK>
+// One 16-row Q4_K tile (row r at W + r*rb, NBLK super-blocks; with RM = 7 an
+// 8-row tile, rows 8-15 repeating rows 0-7) against the lane's token column.
+// xq: the token's Q8_K blocks; a column without a token reads another
+// column's token and its results are not used (the MFMA's output columns are
+// independent), which keeps the loads free of divergent branches.  Returns,
+// for rows 4(l/16)+i, acc_i - accm_i as the per-token path forms them.
+template <int NBLK, int RM = 15>
 __device__ __forceinline__ void tile_q4k(const uint8_t *W, size_t rb, const Q8L *xq, float out[4]) {
-    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 1
     for (int b = 0; b < NBLK; ++b) {
-        const uint8_t *blk_r = W + (size_t)r * rb + (size_t)b * kQ4KBytes;
-        uint2 qa[4];
-#pragma unroll
-        for (int jc = 0; jc < 4; ++jc) qa[jc] = *reinterpret_cast<const uint2 *>(blk_r + 16 + 32 * jc + 8 * q);
-        uint4 hd[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) hd[i] = *reinterpret_cast<const uint4 *>(W + (size_t)(4 * q + i) * rb + (size_t)b * kQ4KBytes);
-        long xb[8];
-        int bs[8];
-        float xd = 0.0f;
-        if (xq) {
-            const Q8L &x = xq[b];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) xb[s] = *reinterpret_cast<const long *>(&x.qs[8 * s + 2 * q]);
-            const uint4 b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
-            const uint4 b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
-            const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) bs[s] = (int)(int16_t)(w[s] & 0xffffu) + (int)(int16_t)(w[s] >> 16);
-            xd = x.d;
-        } else {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                xb[s] = 0;
-                bs[s] = 0;
-            }
-        }
-        int isum[4] = {0, 0, 0, 0}, msum[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const long a = (s & 1) ? hi_nibbles(qa[s >> 1]) : lo_nibbles(qa[s >> 1]);
-            const v4i d = mfma_16x16x32(a, xb[s]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int sc, mn;
-                q4k_sm(hd[i], s, sc, mn);
-                isum[i] += sc * d[i];
-                msum[i] += mn * bs[s];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float dd = half_bits_to_float(hd[i].x & 0xffffu) * xd;
-            const float dm = half_bits_to_float(hd[i].x >> 16) * xd;
-            acc[i] = acc[i] + dd * (float)isum[i];
-            accm[i] = accm[i] + dm * (float)msum[i];
-        }
+        Q4Ops o;
+        q4_load<RM>(W, rb, xq, b, o);
+        q4_compute(o, acc, accm);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) out[i] = acc[i] - accm[i];
@@ -123,11 +139,29 @@ __device__ __forceinline__ void tile_q4k(const uint8_t *W, size_t rb, const Q8L 
 
 // 8 bytes at a 2-byte aligned LDS address.
 __device__ __forceinline__ uint2 lds_u64_a2(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3u);
+    // aligned base by pointer arithmetic, so that the compiler still sees an
+    // LDS pointer and emits ds_read rather than flat loads
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);
     const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
     return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
+}
+
+// A token's Q8_K operands of one super-block for one lane (see q4_load).
+struct Q6X {
+    long xb[8];
+    uint4 b0, b1;
+    float xd;
+};
+
+__device__ __forceinline__ void q6_load_x(const Q8L *xq, int b, Q6X &o) {
+    const int q = (threadIdx.x & 63) >> 4;
+    const Q8L &x = xq[b];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) o.xb[s] = *reinterpret_cast<const long *>(&x.qs[8 * s + 2 * q]);
+    o.b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
+    o.b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
+    o.xd = x.d;
 }
 
 // One 16-row Q6_K tile staged in LDS (row r at T + r*rb).  Element e of a
@@ -142,22 +176,15 @@ __device__ __forceinline__ void tile_q6k(const uint8_t *T, size_t rb, const Q8L 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 1
     for (int b = 0; b < NBLK; ++b) {
+        Q6X cur;
+        q6_load_x(xq, b, cur);
         const uint8_t *blk_r = T + (size_t)r * rb + (size_t)b * kQ6KBytes;
+        const uint32_t w[8] = {cur.b0.x, cur.b0.y, cur.b0.z, cur.b0.w, cur.b1.x, cur.b1.y, cur.b1.z, cur.b1.w};
         int bs[16];
-        float xd = 0.0f;
-        if (xq) {
-            const uint4 b0 = *reinterpret_cast<const uint4 *>(&xq[b].bsums[0]);
-            const uint4 b1 = *reinterpret_cast<const uint4 *>(&xq[b].bsums[8]);
-            const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                bs[2 * g] = (int)(int16_t)(w[g] & 0xffffu);
-                bs[2 * g + 1] = (int)(int16_t)(w[g] >> 16);
-            }
-            xd = xq[b].d;
-        } else {
-#pragma unroll
-            for (int g = 0; g < 16; ++g) bs[g] = 0;
+        for (int g = 0; g < 8; ++g) {
+            bs[2 * g] = (int)(int16_t)(w[g] & 0xffffu);
+            bs[2 * g + 1] = (int)(int16_t)(w[g] >> 16);
         }
         int isum[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -169,9 +196,8 @@ __device__ __forceinline__ void tile_q6k(const uint8_t *T, size_t rb, const Q8L 
             const uint32_t v0 = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
             const uint32_t v1 = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
             const long a = (long)(((unsigned long)v1 << 32) | v0);
-            const long xb = xq ? *reinterpret_cast<const long *>(&xq[b].qs[8 * s + 2 * q]) : 0;
-            const v4i d0 = mfma_16x16x32(first_half ? a : 0, xb);
-            const v4i d1 = mfma_16x16x32(first_half ? 0 : a, xb);
+            const v4i d0 = mfma_16x16x32(first_half ? a : 0, cur.xb[s]);
+            const v4i d1 = mfma_16x16x32(first_half ? 0 : a, cur.xb[s]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint8_t *blk_i = T + (size_t)(4 * q + i) * rb + (size_t)b * kQ6KBytes;
@@ -183,7 +209,7 @@ __device__ __forceinline__ void tile_q6k(const uint8_t *T, size_t rb, const Q8L 
         for (int i = 0; i < 4; ++i) {
             const uint8_t *blk_i = T + (size_t)(4 * q + i) * rb + (size_t)b * kQ6KBytes;
             const uint32_t dbits = (uint32_t)blk_i[208] | ((uint32_t)blk_i[209] << 8);
-            acc[i] = acc[i] + (half_bits_to_float(dbits) * xd) * (float)isum[i];
+            acc[i] = acc[i] + (half_bits_to_float(dbits) * cur.xd) * (float)isum[i];
         }
     }
 #pragma unroll
@@ -247,30 +273,101 @@ __global__ __launch_bounds__(64) void prep_kernel(BatchedArgs a) {
     if (lane == 0) a.n_unique[0] = wave_total;
 }
 
-// -- gate/up: one 16-row tile of gate (wave 0) and up (wave 1) of one expert --
-template <int NB>
-__global__ __launch_bounds__(128) void gateup_mfma_kernel(BatchedArgs a) {
-    const int u = blockIdx.y;
-    if (u >= a.n_unique[0]) return;
-    __shared__ float gu[2][kTile][kMaxTok];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = a.uexp[u], m = min(a.ucount[u], kMaxTok);
-    const int row0 = blockIdx.x * kTile;
-    const size_t rb = (size_t)NB * kQ4KBytes;
-    const uint8_t *W = (wave ? a.up + (size_t)e * a.ustride : a.gate + (size_t)e * a.gstride) + (size_t)row0 * rb;
-    const int c = lane & 15;
-    const Q8L *xq = c < m ? q8(a.q8x) + (size_t)a.utok[u * kMaxTok + c] * NB : nullptr;
-    float v[4];
-    tile_q4k<NB>(W, rb, xq, v);
+// Expert groups are computed two ways.  A group of fewer than kMfmaMinTokens
+// tokens runs token by token with the per-token row dot, whose cost grows with
+// the group; a larger group runs on MFMA, whose cost is that of 16 token
+// columns whatever the group's size.  Both give the per-token path's bits.
+// Weight tiles are contiguous rows of the expert and are copied into LDS in
+// one burst.
+
+// A group's expert and size are read together with the group count (u < the
+// grid's umax keeps them in bounds): one latency rather than two.  Testing them
+// too keeps the compiler from moving their loads after the test (a group
+// always has an expert >= 0 and a token).
+__device__ __forceinline__ bool load_group(const BatchedArgs &a, int u, int &e, int &m) {
+    const int nu = a.n_unique[0];
+    e = a.uexp[u];
+    m = min(a.ucount[u], kMaxTok);
+    return (u < nu) & (e >= 0) & (m >= 1);
+}
+
+// Gather the Q8_K rows (nb blocks each) of tokens tok[c0 .. c0+mc) into LDS at
+// xs, 16-byte granules spread over the workgroup's nw waves (issued, not
+// waited for).
+template <int NBX>
+__device__ __forceinline__ void gather_tokens(uint8_t *xs, const uint8_t *q8base, const int *tok, int c0, int mc,
+                                              int m, int wave, int nw) {
+    constexpr int kTokGran = NBX * (int)sizeof(Q8L) / 16;
+    int tk[kXChunk];  // uniform indices: scalar loads
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gu[wave][4 * (lane >> 4) + i][c] = v[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < kTile * kMaxTok; i += blockDim.x) {
-        const int r = i / kMaxTok, cc = i % kMaxTok;
-        if (cc < m) {
-            const float g = gu[0][r][cc], uu = gu[1][r][cc];
-            a.hbuf[((size_t)u * kMaxTok + cc) * a.n_ff + row0 + r] = g / (1.0f + expf(-g)) * uu;
+    for (int i = 0; i < kXChunk; ++i) tk[i] = tok[min(c0 + i, m - 1)];
+    const int lane = threadIdx.x & 63, ng = mc * kTokGran;
+    for (int k = wave; 64 * k < ng; k += nw) {
+        const int p = 64 * k + lane;
+        if (p < ng) {
+            const int t = p / kTokGran, o = p - t * kTokGran;
+            int tt = tk[0];
+#pragma unroll
+            for (int i = 1; i < kXChunk; ++i) tt = t == i ? tk[i] : tt;
+            dma_lanes(xs + 1024 * k, q8base + (size_t)tt * (NBX * sizeof(Q8L)) + 16 * o);
         }
+    }
+}
+
+// -- gate/up: 8 rows of gate (wave 0) and up (wave 1) of one expert ----------
+// Per-token dot: one 8-lane group per row, lane t holding the token's Q8_K
+// block t.  MFMA: the 8 rows fill a 16-row tile twice.
+template <int NB>
+__global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
+    static_assert(NB == 8, "one 8-lane group per row, one lane per super-block");
+    constexpr int kRows = 8;
+    constexpr int kRowBytes = NB * kQ4KBytes;
+    constexpr int kTileBytes = kRows * kRowBytes;
+    const int u = blockIdx.y;
+    int e, m;
+    if (!load_group(a, u, e, m)) return;
+    __shared__ __align__(16) uint8_t wt[2][kTileBytes];
+    __shared__ __align__(16) uint8_t xs[kXChunk * NB * sizeof(Q8L)];
+    __shared__ float gu[2][kRows][kMaxTok];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
+    const int row0 = blockIdx.x * kRows;
+    const int *tok = a.utok + u * kMaxTok;
+    const uint8_t *W = (wave ? a.up + (size_t)e * a.ustride : a.gate + (size_t)e * a.gstride) + (size_t)row0 * kRowBytes;
+    if (m >= kMfmaMinTokens) {
+        dma_wave_copy(wt[wave], W, kTileBytes);
+        const int c = lane & 15;
+        const Q8L *xq = q8(a.q8x) + (size_t)tok[c < m ? c : 0] * NB;
+        lds_dma_wait();
+        float v[4];
+        tile_q4k<NB, 7>(wt[wave], kRowBytes, xq, v);
+        if (lane < 32) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gu[wave][4 * (lane >> 4) + i][c] = v[i];
+        }
+    } else {
+        // x goes into LDS with the tile, kXChunk tokens at a time: a vector
+        // load issued during the compute would queue behind the tile copies
+        // of the other workgroups on this CU
+        const Q8L *xl = reinterpret_cast<const Q8L *>(xs);
+        for (int c0 = 0; c0 < m; c0 += kXChunk) {
+            const int mc = min(m - c0, kXChunk);
+            if (c0 > 0) __syncthreads();  // both waves are done with the previous chunk
+            gather_tokens<NB>(xs, a.q8x, tok, c0, mc, m, wave, 2);
+            if (c0 == 0) dma_wave_copy(wt[wave], W, kTileBytes);
+            lds_dma_wait();
+            __syncthreads();
+#pragma unroll 1
+            for (int c = 0; c < mc; ++c) {
+                const float v = lpb_row_q4k_mem<NB>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
+                if (t8 == NB - 1) gu[wave][grp][c0 + c] = v;
+            }
+        }
+    }
+    __syncthreads();
+    const int r = threadIdx.x / kMaxTok, cc = threadIdx.x % kMaxTok;  // 128 threads: 8 rows x 16 columns
+    if (cc < m) {
+        const float g = gu[0][r][cc], uu = gu[1][r][cc];
+        a.hbuf[((size_t)u * kMaxTok + cc) * a.n_ff + row0 + r] = g / (1.0f + expf(-g)) * uu;
     }
 }
 
@@ -284,36 +381,66 @@ __global__ __launch_bounds__(64) void quant_h_kernel(BatchedArgs a) {
 }
 
 // -- down: one 16-row tile of one expert; y to Y[token][slot] -------------------
+// Q6_K rows are only 2-byte aligned, which LDS reads handle with alignbyte;
+// the per-token Q6_K dot wants one alignment per wave, so each pass takes the
+// rows of one parity (the row size is 2 mod 4).
 template <int TD, int NBH>
-__global__ __launch_bounds__(64) void down_mfma_kernel(BatchedArgs a) {
+__global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
+    constexpr int kRowBytes = NBH * (TD == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
+    constexpr int kTileBytes = kTile * kRowBytes;
     const int u = blockIdx.y;
-    if (u >= a.n_unique[0]) return;
-    const int lane = threadIdx.x & 63, c = lane & 15;
-    const int e = a.uexp[u], m = min(a.ucount[u], kMaxTok);
+    int e, m;
+    if (!load_group(a, u, e, m)) return;
+    __shared__ __align__(16) uint8_t tile[kTileBytes];
+    __shared__ __align__(16) uint8_t xs[kXChunk * NBH * sizeof(Q8L)];
+    const int lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kTile;
-    const Q8L *xq = c < m ? q8(a.q8h) + ((size_t)u * kMaxTok + c) * NBH : nullptr;
-    float v[4];
-    if constexpr (TD == kTypeQ4K) {
-        const size_t rb = (size_t)NBH * kQ4KBytes;
-        tile_q4k<NBH>(a.down + (size_t)e * a.dstride + (size_t)row0 * rb, rb, xq, v);
-    } else {
-        // stage the tile's 16 rows (contiguous in the expert) in LDS: Q6_K rows
-        // are only 2-byte aligned, which LDS reads handle with alignbyte
-        constexpr size_t rb = (size_t)NBH * kQ6KBytes;
-        constexpr int kBytes = (int)(kTile * rb);
-        __shared__ __align__(16) uint8_t tile[kBytes + 16];
-        const uint8_t *src = a.down + (size_t)e * a.dstride + (size_t)row0 * rb;
-        for (int i = lane; i < kBytes / 16; i += 64)
-            reinterpret_cast<uint4 *>(tile)[i] = reinterpret_cast<const uint4 *>(src)[i];
-        for (int i = (kBytes / 16) * 16 + lane; i < kBytes; i += 64) tile[i] = src[i];
-        __syncthreads();
-        tile_q6k<NBH>(tile, rb, xq, v);
-    }
-    if (c < m) {
-        const int t = a.utok[u * kMaxTok + c], j = a.uslot[u * kMaxTok + c];
-        float *y = a.ybuf + ((size_t)t * a.k + j) * a.n_embd + row0;
+    const int *tok = a.utok + u * kMaxTok, *slot = a.uslot + u * kMaxTok;
+    const uint8_t *src = a.down + (size_t)e * a.dstride + (size_t)row0 * kRowBytes;
+    if (m >= kMfmaMinTokens) {
+        dma_wave_copy(tile, src, kTileBytes);
+        const int c = lane & 15;
+        const Q8L *xq = q8(a.q8h) + ((size_t)u * kMaxTok + (c < m ? c : 0)) * NBH;
+        lds_dma_wait();
+        float v[4];
+        if constexpr (TD == kTypeQ4K)
+            tile_q4k<NBH>(tile, kRowBytes, xq, v);
+        else
+            tile_q6k<NBH>(tile, kRowBytes, xq, v);
+        if (c < m) {
+            float *y = a.ybuf + ((size_t)tok[c] * a.k + slot[c]) * a.n_embd + row0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[4 * (lane >> 4) + i] = v[i];
+            for (int i = 0; i < 4; ++i) y[4 * (lane >> 4) + i] = v[i];
+        }
+        return;
+    }
+    const Q8L *xl = reinterpret_cast<const Q8L *>(xs);
+    for (int c0 = 0; c0 < m; c0 += kXChunk) {
+        const int mc = min(m - c0, kXChunk);
+        // the group's Q8_K h rows are contiguous, token-major
+        dma_wave_copy(xs, a.q8h + ((size_t)u * kMaxTok + c0) * NBH * sizeof(Q8L), mc * NBH * (int)sizeof(Q8L));
+        if (c0 == 0) dma_wave_copy(tile, src, kTileBytes);
+        lds_dma_wait();
+#pragma unroll 1
+        for (int c = 0; c < mc; ++c) {
+            float *y = a.ybuf + ((size_t)tok[c0 + c] * a.k + slot[c0 + c]) * a.n_embd + row0;
+            if constexpr (TD == kTypeQ6K) {
+#pragma unroll 1
+                for (int p = 0; p < 2; ++p) {
+                    const int row = 2 * grp + p;
+                    const float v = g8_row_q6k_u<NBH>(tile + row * kRowBytes, xl + c * NBH, t8);
+                    if (t8 == 0) y[row] = v;
+                }
+            } else {
+#pragma unroll 1
+                for (int p = 0; p < 2; ++p) {
+                    const int row = 8 * p + grp;
+                    const float v = lpb_row_q4k_mem<NBH>(tile + row * kRowBytes, xl[c * NBH + min(t8, NBH - 1)], t8);
+                    if (t8 == NBH - 1) y[row] = v;
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's LDS reads precede the next copy
     }
 }
 
@@ -340,12 +467,12 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     const int nb = a.n_embd / QK, nbh = a.n_ff / QK;
     const int umax = a.E < a.M * a.k ? a.E : a.M * a.k;
     hipLaunchKernelGGL(prep_kernel, dim3(a.M * nb + 1), dim3(64), 0, s, a);
-    hipLaunchKernelGGL(gateup_mfma_kernel<8>, dim3(a.n_ff / kTile, umax), dim3(128), 0, s, a);
+    hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, kMaxTok, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
-#define HOARD_DOWN(T, N)                                                              \
-    if (a.d_type == T && nbh == N) {                                                  \
-        hipLaunchKernelGGL((down_mfma_kernel<T, N>), dg, dim3(64), 0, s, a);          \
+#define HOARD_DOWN(T, N)                                                  \
+    if (a.d_type == T && nbh == N) {                                      \
+        hipLaunchKernelGGL((down_kernel<T, N>), dg, dim3(64), 0, s, a);    \
     } else
     HOARD_DOWN(kTypeQ6K, 3) HOARD_DOWN(kTypeQ6K, 2) HOARD_DOWN(kTypeQ6K, 4) HOARD_DOWN(kTypeQ4K, 4)
     HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }

@@ -22,6 +22,7 @@
 // (L2-bypassing) loads and stores.  Every wait is bounded by a wall-clock
 // timeout that raises an error flag and poisons the output instead of hanging.
 #include "kernels.h"
+#include "lds_dma.h"
 #include "qblocks.h"
 #include "rowdot.h"
 #include "wave.h"
@@ -29,8 +30,6 @@
 namespace hoard {
 
 namespace {
-
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
@@ -68,7 +67,6 @@ __device__ __forceinline__ bool reached(unsigned v, unsigned target) { return (i
 // 1 KB chunks (64 lanes x 16 B) spread over waves [w0, w0+nw).  Rounds the
 // source down to 16 bytes (returned offset) and reads whole chunks, i.e. up to
 // 1 KB + 15 bytes past the end, which device allocations keep as padding.
-__device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src);
 __device__ __forceinline__ int issue_lds_copy(uint8_t *dst, const uint8_t *src, size_t nbytes, int w0, int nw) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(src);
     const uintptr_t a0 = a & ~(uintptr_t)15;
@@ -80,20 +78,6 @@ __device__ __forceinline__ int issue_lds_copy(uint8_t *dst, const uint8_t *src, 
             dma_chunk(dst + c * 1024, reinterpret_cast<const uint8_t *>(a0) + (size_t)c * 1024);
     }
     return off;
-}
-
-// One 1 KB chunk (64 lanes x 16 bytes) from global memory into LDS, issued
-// from inline assembly: the compiler then does not know the wave has LDS DMA
-// in flight and does not make its next LDS read wait for it.  Every wave that
-// issues chunks waits for them itself (s_waitcnt vmcnt) before the barrier
-// after which other waves read them.
-__device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src) {
-    const int lane = threadIdx.x & 63;
-    const lds_void *lp = (const lds_void *)dst;  // generic -> LDS address space: the 32-bit LDS offset
-    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lp);
-    const uint8_t *g = src + lane * 16;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
-                 : "memory", "m0");
 }
 
 __host__ __device__ __forceinline__ size_t chunk_region(size_t nbytes) { return ((nbytes + 15 + 1023) >> 10) << 10; }

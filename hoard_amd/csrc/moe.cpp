@@ -754,6 +754,10 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
+    // the weight tiles are copied to LDS in 16-byte units
+    if (((uintptr_t)L.gate | (uintptr_t)L.up | (uintptr_t)L.down | (uintptr_t)L.gstride | (uintptr_t)L.ustride |
+         (uintptr_t)L.dstride) & 15)
+        return fail(HOARD_ERR_UNSUPPORTED, "batched path: expert matrices must be 16-byte aligned");
     const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
     const int umax = std::min(c.n_expert, T * c.n_used);
     const int nb = c.n_embd / 256, nbh = c.n_ff / 256;

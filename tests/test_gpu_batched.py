@@ -53,6 +53,29 @@ def test_batched_matches_single_token_and_oracle(orc, stage, M):
     assert stats.last_unique == int((counts > 0).sum())
 
 
+@pytest.mark.parametrize("M", [11, 12, 16])
+def test_batched_large_expert_groups(orc, stage, M):
+    """M copies of one token's fx (each with its own residual) put all M tokens
+    in each of its k expert groups: 11 runs the per-token dot path at its
+    largest group, 12 and 16 the MFMA path."""
+    shape, hl, st = stage
+    fx1, _ = _tokens(shape, 1, 700 + M)
+    _, res = _tokens(shape, M, 800 + M)
+    fx = np.repeat(fx1, M, axis=0)
+    print(f"batched {shape.name} one token x M={M}", flush=True)
+    out, sel, w = st.forward_batched(0, fx, res)
+    stats = st.stats()
+    assert stats.last_unique == shape.n_used
+    assert sorted(set(np.array(stats.expert_hist[:shape.n_expert]).tolist())) == [0, M]
+    ref, sel_o, _ = orc.moe_layer_batched(hl, fx, res)
+    assert np.array_equal(sel, sel_o)
+    for t in (0, M // 2, M - 1):
+        o1, s1, _ = st.layer(0, fx[t], res[t])
+        assert np.array_equal(s1, sel[t])
+        assert np.array_equal(o1.view(np.uint32), out[t].view(np.uint32)), f"token {t}"
+        parity.assert_parity(out[t], ref[t], f"batched {shape.name} M={M} token {t}")
+
+
 def test_batched_aliasing_and_repeated_tokens(stage):
     """out may alias res; identical tokens in one call give identical rows."""
     shape, _, st = stage
