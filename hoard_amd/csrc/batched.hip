@@ -21,6 +21,7 @@
 #include "lds_dma.h"
 #include "qblocks.h"
 #include "rowdot.h"
+#include "router_tail.h"
 
 namespace hoard {
 
@@ -216,61 +217,140 @@ __device__ __forceinline__ void tile_q6k(const uint8_t *T, size_t rb, const Q8L 
     for (int i = 0; i < 4; ++i) out[i] = acc[i];
 }
 
-// -- prep: Q8_K of every token's fx; grouping of (token, slot) by expert -----
-__global__ __launch_bounds__(64) void prep_kernel(BatchedArgs a) {
-    const int nb = a.n_embd / QK;
-    if ((int)blockIdx.x < a.M * nb) {
-        const int t = blockIdx.x / nb, b = blockIdx.x % nb;
-        wave_quantize_q8l(a.fx + (size_t)t * a.n_embd + (size_t)b * QK, q8(a.q8x) + (size_t)t * nb + b);
-        return;
-    }
-    // last workgroup: group the (token, slot) pairs by expert.  A token selects
-    // an expert at most once, so a per-expert bitmask of tokens orders each
-    // group by token; groups are numbered in ascending expert id.
+// -- route: router logits, softmax / top-k, Q8_K of fx, grouping by expert ----
+// One launch replaces the router kernels and the grouping pass.  A workgroup
+// (4 waves) takes kRouteRows router rows against kRouteTok tokens, a wave per
+// token and a half-wave per row, with the single-token router's per-row
+// accumulation order
+// (lane l of 32 owns elements l, l+32, ...; ggml's f32 dot fold).  The last
+// workgroup of a token group (device-scope counter) runs the tails of its
+// tokens; the last token group's tail workgroup then groups the (token, slot)
+// pairs by expert.  Waves with a spare slot quantise fx to Q8_K.
+constexpr int kRouteRows = 2;
+constexpr int kRouteTok = 4;
+constexpr int kRouteN = 2048;  // n_embd of the batched path
+
+// Group the (token, slot) pairs by expert (all threads of the workgroup call
+// this).  A token selects an expert at most once, so a per-expert bitmask of
+// tokens orders each group by token; groups are numbered in ascending expert
+// id.
+__device__ void group_by_expert(const BatchedArgs &a) {
     __shared__ unsigned mask[kMaxExperts];
     __shared__ int uidx[kMaxExperts];
     __shared__ int wave_total;
-    const int lane = threadIdx.x, E = a.E, P = a.M * a.k;
-    for (int e = lane; e < E; e += 64) mask[e] = 0u;
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.E, P = a.M * a.k;
+    for (int e = tid; e < E; e += nt) mask[e] = 0u;
     __syncthreads();
-    for (int p = lane; p < P; p += 64) {
-        int e = a.sel[p];
-        if (e < 0 || e >= E) e = 0;  // the router maps NaN logits to expert 0 with a NaN weight
+    for (int p = tid; p < P; p += nt) {
+        int e = __hip_atomic_load(a.sel + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (e < 0 || e >= E) e = 0;  // out-of-range selections count as expert 0
         atomicOr(&mask[e], 1u << (p / a.k));
     }
     __syncthreads();
-    // ascending prefix count of used experts: lane owns a contiguous run of experts
-    const int per = (E + 63) / 64, e0 = lane * per;
-    int cnt = 0;
-    for (int e = e0; e < e0 + per && e < E; ++e) cnt += mask[e] ? 1 : 0;
-    int incl = cnt;
+    if (tid < 64) {
+        // ascending prefix count of used experts: lane owns a contiguous run of experts
+        const int lane = tid, per = (E + 63) / 64, e0 = lane * per;
+        int cnt = 0;
+        for (int e = e0; e < e0 + per && e < E; ++e) cnt += mask[e] ? 1 : 0;
+        int incl = cnt;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int o = __shfl_up(incl, off);
-        if (lane >= off) incl += o;
-    }
-    int u = incl - cnt;
-    for (int e = e0; e < e0 + per && e < E; ++e) {
-        const unsigned m = mask[e];
-        a.hist[e] = (unsigned)__popc(m);
-        if (m) {
-            uidx[e] = u;
-            a.uexp[u] = e;
-            a.ucount[u] = __popc(m);
-            ++u;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off);
+            if (lane >= off) incl += o;
         }
+        int u = incl - cnt;
+        for (int e = e0; e < e0 + per && e < E; ++e) {
+            const unsigned m = mask[e];
+            a.hist[e] = (unsigned)__popc(m);
+            if (m) {
+                uidx[e] = u;
+                a.uexp[u] = e;
+                a.ucount[u] = __popc(m);
+                ++u;
+            }
+        }
+        if (lane == 63) wave_total = incl;
     }
-    if (lane == 63) wave_total = incl;
     __syncthreads();
-    for (int p = lane; p < P; p += 64) {
+    for (int p = tid; p < P; p += nt) {
         const int t = p / a.k, j = p % a.k;
-        int e = a.sel[p];
+        int e = __hip_atomic_load(a.sel + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (e < 0 || e >= E) e = 0;
         const int g = uidx[e], c = __popc(mask[e] & ((1u << t) - 1u));
         a.utok[g * kMaxTok + c] = t;
         a.uslot[g * kMaxTok + c] = j;
     }
-    if (lane == 0) a.n_unique[0] = wave_total;
+    if (tid == 0) a.n_unique[0] = wave_total;
+}
+
+__global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
+    constexpr int n = kRouteN, nb = kRouteN / QK;
+    const int E = a.E;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
+    const int tg = blockIdx.y;
+    const int t = tg * kRouteTok + wave;  // this wave's token; its half-waves take one row each
+    const int r0 = blockIdx.x * kRouteRows;
+    const int nrows = min(kRouteRows, E - r0);
+    // the workgroup's token rows and router rows go to LDS in one burst, so
+    // that every load is in flight at once; the dot then reads them in the
+    // per-lane order the accumulation needs
+    __shared__ __align__(16) float xl[kRouteTok][kRouteN];
+    __shared__ __align__(16) float wl[kRouteRows][kRouteN];
+    if (t < a.M) dma_wave_copy(reinterpret_cast<uint8_t *>(xl[wave]), reinterpret_cast<const uint8_t *>(a.fx + (size_t)t * n),
+                               n * (int)sizeof(float));
+    {
+        const int wbytes = nrows * n * (int)sizeof(float), per = wbytes / 4;  // a quarter per wave
+        dma_wave_copy(reinterpret_cast<uint8_t *>(wl[0]) + wave * per,
+                      reinterpret_cast<const uint8_t *>(a.router + (size_t)r0 * n) + wave * per, per);
+    }
+    lds_dma_wait();
+    __syncthreads();
+    const int row = r0 + (lane >> 5);
+    if (t < a.M) {
+        const float *x = xl[wave];
+        const float *wr = wl[min(lane >> 5, nrows - 1)];
+        float acc = 0.0f;
+#pragma unroll 16
+        for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l], acc);
+        acc = acc + __shfl_xor(acc, 16);
+        acc = acc + __shfl_xor(acc, 8);
+        acc = acc + __shfl_xor(acc, 4);
+        acc = acc + __shfl_xor(acc, 1);
+        acc = acc + __shfl_xor(acc, 2);
+        if (l == 0 && row < E)
+            __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Q8_K of fx: the first nb workgroups of a token group quantise block
+        // blockIdx.x of their tokens
+        if ((int)blockIdx.x < nb) wave_quantize_q8l(x + blockIdx.x * QK, q8(a.q8x) + (size_t)t * nb + blockIdx.x);
+    }
+    // Completion protocol without cache-flushing fences: the logits and the
+    // tails' sel / wsel are stored at device scope (through to memory, past
+    // the per-XCD L2) and read back at device scope; each wave waits for its
+    // stores to be acknowledged before its workgroup counts itself done.
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(&a.counters[tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int tt = wave; tt < kRouteTok; tt += 4) {
+        const int tok = tg * kRouteTok + tt;
+        if (tok < a.M) router_tail<true>(a.logits, E, a.k, a.renorm, a.sel, a.wsel, tok);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&a.counters[tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = __hip_atomic_fetch_add(&a.counters[kBatchedCounters - 1], 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    group_by_expert(a);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[kBatchedCounters - 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Expert groups are computed two ways.  A group of fewer than kMfmaMinTokens
@@ -466,7 +546,10 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (a.M < 1 || a.M > kMaxTok || a.n_embd != 2048 || a.gu_type != kTypeQ4K) return hipErrorInvalidValue;
     const int nb = a.n_embd / QK, nbh = a.n_ff / QK;
     const int umax = a.E < a.M * a.k ? a.E : a.M * a.k;
-    hipLaunchKernelGGL(prep_kernel, dim3(a.M * nb + 1), dim3(64), 0, s, a);
+    if ((a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1 || a.E > kMaxExperts || a.k > kMaxK)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(route_kernel, dim3((a.E + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
+                       dim3(256), 0, s, a);
     hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, kMaxTok, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);

@@ -71,8 +71,12 @@ struct BatchedArgs {
     const float *fx;        // [M][n_embd] normalised inputs
     const float *res;       // [M][n_embd]
     float *out;             // [M][n_embd] (may alias res)
-    const int32_t *sel;     // [M][k] from the router
-    const float *wsel;      // [M][k]
+    const float *router;    // [E][n_embd] f32 router weight
+    int renorm;             // renormalise the top-k weights
+    float *logits;          // [M][E] scratch
+    unsigned *counters;     // [kBatchedCounters], zero on entry, left zero on exit
+    int32_t *sel;           // [M][k] selected experts (written by the call)
+    float *wsel;            // [M][k] their weights
     const uint8_t *gate, *up, *down;
     size_t gstride, ustride, dstride;
     uint8_t *q8x;           // Q8_K(fx): [M][n_embd/256] blocks of 304 bytes
@@ -86,6 +90,7 @@ struct BatchedArgs {
     unsigned *hist;         // [E] tokens per expert in the call
 };
 constexpr int kBatchedMaxTokens = 16;
+constexpr int kBatchedCounters = 8;
 constexpr size_t kQ8LBytes = 304;
 hipError_t launch_batched(const BatchedArgs &a, hipStream_t s);
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);

@@ -114,6 +114,7 @@ struct hoard_moe {
     float *b_h = nullptr, *b_y = nullptr;
     int *b_ints = nullptr;          // n_unique, slot_of[E], uexp, ucount, utok, uslot
     unsigned *b_hist = nullptr;     // [E]
+    unsigned *b_counters = nullptr; // route kernel's completion counters
     bool hist_pending = false;      // a batched call ran since the histogram was last read
     size_t trace_layers = 0;
     bool tracing = false;
@@ -150,6 +151,7 @@ struct hoard_moe {
         hipFree(b_y);
         hipFree(b_ints);
         hipFree(b_hist);
+        hipFree(b_counters);
     }
     static void free_layer(Layer &L) {
         if (L.copied) hipEventDestroy(L.copied);
@@ -754,6 +756,7 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
+    if (((uintptr_t)fx_dev & 15) != 0) return fail(HOARD_ERR_INVALID, "fx must be 16-byte aligned");
     // the weight tiles are copied to LDS in 16-byte units
     if (((uintptr_t)L.gate | (uintptr_t)L.up | (uintptr_t)L.down | (uintptr_t)L.gstride | (uintptr_t)L.ustride |
          (uintptr_t)L.dstride) & 15)
@@ -769,28 +772,13 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
         rc = rc ? rc : dev_alloc((void **)&h->b_ints,
                                  sizeof(int) * (1 + c.n_expert + 2 * umax + 2 * umax * hoard::kBatchedMaxTokens));
         rc = rc ? rc : dev_alloc((void **)&h->b_hist, sizeof(unsigned) * c.n_expert);
+        rc = rc ? rc : dev_alloc((void **)&h->b_counters, sizeof(unsigned) * hoard::kBatchedCounters);
         if (rc) return rc;
+        HIP_TRY(hipMemset(h->b_counters, 0, sizeof(unsigned) * hoard::kBatchedCounters));
     }
     hipStream_t s = (hipStream_t)stream;
     int32_t *sel = sel_dev ? sel_dev : h->sel;
     float *w = w_dev ? w_dev : h->wsel;
-    hoard::RouterArgs ra{};
-    ra.xin = fx_dev;
-    ra.fx_out = h->fx;
-    ra.w = L.router;
-    ra.n = c.n_embd;
-    ra.E = c.n_expert;
-    ra.k = c.n_used;
-    ra.renorm = c.renorm;
-    ra.M = M;
-    ra.logits = h->logits;
-    ra.counters = h->counters;
-    ra.sel = sel;
-    ra.wsel = w;
-    {
-        KernelMark mark(h, HOARD_KERNEL_ROUTER, s);
-        HIP_TRY(hoard::launch_router(ra, s));
-    }
     hoard::BatchedArgs a{};
     a.M = M;
     a.n_embd = c.n_embd;
@@ -802,6 +790,10 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     a.fx = fx_dev;
     a.res = res_dev;
     a.out = out_dev;
+    a.router = L.router;
+    a.renorm = c.renorm;
+    a.logits = h->logits;
+    a.counters = h->b_counters;
     a.sel = sel;
     a.wsel = w;
     a.gate = L.gate;

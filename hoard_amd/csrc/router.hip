@@ -13,16 +13,13 @@
 // (device-scope counter) runs softmax / top-k on one wave.
 #include "kernels.h"
 #include "qblocks.h"
+#include "router_tail.h"
 
 namespace hoard {
 
 namespace {
 
-constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
-constexpr int kMaxK = 16;
 constexpr int kMaxRouterTokens = 16;    // tokens per call of the multi-token logits kernel
-
-__device__ void router_tail(const RouterArgs &a, int tok);
 
 __global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
     const int lane = threadIdx.x;
@@ -75,7 +72,7 @@ __global__ __launch_bounds__(64) void router_kernel(RouterArgs a) {
     __syncthreads();
     if (!is_last) return;
     __threadfence();
-    router_tail(a, tok);
+    router_tail(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, tok);
     if (lane == 0) a.counters[tok] = 0u;
 }
 
@@ -128,95 +125,8 @@ __global__ __launch_bounds__(256) void router_rows_m_kernel(RouterArgs a) {
 }
 
 // Softmax, top-k and renorm of one token per workgroup (M > 1).
-__global__ __launch_bounds__(64) void router_tail_kernel(RouterArgs a) { router_tail(a, blockIdx.x); }
-
-}  // namespace
-
-namespace {
-
-__device__ void router_tail(const RouterArgs &a, int tok) {
-    const int lane = threadIdx.x;
-    const int E = a.E;
-    const float *lg = a.logits + (size_t)tok * E;
-    float p[kMaxExpertsPerLane];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < kMaxExpertsPerLane; ++t) {
-        const int e = lane + 64 * t;
-        p[t] = e < E ? lg[e] : -INFINITY;
-        mx = p[t] > mx ? p[t] : mx;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(mx, off);
-        mx = o > mx ? o : mx;
-    }
-    // softmax: exp(l - max), sum in double, scale by (float)(1/sum)
-    double sum = 0.0;
-#pragma unroll
-    for (int t = 0; t < kMaxExpertsPerLane; ++t) {
-        const int e = lane + 64 * t;
-        if (e < E) {
-            p[t] = expf(p[t] - mx);
-            sum += (double)p[t];
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    const float sc = (float)(1.0 / sum);
-#pragma unroll
-    for (int t = 0; t < kMaxExpertsPerLane; ++t) p[t] = p[t] * sc;
-
-    // top-k: repeated wave argmax, larger probability first, lower index on ties
-    uint32_t taken = 0;
-    int selv[kMaxK];
-    float wv[kMaxK];
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-        if (j >= a.k) break;
-        float bv = 0.0f;
-        int be = 0x7fffffff;
-#pragma unroll
-        for (int t = 0; t < kMaxExpertsPerLane; ++t) {
-            const int e = lane + 64 * t;
-            if (e < E && !((taken >> t) & 1u) && (be == 0x7fffffff || p[t] > bv)) {
-                bv = p[t];
-                be = e;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oe = __shfl_xor(be, off);
-            const bool take = (be == 0x7fffffff) ? (oe != 0x7fffffff)
-                                                 : (oe != 0x7fffffff && (ov > bv || (ov == bv && oe < be)));
-            if (take) {
-                bv = ov;
-                be = oe;
-            }
-        }
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        selv[j] = be;
-        wv[j] = bv;
-    }
-    if (a.renorm) {
-        float ws = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMaxK; ++j)
-            if (j < a.k) ws = ws + wv[j];
-        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
-#pragma unroll
-        for (int j = 0; j < kMaxK; ++j)
-            if (j < a.k) wv[j] = wv[j] / ws;
-    }
-    // lane j < k stores entry j (selv/wv are identical on every lane)
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-        if (j < a.k && lane == j) {
-            a.sel[(size_t)tok * a.k + j] = selv[j];
-            a.wsel[(size_t)tok * a.k + j] = wv[j];
-        }
-    }
+__global__ __launch_bounds__(64) void router_tail_kernel(RouterArgs a) {
+    router_tail(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, blockIdx.x);
 }
 
 }  // namespace
