@@ -158,6 +158,35 @@ __device__ __forceinline__ bool poll(F ready, int *err) {
     }
 }
 
+// Bounded poll with two probes in flight: probe(buf) issues N loads into buf
+// and landed(buf) checks them; the next probe is issued before the previous
+// one is checked, so a probe starts every half round trip.  The probes
+// alternate between two buffers (a copy out of the one in flight would wait
+// for it); the probe's loads must not sit behind branches, or the compiler
+// waits for both.  On success the landed probe is copied to out.
+template <int N, class P, class C>
+__device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int *err) {
+    uint64_t pa[N], pb[N];
+    probe(pa);
+    return poll(
+        [&]() {
+            probe(pb);
+            if (landed(pa)) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) out[i] = pa[i];
+                return true;
+            }
+            probe(pa);
+            if (landed(pb)) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) out[i] = pb[i];
+                return true;
+            }
+            return false;
+        },
+        err);
+}
+
 // TGU/NB: gate and up type and super-blocks per row (n_embd / 256);
 // TD/NBH: down type and super-blocks per row (n_ff / 256).  Compile-time
 // shapes keep the code of one instantiation well inside the instruction cache.
@@ -511,20 +540,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             for (int t = lane; t < RD; t += 64) {
                 const int d = rank * RD + t;
                 const float res = xs[d];
+                // slots past k read slot 0 again: no branches around the loads
                 uint64_t yw[8];
-                const bool got = poll(
-                    [&]() {
+                const bool got = poll2(
+                    [&](uint64_t(&w)[8]) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            w[j] = ld_dev64(a.Y + ((size_t)cur * kXcds + (j < k ? j : 0)) * n + d);
+                    },
+                    [&](const uint64_t(&w)[8]) {
                         bool r = true;
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            if (j < k) {
-                                yw[j] = ld_dev64(a.Y + ((size_t)cur * kXcds + j) * n + d);
-                                r = r && tag_seq(yw[j]) == seq + 2u;
-                            }
-                        }
+                        for (int j = 0; j < 8; ++j) r = r & ((j >= k) | (tag_seq(w[j]) == seq + 2u));
                         return r;
                     },
-                    a.err);
+                    yw, a.err);
                 if (!got) sh_fail = 1;
                 float acc = 0.0f;
 #pragma unroll
