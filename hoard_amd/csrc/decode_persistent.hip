@@ -267,22 +267,30 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             // x of this layer: the XCD's 32 workgroups published 64 rows each; gathered
             // by waves 4-7 (wave 0 has just stored its combined rows)
             const uint64_t *xsrc = a.X + ((size_t)cur * kXcds + xcc) * n;
-            for (int i0 = 4 * (tid - kThreads / 2); i0 < n; i0 += 4 * (kThreads / 2)) {
-                uint64_t w[4];
-                const bool got = poll(
-                    [&]() {
-                        bool r = true;
+            // both of the thread's 4-word chunks in one probe: one round trip
+            // once the data is there, not one per chunk
+            static_assert(kEmbd == 8 * (kThreads / 2), "two 4-word chunks per gathering thread");
+            const int i0 = 4 * (tid - kThreads / 2), i1 = i0 + 4 * (kThreads / 2);
+            uint64_t w[8];
+            const bool got = poll(
+                [&]() {
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            w[c] = ld_l2(xsrc + i0 + c);
-                            r = r && tag_seq(w[c]) == seq - 1u;
-                        }
-                        return r;
-                    },
-                    a.err);
-                if (!got) sh_fail = 1;
-                const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
-                *reinterpret_cast<float4 *>(xs + i0) = make_float4(v[0], v[1], v[2], v[3]);
+                    for (int c = 0; c < 4; ++c) {
+                        w[c] = ld_l2(xsrc + i0 + c);
+                        w[4 + c] = ld_l2(xsrc + i1 + c);
+                    }
+                    bool r = true;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 1u);
+                    return r;
+                },
+                a.err);
+            if (!got) sh_fail = 1;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float v[4] = {tag_val(w[4 * h]), tag_val(w[4 * h + 1]), tag_val(w[4 * h + 2]),
+                                    tag_val(w[4 * h + 3])};
+                *reinterpret_cast<float4 *>(xs + (h ? i1 : i0)) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) ss += (double)(v[c] * v[c]);
             }
