@@ -35,6 +35,8 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kXcds = 8;
 constexpr int kPerXcd = 32;
+constexpr int kRankSlots = 128;              // experts the softmax / rank covers (E <= 128)
+static_assert(kRankSlots == kThreads / 4, "four threads per expert in the rank");
 constexpr int kFlagStride = 32;             // words: one 128-byte line per flag
 constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
 constexpr int kDecodeK = 8;                     // experts per token: one per XCD
@@ -105,7 +107,7 @@ __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, si
     s.q8h = take(sizeof(Q8L) * (a.n_ff / QK));
     s.gu = take(4 * 2 * (size_t)a.rows_gu);
     s.ys = take(4 * (size_t)a.rows_d);
-    s.ps = take(4 * (size_t)a.E);
+    s.ps = take(4 * (size_t)kRankSlots);
     if (total) *total = o;
     return s;
 }
@@ -366,34 +368,30 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             }
             sum = wave_sum_d(sum);
             const float sc = (float)(1.0 / sum);
-            if (lane < E) ps[lane] = p0 * sc;
-            if (lane + 64 < E) ps[lane + 64] = p1 * sc;
+            // kRankSlots entries; absent experts hold -1, below every probability
+            ps[lane] = lane < E ? p0 * sc : -1.0f;
+            ps[lane + 64] = lane + 64 < E ? p1 * sc : -1.0f;
             if (lane < 16) sel_s[lane] = -1;
         }
         lds_barrier();
         {
             // rank of expert e = experts ahead of it in (probability desc, index asc)
-            // order; four lanes split the comparisons and add their counts
+            // order; four lanes split the kRankSlots comparisons and add their
+            // counts.  Fixed trip counts: no branches, no scalar spills.
             const int e = tid >> 2, q = tid & 3;
-            const int span = E >> 2;  // a multiple of 8, at most 32
+            constexpr int kSpan = kRankSlots / 4;
+            const float pe = ps[e];
+            float4 pv[kSpan / 4];
+#pragma unroll
+            for (int c = 0; c < kSpan / 4; ++c) pv[c] = *reinterpret_cast<const float4 *>(ps + q * kSpan + 4 * c);
             int r = 0;
-            float pe = 0.0f;
-            if (e < E) {
-                pe = ps[e];
-                float4 pv[8];
 #pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    if (4 * c < span) pv[c] = *reinterpret_cast<const float4 *>(ps + q * span + 4 * c);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    if (4 * c < span) {
-                        const int e4 = q * span + 4 * c;
-                        r += (pv[c].x > pe || (pv[c].x == pe && e4 < e)) ? 1 : 0;
-                        r += (pv[c].y > pe || (pv[c].y == pe && e4 + 1 < e)) ? 1 : 0;
-                        r += (pv[c].z > pe || (pv[c].z == pe && e4 + 2 < e)) ? 1 : 0;
-                        r += (pv[c].w > pe || (pv[c].w == pe && e4 + 3 < e)) ? 1 : 0;
-                    }
-                }
+            for (int c = 0; c < kSpan / 4; ++c) {
+                const int e4 = q * kSpan + 4 * c;
+                r += (pv[c].x > pe) | ((pv[c].x == pe) & (e4 < e));
+                r += (pv[c].y > pe) | ((pv[c].y == pe) & (e4 + 1 < e));
+                r += (pv[c].z > pe) | ((pv[c].z == pe) & (e4 + 2 < e));
+                r += (pv[c].w > pe) | ((pv[c].w == pe) & (e4 + 3 < e));
             }
             r = group4_sum(r);
             if (e < E && q == 0 && r < k) {
