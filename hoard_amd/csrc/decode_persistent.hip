@@ -86,7 +86,7 @@ __host__ __device__ __forceinline__ size_t chunk_region(size_t nbytes) { return 
 
 struct Smem {
     // byte offsets into dynamic LDS
-    int xs, fxs, w, gate, up, down, q8x, q8h, gu, ys, ps;
+    int xs, w, gate, up, down, q8x, q8h, gu, ys, ps;
 };
 
 __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, size_t *total) {
@@ -98,7 +98,6 @@ __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, si
         return r;
     };
     s.xs = take(4 * (size_t)a.n_embd);
-    s.fxs = take(4 * (size_t)a.n_embd);
     s.w = take((size_t)(a.E / kPerXcd) * a.n_embd * 4);
     s.gate = take(chunk_region((size_t)a.rows_gu * a.max_rb_gu));
     s.up = take(chunk_region((size_t)a.rows_gu * a.max_rb_gu));
@@ -213,7 +212,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     const int rank = sh_rank;
     const Smem S = smem_layout(a, nullptr);
     float *xs = reinterpret_cast<float *>(smem + S.xs);
-    float *fxs = reinterpret_cast<float *>(smem + S.fxs);
     const float *wl = reinterpret_cast<const float *>(smem + S.w);
     Q8L *q8x = reinterpret_cast<Q8L *>(smem + S.q8x);
     Q8L *q8h = reinterpret_cast<Q8L *>(smem + S.q8h);
@@ -306,30 +304,31 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         }
         stamp(l, 1);
 
-        // -- P1: rms_norm scale, fx, router rows (32 lanes each) --
+        // -- P1: rms_norm scale, router rows (32 lanes each) --
+        // fx = x * scale is formed where it is read (router, Q8_K(fx)): no
+        // separate pass over x and no barrier for it
+        float scale;
         {
             double tot = 0.0;
             for (int w = 0; w < kWaves; ++w) tot += red_d[w];
             static_assert((kEmbd & (kEmbd - 1)) == 0, "n_embd a power of two: the mean is an exact multiply");
             const float mean = (float)(tot * (1.0 / (double)kEmbd));
-            const float scale = 1.0f / sqrtf(mean + a.eps);
-            for (int i = tid; i < n; i += kThreads) fxs[i] = xs[i] * scale;
+            scale = 1.0f / sqrtf(mean + a.eps);
         }
-        lds_barrier();
         {
             // lane l of a 32-lane half-wave holds accumulator l of ggml's x86 f32
             // dot (elements 32i + l, i ascending); rows 2w and 2w+1 on wave w
             const int row = 2 * wave + (lane >> 5), l32 = lane & 31;
             if (row < rw) {
                 const float *wr = wl + (size_t)row * kEmbd + l32;
-                const float *fr = fxs + l32;
+                const float *fr = xs + l32;
                 float acc = 0.0f;
                 for (int i0 = 0; i0 < kEmbd; i0 += 32 * 16) {
                     float wv[16], fv[16];
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
                         wv[j] = wr[i0 + 32 * j];
-                        fv[j] = fr[i0 + 32 * j];
+                        fv[j] = fr[i0 + 32 * j] * scale;
                     }
 #pragma unroll
                     for (int j = 0; j < 16; ++j) acc = fmaf(wv[j], fv[j], acc);
@@ -430,7 +429,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             }
         }
         // Q8_K(fx) while the rows are in flight
-        for (int b = wave; b < nb; b += kWaves) wave_quantize_q8l(fxs + b * QK, &q8x[b]);
+        for (int b = wave; b < nb; b += kWaves) {
+            const float4 x4 = *reinterpret_cast<const float4 *>(xs + b * QK + 4 * lane);
+            const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
+            wave_quantize_q8l_regs(v, &q8x[b]);
+        }
         if (wave == 0) {
             // renormalise the weights (only the combine, on this wave, reads them): every
             // lane forms the same left-to-right sum; lane j normalises weight j
