@@ -115,7 +115,6 @@ __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, si
 // stores and LDS DMA may stay in flight (the fence of __syncthreads would wait
 // for them).  Waves exchange data only through LDS inside the layer loop, and
 // every wave that issued LDS DMA waits for it itself before such a barrier.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // {value, seq} words: the value travels with the sequence number of the step that
 // produced it, so a consumer polls the data itself instead of a separate flag.

@@ -39,6 +39,10 @@ __device__ __forceinline__ void dma_wave_copy(uint8_t *dst, const uint8_t *src, 
     }
 }
 
+// Workgroup barrier after this wave's LDS operations: the data the waves
+// exchange goes through LDS, so the vector-memory counters need not drain.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Wait for every vector-memory operation of the wave, LDS copies included;
 // the memory clobber keeps the compiler from moving LDS reads above it.
 __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
