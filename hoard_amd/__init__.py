@@ -64,6 +64,9 @@ TRACE_PHASES = 12
 OPT_PERSISTENT_DECODE = 1
 OPT_PERSISTENT_AVAILABLE = 2
 OPT_POOL_NAIVE = 3
+OPT_DECODE_KERNEL = 4
+OPT_DECODE_KERNELS_AVAILABLE = 5
+DECODE_AUTO, DECODE_XCD, DECODE_SPREAD = 0, 1, 2
 
 
 class KernelTimes(ctypes.Structure):

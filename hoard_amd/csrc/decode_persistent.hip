@@ -21,6 +21,7 @@
 // polled after invalidating L1; cross-XCD flags and y use device-scope
 // (L2-bypassing) loads and stores.  Every wait is bounded by a wall-clock
 // timeout that raises an error flag and poisons the output instead of hanging.
+#include "exchange.h"
 #include "kernels.h"
 #include "lds_dma.h"
 #include "qblocks.h"
@@ -38,32 +39,9 @@ constexpr int kPerXcd = 32;
 constexpr int kRankSlots = 128;              // experts the softmax / rank covers (E <= 128)
 static_assert(kRankSlots == kThreads / 4, "four threads per expert in the rank");
 constexpr int kFlagStride = 32;             // words: one 128-byte line per flag
-constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
 constexpr int kDecodeK = 8;                     // experts per token: one per XCD
 constexpr int kTopkWave = 2;                    // polls the logits, softmax, renorm
 constexpr int kPublishWave = 7;                 // stores h and y
-
-__device__ __forceinline__ unsigned xcc_id() {
-    unsigned v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    return v & 7u;
-}
-
-
-__device__ __forceinline__ unsigned ld_dev_u32(const unsigned *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev_f32(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_u32(unsigned *p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_f32(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ bool reached(unsigned v, unsigned target) { return (int)(v - target) >= 0; }
 
 // Issue global_load_lds_dwordx4 for [src, src+nbytes) into LDS at dst, in
 // 1 KB chunks (64 lanes x 16 B) spread over waves [w0, w0+nw).  Rounds the
@@ -115,77 +93,6 @@ __host__ __device__ __forceinline__ Smem smem_layout(const PersistentArgs &a, si
 // stores and LDS DMA may stay in flight (the fence of __syncthreads would wait
 // for them).  Waves exchange data only through LDS inside the layer loop, and
 // every wave that issued LDS DMA waits for it itself before such a barrier.
-
-// {value, seq} words: the value travels with the sequence number of the step that
-// produced it, so a consumer polls the data itself instead of a separate flag.
-__device__ __forceinline__ uint64_t tag(float v, unsigned seq) {
-    return ((uint64_t)seq << 32) | (uint64_t)__float_as_uint(v);
-}
-__device__ __forceinline__ unsigned tag_seq(uint64_t w) { return (unsigned)(w >> 32); }
-__device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((unsigned)w); }
-// XCD-local words: plain 8-byte stores, which write through the CU's L1 into
-// the XCD's L2.  Readers use device-scope (sc1) loads: they skip L1 and are
-// served by this XCD's L2 for lines its own CUs wrote.  No L1 invalidate is
-// used anywhere: a buffer_inv issued while another wave of the same CU still
-// has stores in flight lost those stores on gfx950.  One aligned 8-byte access
-// is a single memory transaction, so a value and its sequence number are
-// always read together.
-__device__ __forceinline__ void st_l2(uint64_t *p, uint64_t w) { *p = w; }
-__device__ __forceinline__ uint64_t ld_l2(const uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Device-wide words (L2-bypassing).
-__device__ __forceinline__ void st_dev64(uint64_t *p, uint64_t w) {
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev64(const uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Bounded poll: true once ready() holds; false on timeout or a raised error.
-template <class F>
-__device__ __forceinline__ bool poll(F ready, int *err) {
-    const long long t0 = wall_clock64();
-    for (int it = 0;; ++it) {
-        if (ready()) return true;
-        if ((it & 31) == 31) {
-            if (ld_dev_u32((const unsigned *)err) != 0u) return false;
-            if (wall_clock64() - t0 > kTimeoutTicks) {
-                st_dev_u32((unsigned *)err, 1u);
-                return false;
-            }
-        }
-    }
-}
-
-// Bounded poll with two probes in flight: probe(buf) issues N loads into buf
-// and landed(buf) checks them; the next probe is issued before the previous
-// one is checked, so a probe starts every half round trip.  The probes
-// alternate between two buffers (a copy out of the one in flight would wait
-// for it); the probe's loads must not sit behind branches, or the compiler
-// waits for both.  On success the landed probe is copied to out.
-template <int N, class P, class C>
-__device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int *err) {
-    uint64_t pa[N], pb[N];
-    probe(pa);
-    return poll(
-        [&]() {
-            probe(pb);
-            if (landed(pa)) {
-#pragma unroll
-                for (int i = 0; i < N; ++i) out[i] = pa[i];
-                return true;
-            }
-            probe(pa);
-            if (landed(pb)) {
-#pragma unroll
-                for (int i = 0; i < N; ++i) out[i] = pb[i];
-                return true;
-            }
-            return false;
-        },
-        err);
-}
 
 // TGU/NB: gate and up type and super-blocks per row (n_embd / 256);
 // TD/NBH: down type and super-blocks per row (n_ff / 256).  Compile-time

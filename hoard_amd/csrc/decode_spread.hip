@@ -1,0 +1,497 @@
+// One-launch stacked decode with every selected expert's rows spread over all
+// 256 workgroups (one per CU): the shape for many small experts, where the
+// k routed experts plus a shared one do not map one expert to one XCD
+// (Qwen3-Next: 512 experts, top-10 of ff 512, a gated shared expert).
+//
+// Replaces, for a whole token, the reference's per-layer loop of graph A's
+// router tail (src/run_qwen35.cpp:554-580), graph B with the shared expert
+// (:640-665) and the host combine (:675-676), with no host round trip.
+//
+// Per layer, workgroup g (of 256) owns
+//   * router rows [RR*g, RR*g + RR) (RR = E/256), prefetched into LDS while
+//     the previous layer finishes;
+//   * routed h rows [HR*g, HR*g + HR) of the concatenated h of the k selected
+//     experts (HR = k*ff/256; a range may cross from one expert into the next)
+//     and shared-expert h rows [HS*g, HS*g + HS);
+//   * output rows [8g, 8g + 8): their down rows for every selected expert and
+//     the shared one, so the weighted combine of those rows needs no further
+//     exchange.
+// Three all-to-all exchanges per layer, in device-scope words {value, seq}:
+// the logits (E words), h ((k+1)*ff words) and x (n_embd words).  Each is a
+// full barrier between the phases either side of it, so one buffer per
+// exchange suffices: a workgroup can only overwrite a word of layer l with
+// layer l+1's after every workgroup has read it.
+//
+// Top-k over E <= 512 probabilities: one per thread, keyed (probability bits,
+// inverted index) so larger keys come first and ties go to the lower index;
+// each wave ranks its 64 keys, the k best of every wave (8k candidates) are
+// ranked against each other.
+#include "exchange.h"
+#include "kernels.h"
+#include "lds_dma.h"
+#include "qblocks.h"
+#include "rowdot.h"
+#include "wave.h"
+
+namespace hoard {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kGroups = 256;  // workgroups, one per CU
+
+constexpr int align16(int v) { return (v + 15) & ~15; }
+
+// LDS layout of one instantiation (byte offsets, 16-byte aligned).
+template <int NB, int NBH, int K, int E, bool SH>
+struct SpreadShape {
+    static constexpr int kEmbd = NB * QK;
+    static constexpr int kFF = NBH * QK;
+    static constexpr int U = K + (SH ? 1 : 0);          // expert units: routed slots, then the shared expert
+    static constexpr int HR = K * kFF / kGroups;        // routed h rows per workgroup
+    static constexpr int HS = SH ? kFF / kGroups : 0;   // shared h rows per workgroup
+    static constexpr int NH = U * kFF;                  // h words exchanged
+    static constexpr int RR = E >= kGroups ? E / kGroups : 1;  // router rows per workgroup
+    static constexpr int DR = kEmbd / kGroups;          // output rows per workgroup
+    static constexpr int RBG = NB * kQ4KBytes;          // gate/up row bytes
+    static constexpr int RBD = NBH * kQ6KBytes;         // down row bytes
+    static constexpr int NGU = 2 * HR + 2 * HS;         // gate/up rows dotted per workgroup
+    static constexpr int kCand = 8 * K;                 // top-k candidates, k per wave
+    static constexpr int kHalfRows = U * DR / 2;        // down rows of one parity
+    static constexpr int kGatherH = (NH + 383) / 384;   // h words per gathering thread (waves 0-5)
+
+    static_assert(NB == 8, "one 8-lane group per gate/up row, one lane per super-block");
+    static_assert((K * kFF) % kGroups == 0 && (!SH || kFF % kGroups == 0), "h rows split evenly");
+    static_assert(E <= kThreads && (E % kGroups == 0 || kGroups % E == 0) && RR <= 2, "router rows per workgroup");
+    static_assert(K <= 16 && K <= E && 4 * kCand <= kThreads, "top-k");
+    static_assert(DR % 2 == 0 && kEmbd % kGroups == 0, "output rows split evenly, in parity pairs");
+    static_assert(NGU <= 48, "gate/up rows on waves 0-5");
+    static_assert(HR + HS <= 64, "h published by one wave");
+
+    static constexpr int oXS = 0;
+    static constexpr int oWR = oXS + 4 * kEmbd;
+    static constexpr int oSGR = oWR + 4 * RR * kEmbd;
+    static constexpr int oSHGU = oSGR + (SH ? 4 * kEmbd : 0);
+    static constexpr int oSHD = align16(oSHGU + 2 * HS * RBG);
+    static constexpr int oGU = align16(oSHD + (SH ? DR * RBD : 0));
+    static constexpr int oDN = align16(oGU + 2 * HR * RBG);
+    static constexpr int oQ8X = align16(oDN + K * DR * RBD);
+    static constexpr int oQ8H = oQ8X + (int)sizeof(Q8L) * NB;
+    static constexpr int oLG = oQ8H + (int)sizeof(Q8L) * U * NBH;
+    static constexpr int oKEY = oLG + 4 * kThreads;
+    static constexpr int oCAND = oKEY + 8 * kThreads;
+    static constexpr int oGUV = oCAND + 8 * kCand;
+    static constexpr int oYS = align16(oGUV + 4 * NGU);
+    static constexpr int kBytes = align16(oYS + 4 * U * DR);
+    static_assert((DR * RBD) % 16 == 0, "per-expert down segments stay 16-byte aligned");
+    static_assert(4 * NH <= 2 * HR * RBG, "h is gathered over the consumed gate/up rows");
+};
+
+// Copy nbytes (a multiple of 16) from src to LDS at dst as 1 KB chunks.  The
+// chunks of consecutive calls form one stream numbered from `base`, dealt
+// round-robin to nw waves; the calling wave is number wrel of them.  Lanes
+// past the end copy nothing, so exactly [src, src + nbytes) is read.
+// Returns the chunk number after this segment.
+__device__ __forceinline__ int dma_seg(uint8_t *dst, const uint8_t *src, int nbytes, int base, int wrel, int nw) {
+    const int lane = threadIdx.x & 63;
+    const int nch = (nbytes + 1023) >> 10;
+    for (int c = ((wrel - base) % nw + nw) % nw; c < nch; c += nw)
+        if (c * 1024 + 16 * lane < nbytes) dma_chunk(dst + c * 1024, src + (size_t)c * 1024);
+    return base + nch;
+}
+
+// ggml's x86 f32 dot of one row held by a 32-lane half-wave against x*scale:
+// lane l accumulates elements 32i + l with fma, i ascending, then the fold.
+// Exact in lane 0 of the half-wave.
+template <int N>
+__device__ __forceinline__ float half_wave_dot(const float *w, const float *x, float scale) {
+    const int l32 = threadIdx.x & 31;
+    const float *wr = w + l32;
+    const float *fr = x + l32;
+    float acc = 0.0f;
+    for (int i0 = 0; i0 < N; i0 += 32 * 16) {
+        float wv[16], fv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            wv[j] = wr[i0 + 32 * j];
+            fv[j] = fr[i0 + 32 * j] * scale;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = fmaf(wv[j], fv[j], acc);
+    }
+    acc = acc + __shfl_xor(acc, 16);  // accumulators a and a+16
+    return row16_ggml_fold(acc);
+}
+
+template <int NB, int NBH, int K, int E, bool SH>
+__global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
+    using S = SpreadShape<NB, NBH, K, E, SH>;
+    constexpr int kEmbd = S::kEmbd, kFF = S::kFF, HR = S::HR, HS = S::HS, NH = S::NH, RR = S::RR, DR = S::DR;
+    constexpr int RBG = S::RBG, RBD = S::RBD, NGU = S::NGU, kCand = S::kCand;
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float red_mx[kWaves];
+    __shared__ double red_ss[kWaves], red_sum[kWaves];
+    __shared__ int sel_s[16];
+    __shared__ float w_s[16];
+    __shared__ float sg_s;
+    __shared__ int fail_s;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int grp = tid >> 3, t8 = tid & 7;
+    const int g = blockIdx.x;
+    float *xs = reinterpret_cast<float *>(smem + S::oXS);
+    const float *wr = reinterpret_cast<const float *>(smem + S::oWR);
+    float *hb = reinterpret_cast<float *>(smem + S::oGU);  // gathered h, over the consumed gate/up rows
+    Q8L *q8x = reinterpret_cast<Q8L *>(smem + S::oQ8X);
+    Q8L *q8h = reinterpret_cast<Q8L *>(smem + S::oQ8H);
+    float *lgv = reinterpret_cast<float *>(smem + S::oLG);
+    uint64_t *keys = reinterpret_cast<uint64_t *>(smem + S::oKEY);
+    uint64_t *cand = reinterpret_cast<uint64_t *>(smem + S::oCAND);
+    float *guv = reinterpret_cast<float *>(smem + S::oGUV);
+    float *ys = reinterpret_cast<float *>(smem + S::oYS);
+
+    // this workgroup's routed h rows: unit u0 rows [r0, r0 + n0), then unit u0 + 1 rows [0, n1)
+    const int h0 = g * HR, u0 = h0 / kFF, r0 = h0 % kFF;
+    const int n0 = HR < kFF - r0 ? HR : kFF - r0, n1 = HR - n0;
+    const int rrow0 = g * RR;
+    const bool has_router = rrow0 < E;
+
+    if (tid == 0) fail_s = 0;
+
+    // Router rows, and the shared expert's gate row, gate/up rows and down rows,
+    // of layer l: none depends on the routing.
+    auto prefetch = [&](int l, int w0, int nw) {
+        if (wave < w0 || wave >= w0 + nw) return;
+        const DecodeLayer &L = a.layers[l];
+        const int wrel = wave - w0;
+        int b = 0;
+        if (has_router)
+            b = dma_seg(smem + S::oWR, reinterpret_cast<const uint8_t *>(L.router + (size_t)rrow0 * kEmbd),
+                        4 * RR * kEmbd, b, wrel, nw);
+        if constexpr (SH) {
+            b = dma_seg(smem + S::oSGR, reinterpret_cast<const uint8_t *>(L.sh_gate_inp), 4 * kEmbd, b, wrel, nw);
+            b = dma_seg(smem + S::oSHGU, L.sh_gate + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
+            b = dma_seg(smem + S::oSHGU + HS * RBG, L.sh_up + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
+            b = dma_seg(smem + S::oSHD, L.sh_down + (size_t)g * DR * RBD, DR * RBD, b, wrel, nw);
+        }
+    };
+
+    prefetch(a.l0, 0, kWaves);
+    double ss = 0.0;  // this thread's part of sum(x*x), for rms_norm
+    for (int i = tid; i < kEmbd; i += kThreads) {
+        const float v = a.x[i];
+        xs[i] = v;
+        ss += (double)(v * v);
+    }
+
+    for (int l = a.l0; l < a.l1; ++l) {
+        const DecodeLayer &L = a.layers[l];
+        const unsigned seq = a.seq0 + 4u * (unsigned)(l - a.l0);
+        const bool last = l + 1 == a.l1;
+
+        // -- x of this layer: waves 4-7 gather it; waves 0-3 prefetched this layer's rows --
+        if (l > a.l0) {
+            ss = 0.0;
+            if (wave >= 4) {
+                const int t4 = tid - 256;
+                uint64_t w[8];
+                const bool got = poll(
+                    [&]() {
+                        bool r = true;
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) w[c] = ld_dev64(a.X + t4 + 256 * c);
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 2u);
+                        return r;
+                    },
+                    a.err);
+                if (!got) fail_s = 1;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float v = tag_val(w[c]);
+                    xs[t4 + 256 * c] = v;
+                    ss += (double)(v * v);
+                }
+            }
+        }
+        lds_dma_wait();  // the prefetch this wave issued
+        ss = wave_sum_d(ss);
+        if (lane == 0) red_ss[wave] = ss;
+        lds_barrier();
+
+        // rms_norm scale; fx = x*scale is formed where it is read
+        float scale;
+        {
+            double tot = 0.0;
+            for (int w = 0; w < kWaves; ++w) tot += red_ss[w];
+            static_assert((kEmbd & (kEmbd - 1)) == 0, "n_embd a power of two: the mean is an exact multiply");
+            const float mean = (float)(tot * (1.0 / (double)kEmbd));
+            scale = 1.0f / sqrtf(mean + a.eps);
+        }
+
+        // -- router rows (wave 4), shared gate (wave 5), Q8_K(fx) (waves 4-7); logits gathered by waves 0-3 --
+        if (wave == 4 && has_router) {
+            const int row = lane >> 5;
+            if (row < RR && rrow0 + row < E) {
+                const float r = half_wave_dot<kEmbd>(wr + (size_t)row * kEmbd, xs, scale);
+                if ((lane & 31) == 0) st_dev64(a.LG + rrow0 + row, tag(r, seq));
+            }
+        }
+        if constexpr (SH) {
+            if (wave == 5 && lane < 32) {
+                const float r = half_wave_dot<kEmbd>(reinterpret_cast<const float *>(smem + S::oSGR), xs, scale);
+                if (lane == 0) sg_s = 1.0f / (1.0f + expf(-r));
+            }
+        }
+        if (wave >= 4) {
+            for (int b = wave - 4; b < NB; b += 4) {
+                const float4 x4 = *reinterpret_cast<const float4 *>(xs + b * QK + 4 * lane);
+                const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
+                wave_quantize_q8l_regs(v, &q8x[b]);
+            }
+        } else {
+            const int i0 = tid, i1 = tid + 256;
+            const int j0 = i0 < E ? i0 : 0, j1 = i1 < E ? i1 : 0;
+            uint64_t w0 = 0, w1 = 0;
+            const bool got = poll(
+                [&]() {
+                    w0 = ld_dev64(a.LG + j0);
+                    w1 = ld_dev64(a.LG + j1);
+                    return (bool)__all((tag_seq(w0) == seq) & (tag_seq(w1) == seq));
+                },
+                a.err);
+            if (!got) fail_s = 1;
+            const float v0 = i0 < E ? tag_val(w0) : -INFINITY, v1 = i1 < E ? tag_val(w1) : -INFINITY;
+            lgv[i0] = v0;
+            lgv[i1] = v1;
+            const float m = wave_max_f(v1 > v0 ? v1 : v0);
+            if (lane == 0) red_mx[wave] = m;
+        }
+        lds_barrier();
+
+        // -- softmax over all E (thread t: expert t), then the top-k --
+        float pt;
+        {
+            float mx = red_mx[0];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) mx = red_mx[w] > mx ? red_mx[w] : mx;
+            const float et = tid < E ? expf(lgv[tid] - mx) : 0.0f;
+            const double s = wave_sum_d((double)et);
+            if (lane == 0) red_sum[wave] = s;
+            lds_barrier();
+            double tot = 0.0;
+            for (int w = 0; w < kWaves; ++w) tot += red_sum[w];
+            pt = et * (float)(1.0 / tot);
+        }
+        {
+            // key: probability bits over the inverted index (probabilities are >= +0, so
+            // their bit patterns order as the values); absent experts rank last
+            const uint64_t inv = (uint64_t)(0xFFFFu - (unsigned)tid);
+            const uint64_t key = tid < E ? (((uint64_t)__float_as_uint(pt) << 16) | inv) : inv;
+            keys[tid] = key;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's keys are in LDS
+            const uint64_t *kw = keys + 64 * wave;
+            int r1 = 0;
+#pragma unroll
+            for (int j = 0; j < 64; j += 2) {
+                const ulonglong2 kk = *reinterpret_cast<const ulonglong2 *>(kw + j);
+                r1 += (int)(kk.x > key) + (int)(kk.y > key);
+            }
+            if (r1 < K) cand[wave * K + r1] = key;
+        }
+        lds_barrier();
+        if (tid < 4 * kCand) {
+            // rank among the candidates: four lanes per candidate, a quarter each
+            constexpr int kSpan = kCand / 4;
+            const int c = tid >> 2, q = tid & 3;
+            const uint64_t kc = cand[c];
+            int r2 = 0;
+#pragma unroll
+            for (int j = 0; j < kSpan; ++j) r2 += (int)(cand[q * kSpan + j] > kc);
+            r2 = group4_sum(r2);
+            if (q == 0 && r2 < K) {
+                sel_s[r2] = (int)(0xFFFFu - (unsigned)(kc & 0xFFFFu));
+                w_s[r2] = __uint_as_float((unsigned)(kc >> 16));
+            }
+        }
+        lds_barrier();
+
+        // -- waves 0-5 stream this workgroup's routed gate/up rows into LDS --
+        auto expert = [&](int u) {
+            const int e = sel_s[u];
+            return (e < 0 || e >= E) ? 0 : e;
+        };
+        if (wave < 6) {
+            __builtin_amdgcn_s_waitcnt(0);  // ordinary loads first: the copies retire behind them
+            const size_t e0 = (size_t)expert(u0), e1 = n1 ? (size_t)expert(u0 + 1) : 0;
+            int b = 0;
+            b = dma_seg(smem + S::oGU, L.gate + e0 * L.gstride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
+            if (n1) b = dma_seg(smem + S::oGU + n0 * RBG, L.gate + e1 * L.gstride, n1 * RBG, b, wave, 6);
+            b = dma_seg(smem + S::oGU + HR * RBG, L.up + e0 * L.ustride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
+            if (n1) b = dma_seg(smem + S::oGU + (HR + n0) * RBG, L.up + e1 * L.ustride, n1 * RBG, b, wave, 6);
+        } else if (wave == 7) {
+            // renormalise the weights (read only by the combine): every lane forms the
+            // same left-to-right sum; lane j normalises weight j
+            float ws = 0.0f;
+#pragma unroll
+            for (int j = 0; j < K; ++j) ws = ws + w_s[j];
+            float wj = lane < K ? w_s[lane] : 0.0f;
+            if (a.renorm) {
+                if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+                wj = wj / ws;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every lane's reads precede the writes
+            if (lane < K) w_s[lane] = wj;
+        }
+        if (wave < 6) lds_dma_wait();
+        lds_barrier();
+
+        // -- wave 6 streams the down rows (needed after the h exchange); waves 0-5 dot gate/up --
+        if (wave == 6) {
+            int b = 0;
+#pragma unroll 1
+            for (int u = 0; u < K; ++u)
+                b = dma_seg(smem + S::oDN + u * DR * RBD, L.down + (size_t)expert(u) * L.dstride + (size_t)g * DR * RBD,
+                            DR * RBD, b, 0, 1);
+        }
+        if (grp < NGU) {
+            Q8Reg xr;
+            load_q8reg(q8x[t8], xr);
+            const uint8_t *rp = grp < 2 * HR ? smem + S::oGU + grp * RBG : smem + S::oSHGU + (grp - 2 * HR) * RBG;
+            const float v = lpb_row_q4k<NB>(rp, xr, t8);
+            if (t8 == NB - 1) guv[grp] = v;
+        }
+        lds_barrier();
+
+        // -- h: published by wave 7, gathered whole by waves 0-5 --
+        if (wave == 7 && lane < HR + HS) {
+            float gv, uv;
+            int dst;
+            if (lane < HR) {
+                gv = guv[lane];
+                uv = guv[HR + lane];
+                dst = h0 + lane;
+            } else {
+                const int i = lane - HR;
+                gv = guv[2 * HR + i];
+                uv = guv[2 * HR + HS + i];
+                dst = K * kFF + g * HS + i;
+            }
+            st_dev64(a.H + dst, tag(gv / (1.0f + expf(-gv)) * uv, seq + 1u));
+        }
+        if (wave < 6) {
+            uint64_t w[S::kGatherH];
+            const bool got = poll(
+                [&]() {
+                    bool r = true;
+#pragma unroll
+                    for (int c = 0; c < S::kGatherH; ++c) {
+                        const int i = tid + 384 * c;
+                        w[c] = ld_dev64(a.H + (i < NH ? i : NH - 1));
+                    }
+#pragma unroll
+                    for (int c = 0; c < S::kGatherH; ++c) r = r & (tag_seq(w[c]) == seq + 1u);
+                    return r;
+                },
+                a.err);
+            if (!got) fail_s = 1;
+#pragma unroll
+            for (int c = 0; c < S::kGatherH; ++c) {
+                const int i = tid + 384 * c;
+                if (i < NH) hb[i] = tag_val(w[c]);
+            }
+        }
+        if (wave == 6) lds_dma_wait();
+        lds_barrier();
+
+        // -- Q8_K(h) of every unit, then the down rows --
+        for (int b = wave; b < S::U * NBH; b += kWaves) wave_quantize_q8l(hb + b * QK, &q8h[b]);
+        lds_barrier();
+        {
+            // a wave takes rows of one parity, so its rows share their 4-byte alignment
+            const int par = wave & 1;
+            const int G = (wave >> 1) * 8 + (grp & 7);
+#pragma unroll
+            for (int pass = 0; pass < (S::kHalfRows + 31) / 32; ++pass) {
+                const int q = G + 32 * pass;
+                if (q < S::kHalfRows) {
+                    const int u = q / (DR / 2), i = 2 * (q % (DR / 2)) + par;
+                    const uint8_t *rp =
+                        (!SH || u < K) ? smem + S::oDN + (u * DR + i) * RBD : smem + S::oSHD + i * RBD;
+                    const float y = g8_row_q6k_u<NBH>(rp, q8h + u * NBH, t8);
+                    if (t8 == 0) ys[u * DR + i] = y;
+                }
+            }
+        }
+        lds_barrier();
+
+        // -- combine rows [8g, 8g + 8) over the slots in order, then the shared expert and residual --
+        if (wave == 0 && lane < DR) {
+            const int d = g * DR + lane;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < K; ++j) acc = acc + w_s[j] * ys[j * DR + lane];
+            float o;
+            if constexpr (SH)
+                o = (acc + ys[K * DR + lane] * sg_s) + xs[d];
+            else
+                o = acc + xs[d];
+            if (last)
+                a.x[d] = o;
+            else
+                st_dev64(a.X + d, tag(o, seq + 2u));
+        }
+        if (!last) prefetch(l + 1, 0, 4);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (fail_s && tid < DR) a.x[g * DR + tid] = __builtin_nanf("");  // the caller sees the failure
+}
+
+}  // namespace
+
+// The shapes with an instantiated kernel: {n_embd/256, n_ff/256, k, E, shared expert}.
+#define HOARD_SPREAD_SHAPES(X) \
+    X(8, 2, 10, 512, true)     \
+    X(8, 3, 8, 128, false)
+
+using SpreadFn = void (*)(SpreadArgs);
+
+static SpreadFn spread_fn(const SpreadArgs &a, size_t *lds) {
+#define HOARD_PICK(P_NB, P_NBH, P_K, P_E, P_SH)                                                 \
+    if (a.n_embd == P_NB * QK && a.n_ff == P_NBH * QK && a.k == P_K && a.E == P_E &&                \
+        (a.shared != 0) == P_SH) {                                                                  \
+        *lds = SpreadShape<P_NB, P_NBH, P_K, P_E, P_SH>::kBytes;                                    \
+        return spread_kernel<P_NB, P_NBH, P_K, P_E, P_SH>;                                          \
+    }
+    HOARD_SPREAD_SHAPES(HOARD_PICK)
+#undef HOARD_PICK
+    *lds = 0;
+    return nullptr;
+}
+
+bool spread_shape_compiled(const SpreadArgs &a) {
+    size_t lds;
+    return spread_fn(a, &lds) != nullptr;
+}
+
+hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s) {
+    size_t lds = 0;
+    const SpreadFn fn = spread_fn(a, &lds);
+    if (!fn || lds > kPersistentMaxLds) return hipErrorInvalidConfiguration;
+    static SpreadFn attr_set[4] = {};
+    int slot = 0;
+    while (slot < 4 && attr_set[slot] && attr_set[slot] != fn) ++slot;
+    if (slot == 4 || attr_set[slot] != fn) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        if (slot < 4) attr_set[slot] = fn;
+    }
+    SpreadArgs args = a;
+    void *params[] = {&args};
+    return hipLaunchCooperativeKernel((const void *)fn, dim3(kGroups), dim3(kThreads), params, (unsigned)lds, s);
+}
+
+}  // namespace hoard

@@ -1,0 +1,102 @@
+// Cross-workgroup exchange words for the persistent decode kernels.
+//
+// A value travels with the sequence number of the step that produced it in
+// one aligned 8-byte word {float bits, seq}, so a consumer polls the data
+// itself instead of a separate flag, and words left over from earlier steps
+// or launches never match.  Every wait is bounded: on a wall-clock timeout
+// the waiter raises a device-wide error flag, and every other wait returns
+// once it sees the flag.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hoard {
+
+constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
+
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 7u;
+}
+
+__device__ __forceinline__ unsigned ld_dev_u32(const unsigned *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u32(unsigned *p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t tag(float v, unsigned seq) {
+    return ((uint64_t)seq << 32) | (uint64_t)__float_as_uint(v);
+}
+__device__ __forceinline__ unsigned tag_seq(uint64_t w) { return (unsigned)(w >> 32); }
+__device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((unsigned)w); }
+
+// XCD-local words: plain 8-byte stores, which write through the CU's L1 into
+// the XCD's L2.  Readers use device-scope (sc1) loads: they skip L1 and are
+// served by this XCD's L2 for lines its own CUs wrote.  No L1 invalidate is
+// used anywhere: a buffer_inv issued while another wave of the same CU still
+// has stores in flight lost those stores on gfx950.  One aligned 8-byte access
+// is a single memory transaction, so a value and its sequence number are
+// always read together.
+__device__ __forceinline__ void st_l2(uint64_t *p, uint64_t w) { *p = w; }
+__device__ __forceinline__ uint64_t ld_l2(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Device-wide words: the store writes past the XCD's L2, the load skips it,
+// so the pair works between any two CUs of the device.
+__device__ __forceinline__ void st_dev64(uint64_t *p, uint64_t w) {
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded poll: true once ready() holds; false on timeout or a raised error.
+template <class F>
+__device__ __forceinline__ bool poll(F ready, int *err) {
+    const long long t0 = wall_clock64();
+    for (int it = 0;; ++it) {
+        if (ready()) return true;
+        if ((it & 31) == 31) {
+            if (ld_dev_u32((const unsigned *)err) != 0u) return false;
+            if (wall_clock64() - t0 > kTimeoutTicks) {
+                st_dev_u32((unsigned *)err, 1u);
+                return false;
+            }
+        }
+    }
+}
+
+// Bounded poll with two probes in flight: probe(buf) issues N loads into buf
+// and landed(buf) checks them; the next probe is issued before the previous
+// one is checked, so a probe starts every half round trip.  The probes
+// alternate between two buffers (a copy out of the one in flight would wait
+// for it); the probe's loads must not sit behind branches, or the compiler
+// waits for both.  On success the landed probe is copied to out.
+template <int N, class P, class C>
+__device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int *err) {
+    uint64_t pa[N], pb[N];
+    probe(pa);
+    return poll(
+        [&]() {
+            probe(pb);
+            if (landed(pa)) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) out[i] = pa[i];
+                return true;
+            }
+            probe(pa);
+            if (landed(pb)) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) out[i] = pb[i];
+                return true;
+            }
+            return false;
+        },
+        err);
+}
+
+}  // namespace hoard

@@ -101,6 +101,9 @@ struct DecodeLayer {
     const uint8_t *gate, *up, *down;
     size_t gstride, ustride, dstride;
     int gate_type, up_type, down_type;
+    // shared expert (spread kernel only; null without one)
+    const uint8_t *sh_gate, *sh_up, *sh_down;
+    const float *sh_gate_inp;
 };
 struct PersistentArgs {
     const DecodeLayer *layers;  // device array, indexed by layer
@@ -126,6 +129,26 @@ constexpr size_t kPersistentMaxLds = 163840 - 1024;
 size_t persistent_lds_bytes(const PersistentArgs &a);
 hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s);
 bool persistent_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
+
+// One-launch decode with each selected expert's rows spread over all 256
+// workgroups (decode_spread.hip): k routed experts plus an optional shared one,
+// gate/up Q4_K and down Q6_K in every layer of the range.
+struct SpreadArgs {
+    const DecodeLayer *layers;  // device array, indexed by layer
+    int l0, l1;
+    float *x;                   // [n_embd] in/out
+    float eps;
+    int renorm;
+    int n_embd, n_ff, E, k, shared;  // select the instantiation (shared: n_ff_shexp == n_ff)
+    // exchanged values carry their sequence number: {float bits, seq} per 64-bit word
+    uint64_t *LG;               // [E]               router logits
+    uint64_t *H;                // [(k+shared)*n_ff] h of the routed experts, then the shared one
+    uint64_t *X;                // [n_embd]          x between layers
+    int *err;
+    unsigned seq0;
+};
+bool spread_shape_compiled(const SpreadArgs &a);
+hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s);
 
 size_t block_bytes(int type);
 

@@ -94,11 +94,15 @@ struct hoard_moe {
     std::vector<Mark> marks;
     std::vector<hipEvent_t> event_pool;
     // persistent stacked decode
-    bool persistent_shape_ok = false;  // shape/device admit the one-launch decode
+    bool persistent_shape_ok = false;  // shape/device admit a one-launch decode
+    bool xcd_ok = false;               // ... the expert-per-XCD kernel
+    bool spread_ok = false;            // ... the rows-spread kernel
     int persistent_mode = 1;           // HOARD_OPT_PERSISTENT_DECODE value
+    int decode_kernel = 0;             // HOARD_OPT_DECODE_KERNEL value
     bool table_dirty = true;
     hoard::DecodeLayer *d_table = nullptr;
     uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
+    uint64_t *sX = nullptr, *sLG = nullptr, *sH = nullptr;  // spread kernel's exchange words
     unsigned *pflags = nullptr;        // tickets
     int *perr = nullptr;
     unsigned seq = 1;
@@ -139,6 +143,9 @@ struct hoard_moe {
         hipFree(pLG);
         hipFree(pH);
         hipFree(pY);
+        hipFree(sX);
+        hipFree(sLG);
+        hipFree(sH);
         hipFree(pflags);
         hipFree(perr);
         hipFree(ptrace);
@@ -385,10 +392,22 @@ int pool_after_route(hoard_moe *h, int layer, const int32_t *sel_dev, int32_t *s
     return pool_ensure(h, layer, h->pin_sel, nullptr, slot_dev, s, s);
 }
 
-// The one-launch decode needs 8 XCDs x 32 CUs (one workgroup per CU), one
-// expert slot per XCD, a router small enough to prefetch into LDS and no shared
-// expert; otherwise hoard_moe_decode launches the per-layer kernels.
+// The one-launch decodes need 8 XCDs x 32 CUs (one workgroup per CU).  The
+// expert-per-XCD kernel takes k = 8 routed experts (one per XCD) of E <= 128
+// with no shared expert; the rows-spread kernel takes the instantiated
+// {n_embd, n_ff, k, E, shared} shapes.  Otherwise hoard_moe_decode launches the
+// per-layer kernels.
 constexpr int kPersistentCus = 256;
+
+hoard::SpreadArgs spread_shape(const hoard_moe_cfg &c) {
+    hoard::SpreadArgs a{};
+    a.n_embd = c.n_embd;
+    a.n_ff = c.n_ff;
+    a.E = c.n_expert;
+    a.k = c.n_used;
+    a.shared = c.n_ff_shexp > 0 ? 1 : 0;
+    return a;
+}
 
 int persistent_setup(hoard_moe *h) {
     const hoard_moe_cfg &c = h->cfg;
@@ -396,29 +415,92 @@ int persistent_setup(hoard_moe *h) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, h->device) != hipSuccess) return fail(HOARD_ERR_HIP, "device properties");
     cus = prop.multiProcessorCount;
-    const bool arch_ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-    h->persistent_shape_ok = arch_ok && cus == kPersistentCus && c.n_embd == 2048 && c.n_used == 8 &&
-                             c.n_expert % 32 == 0 && c.n_expert <= 128 && c.n_ff % 256 == 0 && c.n_ff <= 1024 &&
-                             c.n_ff_shexp == 0 && c.pool_k == 0;
-    if (!h->persistent_shape_ok) return HOARD_OK;
+    const bool arch_ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 && cus == kPersistentCus && c.pool_k == 0;
+    h->xcd_ok = arch_ok && c.n_embd == 2048 && c.n_used == 8 && c.n_expert % 32 == 0 && c.n_expert <= 128 &&
+                c.n_ff % 256 == 0 && c.n_ff <= 1024 && c.n_ff_shexp == 0;
+    h->spread_ok = arch_ok && (c.n_ff_shexp == 0 || c.n_ff_shexp == c.n_ff) &&
+                   hoard::spread_shape_compiled(spread_shape(c));
+    h->persistent_shape_ok = h->xcd_ok || h->spread_ok;
     int rc = 0;
-    rc = rc ? rc : dev_alloc((void **)&h->d_table, sizeof(hoard::DecodeLayer) * c.n_layer);
-    const size_t nX = (size_t)2 * 8 * c.n_embd, nLG = (size_t)8 * c.n_expert, nH = (size_t)8 * c.n_ff;
-    rc = rc ? rc : dev_alloc((void **)&h->pX, sizeof(uint64_t) * nX);
-    rc = rc ? rc : dev_alloc((void **)&h->pLG, sizeof(uint64_t) * nLG);
-    rc = rc ? rc : dev_alloc((void **)&h->pH, sizeof(uint64_t) * nH);
-    rc = rc ? rc : dev_alloc((void **)&h->pY, sizeof(uint64_t) * nX);
-    const size_t flag_words = (size_t)8 * 32;
-    rc = rc ? rc : dev_alloc((void **)&h->pflags, flag_words * sizeof(unsigned));
-    rc = rc ? rc : dev_alloc((void **)&h->perr, sizeof(int));
-    if (rc) return rc;
+    if (h->persistent_shape_ok) {
+        rc = dev_alloc((void **)&h->d_table, sizeof(hoard::DecodeLayer) * c.n_layer);
+        rc = rc ? rc : dev_alloc((void **)&h->perr, sizeof(int));
+        if (rc) return rc;
+        HIP_TRY(hipMemset(h->perr, 0, sizeof(int)));
+    }
     // sequence tags start at 1, so zeroed words never read as current
-    HIP_TRY(hipMemset(h->pX, 0, sizeof(uint64_t) * nX));
-    HIP_TRY(hipMemset(h->pLG, 0, sizeof(uint64_t) * nLG));
-    HIP_TRY(hipMemset(h->pH, 0, sizeof(uint64_t) * nH));
-    HIP_TRY(hipMemset(h->pY, 0, sizeof(uint64_t) * nX));
-    HIP_TRY(hipMemset(h->pflags, 0, flag_words * sizeof(unsigned)));
-    HIP_TRY(hipMemset(h->perr, 0, sizeof(int)));
+    if (h->xcd_ok) {
+        const size_t nX = (size_t)2 * 8 * c.n_embd, nLG = (size_t)8 * c.n_expert, nH = (size_t)8 * c.n_ff;
+        rc = rc ? rc : dev_alloc((void **)&h->pX, sizeof(uint64_t) * nX);
+        rc = rc ? rc : dev_alloc((void **)&h->pLG, sizeof(uint64_t) * nLG);
+        rc = rc ? rc : dev_alloc((void **)&h->pH, sizeof(uint64_t) * nH);
+        rc = rc ? rc : dev_alloc((void **)&h->pY, sizeof(uint64_t) * nX);
+        const size_t flag_words = (size_t)8 * 32;
+        rc = rc ? rc : dev_alloc((void **)&h->pflags, flag_words * sizeof(unsigned));
+        if (rc) return rc;
+        HIP_TRY(hipMemset(h->pX, 0, sizeof(uint64_t) * nX));
+        HIP_TRY(hipMemset(h->pLG, 0, sizeof(uint64_t) * nLG));
+        HIP_TRY(hipMemset(h->pH, 0, sizeof(uint64_t) * nH));
+        HIP_TRY(hipMemset(h->pY, 0, sizeof(uint64_t) * nX));
+        HIP_TRY(hipMemset(h->pflags, 0, flag_words * sizeof(unsigned)));
+    }
+    if (h->spread_ok) {
+        const size_t nX = (size_t)c.n_embd, nLG = (size_t)c.n_expert;
+        const size_t nH = (size_t)(c.n_used + (c.n_ff_shexp > 0 ? 1 : 0)) * c.n_ff;
+        rc = rc ? rc : dev_alloc((void **)&h->sX, sizeof(uint64_t) * nX);
+        rc = rc ? rc : dev_alloc((void **)&h->sLG, sizeof(uint64_t) * nLG);
+        rc = rc ? rc : dev_alloc((void **)&h->sH, sizeof(uint64_t) * nH);
+        if (rc) return rc;
+        HIP_TRY(hipMemset(h->sX, 0, sizeof(uint64_t) * nX));
+        HIP_TRY(hipMemset(h->sLG, 0, sizeof(uint64_t) * nLG));
+        HIP_TRY(hipMemset(h->sH, 0, sizeof(uint64_t) * nH));
+    }
+    return HOARD_OK;
+}
+
+// The rows-spread one-launch decode over [l0, l1); the layer table is current.
+template <class Skip>
+int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t s, bool *used, Skip skip) {
+    const hoard_moe_cfg &c = h->cfg;
+    const bool sh = c.n_ff_shexp > 0;
+    for (int l = l0; l < l1; ++l) {
+        const Layer &L = h->layers[l];
+        if (L.gate_type != HOARD_TYPE_Q4_K || L.down_type != HOARD_TYPE_Q6_K)
+            return skip("rows-spread decode takes Q4_K gate/up and Q6_K down");
+        if (sh) {
+            if (L.sh_gate_type != HOARD_TYPE_Q4_K || L.sh_up_type != HOARD_TYPE_Q4_K ||
+                L.sh_down_type != HOARD_TYPE_Q6_K)
+                return skip("rows-spread decode takes a Q4_K/Q4_K/Q6_K shared expert");
+            const uintptr_t al = reinterpret_cast<uintptr_t>(L.sh_gate) | reinterpret_cast<uintptr_t>(L.sh_up) |
+                                 reinterpret_cast<uintptr_t>(L.sh_down) | reinterpret_cast<uintptr_t>(L.sh_gate_inp);
+            if (al & 15) return skip("shared expert tensors are not 16-byte aligned");
+        }
+        if (reinterpret_cast<uintptr_t>(L.router) & 15) return skip("router is not 16-byte aligned");
+    }
+    hoard::SpreadArgs a = spread_shape(c);
+    a.layers = h->d_table;
+    a.l0 = l0;
+    a.l1 = l1;
+    a.x = x;
+    a.eps = eps;
+    a.renorm = c.renorm;
+    a.LG = h->sLG;
+    a.H = h->sH;
+    a.X = h->sX;
+    a.err = h->perr;
+    a.seq0 = h->seq;
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_DECODE, s);
+        e = hoard::launch_spread_decode(a, s);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        if (h->persistent_mode == 2) return fail(HOARD_ERR_HIP, "spread decode launch: %s", hipGetErrorString(e));
+        return HOARD_OK;  // auto mode: fall back to the per-layer kernels
+    }
+    h->seq += 4u * (unsigned)(l1 - l0) + 4u;
+    *used = true;
     return HOARD_OK;
 }
 
@@ -444,6 +526,21 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
                              reinterpret_cast<uintptr_t>(L.down) | L.gstride | L.ustride | L.dstride;
         if (al & 15) return skip("expert tensors are not 16-byte aligned");
     }
+    // auto picks the expert-per-XCD kernel where it applies, else the rows-spread one
+    const bool spread = h->decode_kernel == 2 || (h->decode_kernel == 0 && !h->xcd_ok);
+    if (spread ? !h->spread_ok : !h->xcd_ok) return skip("the selected decode kernel does not take this shape");
+    if (h->table_dirty) {
+        std::vector<hoard::DecodeLayer> t(c.n_layer);
+        for (int l = 0; l < c.n_layer; ++l) {
+            const Layer &L = h->layers[l];
+            t[l] = hoard::DecodeLayer{L.router,   L.gate,      L.up,        L.down,        L.gstride,
+                                      L.ustride,  L.dstride,   L.gate_type, L.up_type,     L.down_type,
+                                      L.sh_gate,  L.sh_up,     L.sh_down,   L.sh_gate_inp};
+        }
+        HIP_TRY(hipMemcpy(h->d_table, t.data(), sizeof(hoard::DecodeLayer) * t.size(), hipMemcpyHostToDevice));
+        h->table_dirty = false;
+    }
+    if (spread) return spread_decode(h, l0, l1, x, eps, s, used, skip);
     if (!hoard::persistent_shape_compiled(gu_type, c.n_embd, d_type, c.n_ff))
         return skip("no kernel instantiated for these types and sizes");
     const int max_rb_gu = (int)mat_bytes(gu_type, 1, c.n_embd), max_rb_d = (int)mat_bytes(d_type, 1, c.n_ff);
@@ -464,16 +561,6 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     a.gu_type = gu_type;
     a.d_type = d_type;
     if (hoard::persistent_lds_bytes(a) > hoard::kPersistentMaxLds) return skip("LDS footprint too large");
-    if (h->table_dirty) {
-        std::vector<hoard::DecodeLayer> t(c.n_layer);
-        for (int l = 0; l < c.n_layer; ++l) {
-            const Layer &L = h->layers[l];
-            t[l] = hoard::DecodeLayer{L.router, L.gate, L.up, L.down, L.gstride, L.ustride, L.dstride,
-                                      L.gate_type, L.up_type, L.down_type};
-        }
-        HIP_TRY(hipMemcpy(h->d_table, t.data(), sizeof(hoard::DecodeLayer) * t.size(), hipMemcpyHostToDevice));
-        h->table_dirty = false;
-    }
     a.layers = h->d_table;
     a.X = h->pX;
     a.LG = h->pLG;
@@ -859,6 +946,12 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
             return fail(HOARD_ERR_UNSUPPORTED, "shape or device does not admit the persistent decode");
         h->persistent_mode = value;
         return HOARD_OK;
+    case HOARD_OPT_DECODE_KERNEL:
+        if (value < 0 || value > 2) return fail(HOARD_ERR_INVALID, "decode kernel %d", value);
+        if ((value == 1 && !h->xcd_ok) || (value == 2 && !h->spread_ok))
+            return fail(HOARD_ERR_UNSUPPORTED, "decode kernel %d does not take this shape or device", value);
+        h->decode_kernel = value;
+        return HOARD_OK;
     case HOARD_OPT_POOL_NAIVE:
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "pool naive flag %d", value);
         if (value && h->cfg.pool_k > 0) {
@@ -883,6 +976,12 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
         return HOARD_OK;
     case HOARD_OPT_POOL_NAIVE:
         *value = h->pool_naive ? 1 : 0;
+        return HOARD_OK;
+    case HOARD_OPT_DECODE_KERNEL:
+        *value = h->decode_kernel;
+        return HOARD_OK;
+    case HOARD_OPT_DECODE_KERNELS_AVAILABLE:
+        *value = (h->xcd_ok ? 1 : 0) | (h->spread_ok ? 2 : 0);
         return HOARD_OK;
     default:
         return fail(HOARD_ERR_INVALID, "unknown option %d", option);

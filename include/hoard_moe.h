@@ -177,6 +177,15 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
 /* HOARD_OPT_POOL_NAIVE: 1 = the reference's "naive" mode (every selected
    expert is uploaded into slot j on every call, :417), 0 = LRU (default). */
 #define HOARD_OPT_POOL_NAIVE 3
+/* HOARD_OPT_DECODE_KERNEL picks the one-launch decode kernel: 0 = auto (the
+   expert-per-XCD kernel where it applies, else the rows-spread one), 1 = the
+   expert-per-XCD kernel (k = 8 routed experts of E <= 128, one per XCD, no
+   shared expert), 2 = the rows-spread kernel (each selected expert's rows, and
+   a shared expert's, spread over all 256 CUs; Qwen3-Next-shaped layers).
+   HOARD_OPT_DECODE_KERNELS_AVAILABLE (read-only) is a mask: bit 0 the first,
+   bit 1 the second. */
+#define HOARD_OPT_DECODE_KERNEL 4
+#define HOARD_OPT_DECODE_KERNELS_AVAILABLE 5
 int hoard_moe_set_option(hoard_moe *h, int option, int value);
 int hoard_moe_get_option(hoard_moe *h, int option, int *value);
 

@@ -187,13 +187,64 @@ def test_persistent_decode_matches_oracle_and_launch_path(orc, shape):
         st.close()
 
 
-def test_persistent_decode_unavailable_shape_falls_back():
+@pytest.mark.parametrize("shape,kernel", [(W.QWEN3_NEXT, 0), (W.QWEN3_30B, 2)],
+                         ids=["qwen3_next-auto", "qwen3_30b-spread"])
+def test_spread_decode_matches_oracle_and_launch_path(orc, shape, kernel):
+    """One-launch decode with every expert's rows spread over all CUs (router over all
+    E, top-k of up to 512, shared expert, combine, rms_norm) against the oracle layer by
+    layer, the whole range in one launch against the layer-by-layer chain, and both
+    against the per-layer launch path."""
     import hoard_amd as H
-    shape = W.QWEN3_NEXT  # shared expert + 512 experts: per-layer launches
+    nl = 3
+    layers = {l: W.make_layer(shape, 1, l) for l in range(nl)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_PERSISTENT_AVAILABLE) == 1
+        assert st.get_option(H.OPT_DECODE_KERNELS_AVAILABLE) & 2
+        st.set_option(H.OPT_DECODE_KERNEL, kernel)
+        st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+        for tok in range(3):
+            _, x = W.make_hidden(shape, 1, 0, tok)
+            xs = [x]
+            for l in range(nl):
+                print(f"spread {shape.name} token {tok} layer {l}", flush=True)
+                xs.append(st.decode(xs[-1], l, l + 1, W.RMS_EPS))
+                st.sync_check()
+            for l in range(nl):
+                fx = orc.rms_norm(xs[l], W.RMS_EPS)
+                ref, _, _ = orc.moe_layer(layers[l], fx, xs[l])
+                m = parity.assert_parity(xs[l + 1], ref, f"spread {shape.name} tok {tok} layer {l}")
+                print("  ", m, flush=True)
+            print(f"spread {shape.name} token {tok} all layers", flush=True)
+            whole = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.sync_check()
+            assert np.array_equal(whole.view(np.uint32), xs[-1].view(np.uint32))
+            st.set_option(H.OPT_PERSISTENT_DECODE, 0)
+            launched = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+            parity.assert_parity(whole, launched, "spread vs per-layer launches")
+            if shape is W.QWEN3_30B:
+                st.set_option(H.OPT_DECODE_KERNEL, 1)
+                per_xcd = st.decode(xs[0], 0, nl, W.RMS_EPS)
+                st.sync_check()
+                st.set_option(H.OPT_DECODE_KERNEL, kernel)
+                parity.assert_parity(whole, per_xcd, "spread vs expert-per-XCD kernel")
+    finally:
+        st.close()
+
+
+def test_persistent_decode_unavailable_shape_falls_back():
+    import dataclasses
+
+    import hoard_amd as H
+    shape = dataclasses.replace(W.QWEN3_NEXT, n_used=6)  # top-6 of 512: no one-launch kernel
     st = _stage(shape, {0: W.make_layer(shape, 0, 0, experts=[])})
     try:
         assert st.get_option(H.OPT_PERSISTENT_AVAILABLE) == 0
+        assert st.get_option(H.OPT_DECODE_KERNELS_AVAILABLE) == 0
         with pytest.raises(H.HoardError):
             st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+        with pytest.raises(H.HoardError):
+            st.set_option(H.OPT_DECODE_KERNEL, 2)
     finally:
         st.close()
