@@ -7,20 +7,27 @@
 // router tail (src/run_qwen35.cpp:554-580), graph B with the shared expert
 // (:640-665) and the host combine (:675-676), with no host round trip.
 //
-// Per layer, workgroup g (of 256) owns
-//   * router rows [RR*g, RR*g + RR) (RR = E/256), prefetched into LDS while
-//     the previous layer finishes;
-//   * routed h rows [HR*g, HR*g + HR) of the concatenated h of the k selected
-//     experts (HR = k*ff/256; a range may cross from one expert into the next)
-//     and shared-expert h rows [HS*g, HS*g + HS);
-//   * output rows [8g, 8g + 8): their down rows for every selected expert and
-//     the shared one, so the weighted combine of those rows needs no further
-//     exchange.
-// Three all-to-all exchanges per layer, in device-scope words {value, seq}:
-// the logits (E words), h ((k+1)*ff words) and x (n_embd words).  Each is a
-// full barrier between the phases either side of it, so one buffer per
-// exchange suffices: a workgroup can only overwrite a word of layer l with
-// layer l+1's after every workgroup has read it.
+// The U = k (+1 with a shared expert) expert units are laid end to end.
+// Workgroup g = 32*xcd + rank (of 256) owns, per layer,
+//   * router rows [RR*g, RR*g + RR) (RR = E/256);
+//   * routed h rows [HR*g, HR*g + HR) of the k selected experts' h laid end
+//     to end (HR = k*ff/256; a range may cross from one expert into the
+//     next) and shared-expert h rows [HS*g, HS*g + HS);
+//   * U blocks of 8 down rows, blocks U*g .. U*g + U-1 of the U*256 blocks
+//     laid out unit by unit: rows of at most two units, so it needs the h
+//     of at most two experts;
+//   * the combine of output rows [64*rank, 64*rank + 64), which every XCD
+//     forms for itself from the expert outputs y of all units.
+// Exchanges, as {value, seq} words:
+//   logits  all-to-all across XCDs, pushed into one mailbox per workgroup
+//           (a line polled by many workgroups queues on the few memory
+//           channels that hold it);
+//   h       per unit, producers to the ~24 workgroups holding its down rows;
+//   y       every row to the 8 workgroups (one per XCD) that combine it;
+//   x       inside each XCD, through its L2.
+// No buffer needs a second copy for the next layer: before any workgroup
+// writes a word of layer l+1, the exchanges in between have made every
+// reader of layer l's word read it.
 //
 // Top-k over E <= 512 probabilities: one per thread, keyed (probability bits,
 // inverted index) so larger keys come first and ties go to the lower index;
@@ -40,10 +47,13 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kGroups = 256;  // workgroups, one per CU
+constexpr int kXcds = 8;
+constexpr int kPerXcd = 32;
+constexpr int kFlagStride = 32;   // ticket counters one 128-byte line apart
 
 constexpr int align16(int v) { return (v + 15) & ~15; }
 
-// LDS layout of one instantiation (byte offsets, 16-byte aligned).
+// Shape constants and LDS layout of one instantiation (byte offsets, 16-byte aligned).
 template <int NB, int NBH, int K, int E, bool SH>
 struct SpreadShape {
     static constexpr int kEmbd = NB * QK;
@@ -51,41 +61,46 @@ struct SpreadShape {
     static constexpr int U = K + (SH ? 1 : 0);          // expert units: routed slots, then the shared expert
     static constexpr int HR = K * kFF / kGroups;        // routed h rows per workgroup
     static constexpr int HS = SH ? kFF / kGroups : 0;   // shared h rows per workgroup
-    static constexpr int NH = U * kFF;                  // h words exchanged
+    static constexpr int NH = U * kFF;                  // h words
     static constexpr int RR = E >= kGroups ? E / kGroups : 1;  // router rows per workgroup
-    static constexpr int DR = kEmbd / kGroups;          // output rows per workgroup
+    static constexpr int BLK = 8;                       // rows per down block
+    static constexpr int NBLK = kEmbd / BLK;            // down blocks per unit
+    static constexpr int NDR = U * BLK;                 // down rows per workgroup (U blocks)
+    static constexpr int RC = kEmbd / kPerXcd;          // combined rows per workgroup
     static constexpr int RBG = NB * kQ4KBytes;          // gate/up row bytes
     static constexpr int RBD = NBH * kQ6KBytes;         // down row bytes
-    static constexpr int NGU = 2 * HR + 2 * HS;         // gate/up rows dotted per workgroup
+    static constexpr int NGU = 2 * HR;                  // routed gate/up rows dotted per workgroup
+    static constexpr int kGuWaves = (NGU + 7) / 8;      // waves with gate/up rows (8 per wave)
+    static constexpr bool kTwoCopyWaves = kGuWaves <= 5;  // wave 5 free to copy a second down segment
     static constexpr int kCand = 8 * K;                 // top-k candidates, k per wave
-    static constexpr int kHalfRows = U * DR / 2;        // down rows of one parity
-    static constexpr int kGatherH = (NH + 383) / 384;   // h words per gathering thread (waves 0-5)
+    static constexpr int kGatherH = 2 * kFF / 256;      // h words per gathering thread (waves 0-3, two units)
 
     static_assert(NB == 8, "one 8-lane group per gate/up row, one lane per super-block");
     static_assert((K * kFF) % kGroups == 0 && (!SH || kFF % kGroups == 0), "h rows split evenly");
     static_assert(E <= kThreads && (E % kGroups == 0 || kGroups % E == 0) && RR <= 2, "router rows per workgroup");
     static_assert(K <= 16 && K <= E && 4 * kCand <= kThreads, "top-k");
-    static_assert(DR % 2 == 0 && kEmbd % kGroups == 0, "output rows split evenly, in parity pairs");
+    static_assert(NBLK == kGroups && U <= NBLK, "U down blocks per workgroup, from at most two units");
     static_assert(NGU <= 48, "gate/up rows on waves 0-5");
-    static_assert(HR + HS <= 64, "h published by one wave");
+    static_assert(HR <= 64 && 2 * HS <= 8, "h published by one wave; shared rows on one wave");
+    static_assert(RC == 64 && U <= 16, "one combined row per lane of one wave");
+    static_assert(2 * NBH <= 6, "Q8_K(h) of two units on waves 0-5");
+    static_assert((BLK * RBD) % 16 == 0, "down segments start 16-byte aligned");
 
     static constexpr int oXS = 0;
     static constexpr int oWR = oXS + 4 * kEmbd;
     static constexpr int oSGR = oWR + 4 * RR * kEmbd;
     static constexpr int oSHGU = oSGR + (SH ? 4 * kEmbd : 0);
-    static constexpr int oSHD = align16(oSHGU + 2 * HS * RBG);
-    static constexpr int oGU = align16(oSHD + (SH ? DR * RBD : 0));
+    static constexpr int oGU = align16(oSHGU + 2 * HS * RBG);
     static constexpr int oDN = align16(oGU + 2 * HR * RBG);
-    static constexpr int oQ8X = align16(oDN + K * DR * RBD);
+    static constexpr int oQ8X = align16(oDN + NDR * RBD);
     static constexpr int oQ8H = oQ8X + (int)sizeof(Q8L) * NB;
-    static constexpr int oLG = oQ8H + (int)sizeof(Q8L) * U * NBH;
+    static constexpr int oHB = oQ8H + (int)sizeof(Q8L) * 2 * NBH;
+    static constexpr int oLG = oHB + 4 * 2 * kFF;
     static constexpr int oKEY = oLG + 4 * kThreads;
     static constexpr int oCAND = oKEY + 8 * kThreads;
     static constexpr int oGUV = oCAND + 8 * kCand;
     static constexpr int oYS = align16(oGUV + 4 * NGU);
-    static constexpr int kBytes = align16(oYS + 4 * U * DR);
-    static_assert((DR * RBD) % 16 == 0, "per-expert down segments stay 16-byte aligned");
-    static_assert(4 * NH <= 2 * HR * RBG, "h is gathered over the consumed gate/up rows");
+    static constexpr int kBytes = align16(oYS + 4 * NDR);
 };
 
 // Copy nbytes (a multiple of 16) from src to LDS at dst as 1 KB chunks.  The
@@ -127,7 +142,8 @@ __device__ __forceinline__ float half_wave_dot(const float *w, const float *x, f
 template <int NB, int NBH, int K, int E, bool SH>
 __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     using S = SpreadShape<NB, NBH, K, E, SH>;
-    constexpr int kEmbd = S::kEmbd, kFF = S::kFF, HR = S::HR, HS = S::HS, NH = S::NH, RR = S::RR, DR = S::DR;
+    constexpr int kEmbd = S::kEmbd, kFF = S::kFF, U = S::U, HR = S::HR, HS = S::HS, RR = S::RR;
+    constexpr int BLK = S::BLK, NBLK = S::NBLK, NDR = S::NDR, RC = S::RC;
     constexpr int RBG = S::RBG, RBD = S::RBD, NGU = S::NGU, kCand = S::kCand;
 
     extern __shared__ __align__(16) uint8_t smem[];
@@ -136,32 +152,51 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
     __shared__ float sg_s;
-    __shared__ int fail_s;
+    __shared__ int fail_s, rank_s;
+    __shared__ unsigned gu_done;  // waves 0-5 done with their gate/up rows, counted over layers
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int grp = tid >> 3, t8 = tid & 7;
-    const int g = blockIdx.x;
+    const unsigned xcc = xcc_id();
+    if (tid == 0) {
+        const unsigned t = __hip_atomic_fetch_add(a.tickets + xcc * kFlagStride, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        rank_s = (int)(t % kPerXcd);
+        fail_s = 0;
+        gu_done = 0;
+    }
+    __syncthreads();
+    const int rank = rank_s;
+    const int g = (int)xcc * kPerXcd + rank;
+
     float *xs = reinterpret_cast<float *>(smem + S::oXS);
     const float *wr = reinterpret_cast<const float *>(smem + S::oWR);
-    float *hb = reinterpret_cast<float *>(smem + S::oGU);  // gathered h, over the consumed gate/up rows
     Q8L *q8x = reinterpret_cast<Q8L *>(smem + S::oQ8X);
     Q8L *q8h = reinterpret_cast<Q8L *>(smem + S::oQ8H);
+    float *hb = reinterpret_cast<float *>(smem + S::oHB);
     float *lgv = reinterpret_cast<float *>(smem + S::oLG);
     uint64_t *keys = reinterpret_cast<uint64_t *>(smem + S::oKEY);
     uint64_t *cand = reinterpret_cast<uint64_t *>(smem + S::oCAND);
     float *guv = reinterpret_cast<float *>(smem + S::oGUV);
     float *ys = reinterpret_cast<float *>(smem + S::oYS);
 
-    // this workgroup's routed h rows: unit u0 rows [r0, r0 + n0), then unit u0 + 1 rows [0, n1)
+    // routed h rows: unit u0 rows [r0, r0 + n0), then unit u0 + 1 rows [0, n1)
     const int h0 = g * HR, u0 = h0 / kFF, r0 = h0 % kFF;
     const int n0 = HR < kFF - r0 ? HR : kFF - r0, n1 = HR - n0;
+    // down blocks: unit ua blocks [ba, ba + na), then unit ua + 1 blocks [0, nbb)
+    const int q0 = g * U, ua = q0 / NBLK, ba = q0 % NBLK;
+    const int na = U < NBLK - ba ? U : NBLK - ba, nbb = U - na;
+    const int nunits = nbb ? 2 : 1;  // units whose h this workgroup needs
     const int rrow0 = g * RR;
     const bool has_router = rrow0 < E;
 
-    if (tid == 0) fail_s = 0;
+    // phase stamps: [layer][workgroup][phase], by thread 0
+    auto stamp = [&](int l, int phase) {
+        if (a.trace && tid == 0) a.trace[((size_t)(l - a.l0) * kGroups + g) * kTracePhases + phase] = wall_clock64();
+    };
 
-    // Router rows, and the shared expert's gate row, gate/up rows and down rows,
-    // of layer l: none depends on the routing.
+    // Router rows, the shared expert's gate row and gate/up rows of layer l:
+    // none depends on the routing.
     auto prefetch = [&](int l, int w0, int nw) {
         if (wave < w0 || wave >= w0 + nw) return;
         const DecodeLayer &L = a.layers[l];
@@ -174,7 +209,6 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             b = dma_seg(smem + S::oSGR, reinterpret_cast<const uint8_t *>(L.sh_gate_inp), 4 * kEmbd, b, wrel, nw);
             b = dma_seg(smem + S::oSHGU, L.sh_gate + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
             b = dma_seg(smem + S::oSHGU + HS * RBG, L.sh_up + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
-            b = dma_seg(smem + S::oSHD, L.sh_down + (size_t)g * DR * RBD, DR * RBD, b, wrel, nw);
         }
     };
 
@@ -190,20 +224,23 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         const DecodeLayer &L = a.layers[l];
         const unsigned seq = a.seq0 + 4u * (unsigned)(l - a.l0);
         const bool last = l + 1 == a.l1;
+        stamp(l, 0);
 
-        // -- x of this layer: waves 4-7 gather it; waves 0-3 prefetched this layer's rows --
+        // -- x of this layer, from this XCD's combine: waves 4-7 gather it (waves 0-3
+        //    issued the prefetch of this layer's rows) --
         if (l > a.l0) {
             ss = 0.0;
             if (wave >= 4) {
                 const int t4 = tid - 256;
+                const uint64_t *xsrc = a.X + (size_t)xcc * kEmbd;
                 uint64_t w[8];
                 const bool got = poll(
                     [&]() {
                         bool r = true;
 #pragma unroll
-                        for (int c = 0; c < 8; ++c) w[c] = ld_dev64(a.X + t4 + 256 * c);
+                        for (int c = 0; c < 8; ++c) w[c] = ld_l2(xsrc + t4 + 256 * c);
 #pragma unroll
-                        for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 2u);
+                        for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 1u);
                         return r;
                     },
                     a.err);
@@ -220,6 +257,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         ss = wave_sum_d(ss);
         if (lane == 0) red_ss[wave] = ss;
         lds_barrier();
+        stamp(l, 1);
 
         // rms_norm scale; fx = x*scale is formed where it is read
         float scale;
@@ -234,9 +272,15 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         // -- router rows (wave 4), shared gate (wave 5), Q8_K(fx) (waves 4-7); logits gathered by waves 0-3 --
         if (wave == 4 && has_router) {
             const int row = lane >> 5;
-            if (row < RR && rrow0 + row < E) {
-                const float r = half_wave_dot<kEmbd>(wr + (size_t)row * kEmbd, xs, scale);
-                if ((lane & 31) == 0) st_dev64(a.LG + rrow0 + row, tag(r, seq));
+            float r = 0.0f;
+            if (row < RR && rrow0 + row < E) r = half_wave_dot<kEmbd>(wr + (size_t)row * kEmbd, xs, scale);
+            // each half-wave's lane 0 holds its row; lane c writes them to mailboxes c + 64i
+            const float r0 = readlane_f(r, 0), r1 = readlane_f(r, 32);
+#pragma unroll
+            for (int i = 0; i < kGroups / 64; ++i) {
+                uint64_t *mb = a.LG + (size_t)(lane + 64 * i) * E + rrow0;
+                st_dev64(mb, tag(r0, seq));
+                if (RR > 1 && rrow0 + 1 < E) st_dev64(mb + 1, tag(r1, seq));
             }
         }
         if constexpr (SH) {
@@ -254,11 +298,12 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         } else {
             const int i0 = tid, i1 = tid + 256;
             const int j0 = i0 < E ? i0 : 0, j1 = i1 < E ? i1 : 0;
+            const uint64_t *lsrc = a.LG + (size_t)g * E;  // this workgroup's mailbox
             uint64_t w0 = 0, w1 = 0;
             const bool got = poll(
                 [&]() {
-                    w0 = ld_dev64(a.LG + j0);
-                    w1 = ld_dev64(a.LG + j1);
+                    w0 = ld_dev64(lsrc + j0);
+                    w1 = ld_dev64(lsrc + j1);
                     return (bool)__all((tag_seq(w0) == seq) & (tag_seq(w1) == seq));
                 },
                 a.err);
@@ -270,6 +315,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             if (lane == 0) red_mx[wave] = m;
         }
         lds_barrier();
+        stamp(l, 2);
 
         // -- softmax over all E (thread t: expert t), then the top-k --
         float pt;
@@ -317,6 +363,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             }
         }
         lds_barrier();
+        stamp(l, 3);
 
         // -- waves 0-5 stream this workgroup's routed gate/up rows into LDS --
         auto expert = [&](int u) {
@@ -344,52 +391,74 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every lane's reads precede the writes
             if (lane < K) w_s[lane] = wj;
+            if constexpr (SH) {
+                // the shared expert's gate/up rows (prefetched) while the routed rows
+                // stream in: its h goes out a phase early
+                const int sr = lane >> 3;  // rows: HS gate, then HS up
+                float v = 0.0f;
+                if (sr < 2 * HS) {
+                    Q8Reg xr;
+                    load_q8reg(q8x[t8], xr);
+                    v = lpb_row_q4k<NB>(smem + S::oSHGU + sr * RBG, xr, t8);
+                }
+                // row sr's value is in lane 8*sr + 7
+#pragma unroll
+                for (int i = 0; i < HS; ++i) {
+                    const float gv = readlane_f(v, 8 * i + 7), uv = readlane_f(v, 8 * (HS + i) + 7);
+                    if (lane == i) st_dev64(a.H + K * kFF + g * HS + i, tag(gv / (1.0f + expf(-gv)) * uv, seq + 1u));
+                }
+            }
         }
         if (wave < 6) lds_dma_wait();
         lds_barrier();
+        stamp(l, 4);
 
-        // -- wave 6 streams the down rows (needed after the h exchange); waves 0-5 dot gate/up --
+        // -- gate/up rows on the first kGuWaves waves; wave 6 (and wave 5 when it has
+        //    no rows) streams the down rows; wave 7 publishes h once the row waves
+        //    have counted themselves done (no barrier: the copying waves may still
+        //    be issuing).  Rows of two experts are two segments in different pages:
+        //    where a second wave is free each goes out from its own wave, so their
+        //    address translations are not waited for one after the other. --
+        const uint8_t *srcA = ua < K ? L.down + (size_t)expert(ua) * L.dstride : L.sh_down;
+        const uint8_t *srcB = ua + 1 < K ? L.down + (size_t)expert(ua + 1) * L.dstride : L.sh_down;
         if (wave == 6) {
-            int b = 0;
-#pragma unroll 1
-            for (int u = 0; u < K; ++u)
-                b = dma_seg(smem + S::oDN + u * DR * RBD, L.down + (size_t)expert(u) * L.dstride + (size_t)g * DR * RBD,
-                            DR * RBD, b, 0, 1);
-        }
-        if (grp < NGU) {
-            Q8Reg xr;
-            load_q8reg(q8x[t8], xr);
-            const uint8_t *rp = grp < 2 * HR ? smem + S::oGU + grp * RBG : smem + S::oSHGU + (grp - 2 * HR) * RBG;
-            const float v = lpb_row_q4k<NB>(rp, xr, t8);
-            if (t8 == NB - 1) guv[grp] = v;
-        }
-        lds_barrier();
-
-        // -- h: published by wave 7, gathered whole by waves 0-5 --
-        if (wave == 7 && lane < HR + HS) {
-            float gv, uv;
-            int dst;
-            if (lane < HR) {
-                gv = guv[lane];
-                uv = guv[HR + lane];
-                dst = h0 + lane;
-            } else {
-                const int i = lane - HR;
-                gv = guv[2 * HR + i];
-                uv = guv[2 * HR + HS + i];
-                dst = K * kFF + g * HS + i;
+            const int b = dma_seg(smem + S::oDN, srcA + (size_t)ba * BLK * RBD, na * BLK * RBD, 0, 0, 1);
+            if (nbb && !S::kTwoCopyWaves) dma_seg(smem + S::oDN + na * BLK * RBD, srcB, nbb * BLK * RBD, b, 0, 1);
+        } else if (S::kTwoCopyWaves && wave == 5) {
+            if (nbb) dma_seg(smem + S::oDN + na * BLK * RBD, srcB, nbb * BLK * RBD, 0, 0, 1);
+        } else if (wave < S::kGuWaves) {
+            if (grp < NGU) {
+                Q8Reg xr;
+                load_q8reg(q8x[t8], xr);
+                const float v = lpb_row_q4k<NB>(smem + S::oGU + grp * RBG, xr, t8);
+                if (t8 == NB - 1) guv[grp] = v;
             }
-            st_dev64(a.H + dst, tag(gv / (1.0f + expf(-gv)) * uv, seq + 1u));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's guv writes precede its count
+            if (lane == 0) __hip_atomic_fetch_add(&gu_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else if (wave == 7) {
+            const unsigned target = (unsigned)S::kGuWaves * (unsigned)(l - a.l0 + 1);
+            const bool done = poll(
+                [&]() { return __hip_atomic_load(&gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target; },
+                a.err);
+            if (!done) fail_s = 1;
+            if (lane < HR) {
+                const float gv = guv[lane], uv = guv[HR + lane];
+                st_dev64(a.H + h0 + lane, tag(gv / (1.0f + expf(-gv)) * uv, seq + 1u));
+            }
         }
-        if (wave < 6) {
+        stamp(l, 5);
+
+        // -- h of the (at most two) units of this workgroup's down rows: waves 0-3 --
+        if (wave < 4) {
             uint64_t w[S::kGatherH];
+            const int lim = nunits * kFF;
             const bool got = poll(
                 [&]() {
                     bool r = true;
 #pragma unroll
                     for (int c = 0; c < S::kGatherH; ++c) {
-                        const int i = tid + 384 * c;
-                        w[c] = ld_dev64(a.H + (i < NH ? i : NH - 1));
+                        const int i = tid + 256 * c;
+                        w[c] = ld_dev64(a.H + ua * kFF + (i < lim ? i : lim - 1));
                     }
 #pragma unroll
                     for (int c = 0; c < S::kGatherH; ++c) r = r & (tag_seq(w[c]) == seq + 1u);
@@ -399,55 +468,88 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             if (!got) fail_s = 1;
 #pragma unroll
             for (int c = 0; c < S::kGatherH; ++c) {
-                const int i = tid + 384 * c;
-                if (i < NH) hb[i] = tag_val(w[c]);
+                const int i = tid + 256 * c;
+                if (i < lim) hb[i] = tag_val(w[c]);
             }
+            stamp(l, 10);
         }
-        if (wave == 6) lds_dma_wait();
+        if (wave == 6 || (S::kTwoCopyWaves && wave == 5)) {
+            lds_dma_wait();
+            if (wave == 6 && a.trace && lane == 0)
+                a.trace[((size_t)(l - a.l0) * kGroups + g) * kTracePhases + 11] = wall_clock64();
+        }
         lds_barrier();
+        stamp(l, 6);
 
-        // -- Q8_K(h) of every unit, then the down rows --
-        for (int b = wave; b < S::U * NBH; b += kWaves) wave_quantize_q8l(hb + b * QK, &q8h[b]);
+        // -- Q8_K(h) of those units, then the down rows --
+        if (wave < nunits * NBH) wave_quantize_q8l(hb + wave * QK, &q8h[wave]);
         lds_barrier();
+        stamp(l, 7);
         {
-            // a wave takes rows of one parity, so its rows share their 4-byte alignment
+            // local row i = 8*block + r; a wave takes rows of one parity, so its rows
+            // share their 4-byte alignment
             const int par = wave & 1;
             const int G = (wave >> 1) * 8 + (grp & 7);
 #pragma unroll
-            for (int pass = 0; pass < (S::kHalfRows + 31) / 32; ++pass) {
-                const int q = G + 32 * pass;
-                if (q < S::kHalfRows) {
-                    const int u = q / (DR / 2), i = 2 * (q % (DR / 2)) + par;
-                    const uint8_t *rp =
-                        (!SH || u < K) ? smem + S::oDN + (u * DR + i) * RBD : smem + S::oSHD + i * RBD;
-                    const float y = g8_row_q6k_u<NBH>(rp, q8h + u * NBH, t8);
-                    if (t8 == 0) ys[u * DR + i] = y;
+            for (int pass = 0; pass < (NDR / 2 + 31) / 32; ++pass) {
+                const int m = G + 32 * pass;
+                if (m < NDR / 2) {
+                    const int i = 2 * m + par;
+                    const int lu = (q0 + i / BLK) / NBLK - ua;  // 0 or 1
+                    const float y = g8_row_q6k_u<NBH>(smem + S::oDN + i * RBD, q8h + lu * NBH, t8);
+                    if (t8 == 0) ys[i] = y;
                 }
             }
         }
         lds_barrier();
+        stamp(l, 8);
 
-        // -- combine rows [8g, 8g + 8) over the slots in order, then the shared expert and residual --
-        if (wave == 0 && lane < DR) {
-            const int d = g * DR + lane;
+        // -- y rows out (wave 7); next layer's rows in (waves 1-3); combine (wave 0) --
+        if (wave == 7) {
+#pragma unroll
+            for (int i = lane; i < NDR; i += 64) {
+                const int q = q0 + i / BLK;
+                const int u = q / NBLK, d = (q % NBLK) * BLK + i % BLK;
+                st_dev64(a.Y + (size_t)u * kEmbd + d, tag(ys[i], seq + 2u));
+            }
+        }
+        if (!last) prefetch(l + 1, 1, 3);
+        if (wave == 0) {
+            // rows [64*rank, 64*rank + 64): units in order, then the shared expert and residual
+            const int d = rank * RC + lane;
+            uint64_t yw[U];
+            const bool got = poll2(
+                [&](uint64_t(&w)[U]) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) w[u] = ld_dev64(a.Y + (size_t)u * kEmbd + d);
+                },
+                [&](const uint64_t(&w)[U]) {
+                    bool r = true;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) r = r & (tag_seq(w[u]) == seq + 2u);
+                    return r;
+                },
+                yw, a.err);
+            if (!got) fail_s = 1;
             float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < K; ++j) acc = acc + w_s[j] * ys[j * DR + lane];
+            for (int j = 0; j < K; ++j) acc = acc + w_s[j] * tag_val(yw[j]);
             float o;
             if constexpr (SH)
-                o = (acc + ys[K * DR + lane] * sg_s) + xs[d];
+                o = (acc + tag_val(yw[K]) * sg_s) + xs[d];
             else
                 o = acc + xs[d];
-            if (last)
-                a.x[d] = o;
-            else
-                st_dev64(a.X + d, tag(o, seq + 2u));
+            if (last) {
+                if (xcc == 0) a.x[d] = o;
+            } else {
+                st_l2(a.X + (size_t)xcc * kEmbd + d, tag(o, seq + 3u));
+            }
         }
-        if (!last) prefetch(l + 1, 0, 4);
+        stamp(l, 9);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (fail_s && tid < DR) a.x[g * DR + tid] = __builtin_nanf("");  // the caller sees the failure
+    if (fail_s && xcc == 0 && tid < RC) a.x[rank * RC + tid] = __builtin_nanf("");  // the caller sees the failure
 }
 
 }  // namespace

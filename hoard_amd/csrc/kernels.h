@@ -141,11 +141,14 @@ struct SpreadArgs {
     int renorm;
     int n_embd, n_ff, E, k, shared;  // select the instantiation (shared: n_ff_shexp == n_ff)
     // exchanged values carry their sequence number: {float bits, seq} per 64-bit word
-    uint64_t *LG;               // [E]               router logits
-    uint64_t *H;                // [(k+shared)*n_ff] h of the routed experts, then the shared one
-    uint64_t *X;                // [n_embd]          x between layers
+    uint64_t *LG;               // [256][E]             router logits, one mailbox per workgroup
+    uint64_t *H;                // [(k+shared)*n_ff]    h of the routed experts, then the shared one
+    uint64_t *Y;                // [k+shared][n_embd]   expert outputs
+    uint64_t *X;                // [8][n_embd]          x between layers, one copy per XCD
+    unsigned *tickets;          // [8] counters, 128 B apart
     int *err;
     unsigned seq0;
+    unsigned long long *trace;  // optional [layer][256 workgroups][kTracePhases] wall-clock stamps
 };
 bool spread_shape_compiled(const SpreadArgs &a);
 hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s);

@@ -102,7 +102,8 @@ struct hoard_moe {
     bool table_dirty = true;
     hoard::DecodeLayer *d_table = nullptr;
     uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
-    uint64_t *sX = nullptr, *sLG = nullptr, *sH = nullptr;  // spread kernel's exchange words
+    uint64_t *sX = nullptr, *sLG = nullptr, *sH = nullptr, *sY = nullptr;  // spread kernel's exchange words
+    unsigned *sflags = nullptr;                                             // its tickets
     unsigned *pflags = nullptr;        // tickets
     int *perr = nullptr;
     unsigned seq = 1;
@@ -146,6 +147,8 @@ struct hoard_moe {
         hipFree(sX);
         hipFree(sLG);
         hipFree(sH);
+        hipFree(sY);
+        hipFree(sflags);
         hipFree(pflags);
         hipFree(perr);
         hipFree(ptrace);
@@ -445,16 +448,39 @@ int persistent_setup(hoard_moe *h) {
         HIP_TRY(hipMemset(h->pflags, 0, flag_words * sizeof(unsigned)));
     }
     if (h->spread_ok) {
-        const size_t nX = (size_t)c.n_embd, nLG = (size_t)c.n_expert;
-        const size_t nH = (size_t)(c.n_used + (c.n_ff_shexp > 0 ? 1 : 0)) * c.n_ff;
+        const size_t units = (size_t)c.n_used + (c.n_ff_shexp > 0 ? 1 : 0);
+        const size_t nX = (size_t)8 * c.n_embd, nLG = (size_t)256 * c.n_expert;
+        const size_t nH = units * c.n_ff, nY = units * c.n_embd, nF = (size_t)8 * 32;
         rc = rc ? rc : dev_alloc((void **)&h->sX, sizeof(uint64_t) * nX);
         rc = rc ? rc : dev_alloc((void **)&h->sLG, sizeof(uint64_t) * nLG);
         rc = rc ? rc : dev_alloc((void **)&h->sH, sizeof(uint64_t) * nH);
+        rc = rc ? rc : dev_alloc((void **)&h->sY, sizeof(uint64_t) * nY);
+        rc = rc ? rc : dev_alloc((void **)&h->sflags, sizeof(unsigned) * nF);
         if (rc) return rc;
         HIP_TRY(hipMemset(h->sX, 0, sizeof(uint64_t) * nX));
         HIP_TRY(hipMemset(h->sLG, 0, sizeof(uint64_t) * nLG));
         HIP_TRY(hipMemset(h->sH, 0, sizeof(uint64_t) * nH));
+        HIP_TRY(hipMemset(h->sY, 0, sizeof(uint64_t) * nY));
+        HIP_TRY(hipMemset(h->sflags, 0, sizeof(unsigned) * nF));
     }
+    return HOARD_OK;
+}
+
+// Phase-stamp buffer of a traced one-launch decode ([layer][256][kTracePhases]);
+// *out stays null while tracing is off.
+int trace_buffer(hoard_moe *h, int l0, int l1, unsigned long long **out) {
+    *out = nullptr;
+    if (!h->tracing) return HOARD_OK;
+    const int nl = h->cfg.n_layer;
+    if (h->trace_layers < (size_t)nl) {
+        hipFree(h->ptrace);
+        h->ptrace = nullptr;
+        int rc = dev_alloc((void **)&h->ptrace, sizeof(unsigned long long) * nl * 256 * hoard::kTracePhases);
+        if (rc) return rc;
+        h->trace_layers = nl;
+    }
+    *out = h->ptrace;
+    h->trace_last = l1 - l0;
     return HOARD_OK;
 }
 
@@ -486,9 +512,12 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
     a.renorm = c.renorm;
     a.LG = h->sLG;
     a.H = h->sH;
+    a.Y = h->sY;
     a.X = h->sX;
+    a.tickets = h->sflags;
     a.err = h->perr;
     a.seq0 = h->seq;
+    if (int rc = trace_buffer(h, l0, l1, &a.trace)) return rc;
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_DECODE, s);
@@ -569,17 +598,7 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     a.tickets = h->pflags;
     a.err = h->perr;
     a.seq0 = h->seq;
-    if (h->tracing) {
-        if (h->trace_layers < (size_t)c.n_layer) {
-            hipFree(h->ptrace);
-            h->ptrace = nullptr;
-            int rc = dev_alloc((void **)&h->ptrace, sizeof(unsigned long long) * c.n_layer * 256 * hoard::kTracePhases);
-            if (rc) return rc;
-            h->trace_layers = c.n_layer;
-        }
-        a.trace = h->ptrace;
-        h->trace_last = l1 - l0;
-    }
+    if (int rc = trace_buffer(h, l0, l1, &a.trace)) return rc;
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_DECODE, s);
