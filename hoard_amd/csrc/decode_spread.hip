@@ -276,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             if (row < RR && rrow0 + row < E) r = half_wave_dot<kEmbd>(wr + (size_t)row * kEmbd, xs, scale);
             // each half-wave's lane 0 holds its row; lane c writes them to mailboxes c + 64i
             const float r0 = readlane_f(r, 0), r1 = readlane_f(r, 32);
-#pragma unroll
+#pragma unroll 1
             for (int i = 0; i < kGroups / 64; ++i) {
                 uint64_t *mb = a.LG + (size_t)(lane + 64 * i) * E + rrow0;
                 st_dev64(mb, tag(r0, seq));
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's keys are in LDS
             const uint64_t *kw = keys + 64 * wave;
             int r1 = 0;
-#pragma unroll
+#pragma unroll 4
             for (int j = 0; j < 64; j += 2) {
                 const ulonglong2 kk = *reinterpret_cast<const ulonglong2 *>(kw + j);
                 r1 += (int)(kk.x > key) + (int)(kk.y > key);
@@ -396,11 +396,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 // stream in: its h goes out a phase early
                 const int sr = lane >> 3;  // rows: HS gate, then HS up
                 float v = 0.0f;
-                if (sr < 2 * HS) {
-                    Q8Reg xr;
-                    load_q8reg(q8x[t8], xr);
-                    v = lpb_row_q4k<NB>(smem + S::oSHGU + sr * RBG, xr, t8);
-                }
+                if (sr < 2 * HS) v = lpb_row_q4k_mem<NB>(smem + S::oSHGU + sr * RBG, q8x[t8], t8);
                 // row sr's value is in lane 8*sr + 7
 #pragma unroll
                 for (int i = 0; i < HS; ++i) {
@@ -428,9 +424,8 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             if (nbb) dma_seg(smem + S::oDN + na * BLK * RBD, srcB, nbb * BLK * RBD, 0, 0, 1);
         } else if (wave < S::kGuWaves) {
             if (grp < NGU) {
-                Q8Reg xr;
-                load_q8reg(q8x[t8], xr);
-                const float v = lpb_row_q4k<NB>(smem + S::oGU + grp * RBG, xr, t8);
+                // one row per 8-lane group: the lane reads its activation block as it goes
+                const float v = lpb_row_q4k_mem<NB>(smem + S::oGU + grp * RBG, q8x[t8], t8);
                 if (t8 == NB - 1) guv[grp] = v;
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's guv writes precede its count
@@ -518,18 +513,16 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             // rows [64*rank, 64*rank + 64): units in order, then the shared expert and residual
             const int d = rank * RC + lane;
             uint64_t yw[U];
-            const bool got = poll2(
-                [&](uint64_t(&w)[U]) {
+            const bool got = poll(
+                [&]() {
 #pragma unroll
-                    for (int u = 0; u < U; ++u) w[u] = ld_dev64(a.Y + (size_t)u * kEmbd + d);
-                },
-                [&](const uint64_t(&w)[U]) {
+                    for (int u = 0; u < U; ++u) yw[u] = ld_dev64(a.Y + (uint32_t)(u * kEmbd + d));
                     bool r = true;
 #pragma unroll
-                    for (int u = 0; u < U; ++u) r = r & (tag_seq(w[u]) == seq + 2u);
+                    for (int u = 0; u < U; ++u) r = r & (tag_seq(yw[u]) == seq + 2u);
                     return r;
                 },
-                yw, a.err);
+                a.err);
             if (!got) fail_s = 1;
             float acc = 0.0f;
 #pragma unroll
