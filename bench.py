@@ -85,9 +85,13 @@ def kernel_bytes(shape, kind: int, n_layer: int) -> int:
 PHASES = ["layer_start", "x_gathered", "router_rows_q8x", "router_rows_q8x_", "logits_gathered_topk",
           "loads_issued", "gateup_rows_landed", "h_published", "h_gathered_q8h", "down_y_published",
           "y_gathered_x_published", "y_gathered_x_published_"]
+# the rows-spread kernel's stamps (decode_spread.hip), in time order
+PHASES_SPREAD = ["layer_start", "x_gathered", "logits_gathered", "softmax_summed", "wave_candidates",
+                 "topk", "gateup_rows_landed", "wave0_gateup_done", "h_gathered", "q8h", "down_done",
+                 "combined_x_published"]
 
 
-def phase_breakdown(lib, h, step, H):
+def phase_breakdown(lib, h, step, H, names=PHASES):
     """Per-phase time of the one-launch decode: for each boundary, when the slowest
     workgroup reached it, relative to the previous boundary (median over layers)."""
     H.check(lib.hoard_moe_phase_trace(h, 1))
@@ -104,7 +108,7 @@ def phase_breakdown(lib, h, step, H):
     # phases 7..9 are skipped by workgroups without an expert; they hold 0 then
     d = np.diff(reach, axis=1) * 10e-3         # 100 MHz ticks -> us
     med = np.median(d[1:] if nl.value > 1 else d, axis=0)
-    out = {f"{PHASES[i]}->{PHASES[i + 1]}": round(float(med[i]), 3) for i in range(len(PHASES) - 1)}
+    out = {f"{names[i]}->{names[i + 1]}": round(float(med[i]), 3) for i in range(len(names) - 1)}
     out["layer_total"] = round(float(np.median((reach[1:, -1] - reach[1:, 0]) * 10e-3)) if nl.value > 1 else 0.0, 3)
     return out
 
@@ -474,12 +478,6 @@ def main():
                      "traffic": measured_traffic(shape, dom, n_layer),
                      "algorithmic_bytes": dk["bytes"]},
     }
-    if args.phases:
-        ph = phase_breakdown(lib, h, lambda: step(warm), H)
-        if ph:
-            result["phases_us"] = ph
-            for k_, v_ in ph.items():
-                log(f"[phase] {k_:40s} {v_:8.3f} us")
     persistent = ctypes.c_int()
     H.check(lib.hoard_moe_get_option(h, H.OPT_PERSISTENT_AVAILABLE, ctypes.byref(persistent)))
     avail = ctypes.c_int()
@@ -489,6 +487,12 @@ def main():
         ("one cooperative launch per token, " + ("expert rows spread over all CUs" if spread
                                                  else "one expert per XCD"))
         if persistent.value else "router, gate/up and down+combine launches per layer")
+    if args.phases:
+        ph = phase_breakdown(lib, h, lambda: step(warm), H, PHASES_SPREAD if spread else PHASES)
+        if ph:
+            result["phases_us"] = ph
+            for k_, v_ in ph.items():
+                log(f"[phase] {k_:40s} {v_:8.3f} us")
     lib.hoard_moe_destroy(h)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds)

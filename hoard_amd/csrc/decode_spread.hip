@@ -31,8 +31,9 @@
 //
 // Top-k over E <= 512 probabilities: one per thread, keyed (probability bits,
 // inverted index) so larger keys come first and ties go to the lower index;
-// each wave ranks its 64 keys, the k best of every wave (8k candidates) are
-// ranked against each other.
+// each wave finds its k best by a bitwise search for its k-th largest
+// probability, and the k best of every wave (8k candidates) are ranked against
+// each other.
 #include "exchange.h"
 #include "kernels.h"
 #include "lds_dma.h"
@@ -96,8 +97,7 @@ struct SpreadShape {
     static constexpr int oQ8H = oQ8X + (int)sizeof(Q8L) * NB;
     static constexpr int oHB = oQ8H + (int)sizeof(Q8L) * 2 * NBH;
     static constexpr int oLG = oHB + 4 * 2 * kFF;
-    static constexpr int oKEY = oLG + 4 * kThreads;
-    static constexpr int oCAND = oKEY + 8 * kThreads;
+    static constexpr int oCAND = oLG + 4 * kThreads;
     static constexpr int oGUV = oCAND + 8 * kCand;
     static constexpr int oYS = align16(oGUV + 4 * NGU);
     static constexpr int kBytes = align16(oYS + 4 * NDR);
@@ -175,7 +175,6 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     Q8L *q8h = reinterpret_cast<Q8L *>(smem + S::oQ8H);
     float *hb = reinterpret_cast<float *>(smem + S::oHB);
     float *lgv = reinterpret_cast<float *>(smem + S::oLG);
-    uint64_t *keys = reinterpret_cast<uint64_t *>(smem + S::oKEY);
     uint64_t *cand = reinterpret_cast<uint64_t *>(smem + S::oCAND);
     float *guv = reinterpret_cast<float *>(smem + S::oGUV);
     float *ys = reinterpret_cast<float *>(smem + S::oYS);
@@ -274,14 +273,10 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             const int row = lane >> 5;
             float r = 0.0f;
             if (row < RR && rrow0 + row < E) r = half_wave_dot<kEmbd>(wr + (size_t)row * kEmbd, xs, scale);
-            // each half-wave's lane 0 holds its row; lane c writes them to mailboxes c + 64i
+            // each half-wave's lane 0 holds its row; lanes 0-7 write row 0, lanes 8-15 row 1
             const float r0 = readlane_f(r, 0), r1 = readlane_f(r, 32);
-#pragma unroll 1
-            for (int i = 0; i < kGroups / 64; ++i) {
-                uint64_t *mb = a.LG + (size_t)(lane + 64 * i) * E + rrow0;
-                st_dev64(mb, tag(r0, seq));
-                if (RR > 1 && rrow0 + 1 < E) st_dev64(mb + 1, tag(r1, seq));
-            }
+            const int c = lane & 7, rr = lane >> 3;
+            if (rr < RR && rrow0 + rr < E) st_dev64(a.LG + (size_t)c * E + rrow0 + rr, tag(rr ? r1 : r0, seq));
         }
         if constexpr (SH) {
             if (wave == 5 && lane < 32) {
@@ -295,24 +290,32 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
                 wave_quantize_q8l_regs(v, &q8x[b]);
             }
-        } else {
-            const int i0 = tid, i1 = tid + 256;
-            const int j0 = i0 < E ? i0 : 0, j1 = i1 < E ? i1 : 0;
-            const uint64_t *lsrc = a.LG + (size_t)g * E;  // this workgroup's mailbox
-            uint64_t w0 = 0, w1 = 0;
+        } else if (wave == 0) {
+            // one wave polls the XCD's copy: fewer requests on its few lines
+            constexpr int kPer = (E + 63) / 64;
+            const uint64_t *lsrc = a.LG + (size_t)xcc * E;
+            uint64_t w[kPer];
             const bool got = poll(
                 [&]() {
-                    w0 = ld_dev64(lsrc + j0);
-                    w1 = ld_dev64(lsrc + j1);
-                    return (bool)__all((tag_seq(w0) == seq) & (tag_seq(w1) == seq));
+                    bool r = true;
+#pragma unroll
+                    for (int c = 0; c < kPer; ++c) w[c] = ld_dev64(lsrc + (lane + 64 * c < E ? lane + 64 * c : 0));
+#pragma unroll
+                    for (int c = 0; c < kPer; ++c) r = r & (tag_seq(w[c]) == seq);
+                    return (bool)__all(r);
                 },
                 a.err);
             if (!got) fail_s = 1;
-            const float v0 = i0 < E ? tag_val(w0) : -INFINITY, v1 = i1 < E ? tag_val(w1) : -INFINITY;
-            lgv[i0] = v0;
-            lgv[i1] = v1;
-            const float m = wave_max_f(v1 > v0 ? v1 : v0);
-            if (lane == 0) red_mx[wave] = m;
+            float m = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < kThreads / 64; ++c) {
+                const int i = lane + 64 * c;
+                const float v = c < kPer && i < E ? tag_val(w[c < kPer ? c : 0]) : -INFINITY;
+                lgv[i] = v;
+                m = v > m ? v : m;
+            }
+            m = wave_max_f(m);
+            if (lane == 0) red_mx[0] = red_mx[1] = red_mx[2] = red_mx[3] = m;
         }
         lds_barrier();
         stamp(l, 2);
@@ -327,6 +330,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             const double s = wave_sum_d((double)et);
             if (lane == 0) red_sum[wave] = s;
             lds_barrier();
+            stamp(l, 3);
             double tot = 0.0;
             for (int w = 0; w < kWaves; ++w) tot += red_sum[w];
             pt = et * (float)(1.0 / tot);
@@ -336,16 +340,25 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             // their bit patterns order as the values); absent experts rank last
             const uint64_t inv = (uint64_t)(0xFFFFu - (unsigned)tid);
             const uint64_t key = tid < E ? (((uint64_t)__float_as_uint(pt) << 16) | inv) : inv;
-            keys[tid] = key;
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's keys are in LDS
-            const uint64_t *kw = keys + 64 * wave;
-            int r1 = 0;
-#pragma unroll 4
-            for (int j = 0; j < 64; j += 2) {
-                const ulonglong2 kk = *reinterpret_cast<const ulonglong2 *>(kw + j);
-                r1 += (int)(kk.x > key) + (int)(kk.y > key);
+            // this wave's k best: the k-th largest probability bit pattern T by a
+            // bitwise search (32-bit compares), every lane above T, and of the lanes
+            // equal to T the lowest (lower lane = lower index) until there are k
+            const uint32_t pb = tid < E ? __float_as_uint(pt) : 0u;
+            uint32_t T = 0;
+#pragma unroll
+            for (int b = 31; b >= 0; --b) {
+                const uint32_t tc = T | (1u << b);
+                const uint64_t m = __builtin_amdgcn_ballot_w64(pb >= tc);
+                // two 32-bit counts keep the test on the scalar unit
+                const int cnt = __builtin_popcount((uint32_t)m) + __builtin_popcount((uint32_t)(m >> 32));
+                if (cnt >= K) T = tc;
             }
-            if (r1 < K) cand[wave * K + r1] = key;
+            const uint64_t lt = (1ull << lane) - 1ull;
+            const uint64_t eq = __builtin_amdgcn_ballot_w64(pb == T);
+            const int need = K - (int)__popcll(__builtin_amdgcn_ballot_w64(pb > T));
+            const bool in = pb > T || (pb == T && (int)__popcll(eq & lt) < need);  // exactly k lanes
+            if (in) cand[wave * K + __popcll(__builtin_amdgcn_ballot_w64(in) & lt)] = key;
+            stamp(l, 4);
         }
         lds_barrier();
         if (tid < 4 * kCand) {
@@ -363,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             }
         }
         lds_barrier();
-        stamp(l, 3);
+        stamp(l, 5);
 
         // -- waves 0-5 stream this workgroup's routed gate/up rows into LDS --
         auto expert = [&](int u) {
@@ -407,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         }
         if (wave < 6) lds_dma_wait();
         lds_barrier();
-        stamp(l, 4);
+        stamp(l, 6);
 
         // -- gate/up rows on the first kGuWaves waves; wave 6 (and wave 5 when it has
         //    no rows) streams the down rows; wave 7 publishes h once the row waves
@@ -441,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 st_dev64(a.H + h0 + lane, tag(gv / (1.0f + expf(-gv)) * uv, seq + 1u));
             }
         }
-        stamp(l, 5);
+        stamp(l, 7);
 
         // -- h of the (at most two) units of this workgroup's down rows: waves 0-3 --
         if (wave < 4) {
@@ -466,20 +479,15 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 const int i = tid + 256 * c;
                 if (i < lim) hb[i] = tag_val(w[c]);
             }
-            stamp(l, 10);
         }
-        if (wave == 6 || (S::kTwoCopyWaves && wave == 5)) {
-            lds_dma_wait();
-            if (wave == 6 && a.trace && lane == 0)
-                a.trace[((size_t)(l - a.l0) * kGroups + g) * kTracePhases + 11] = wall_clock64();
-        }
+        if (wave == 6 || (S::kTwoCopyWaves && wave == 5)) lds_dma_wait();
         lds_barrier();
-        stamp(l, 6);
+        stamp(l, 8);
 
         // -- Q8_K(h) of those units, then the down rows --
         if (wave < nunits * NBH) wave_quantize_q8l(hb + wave * QK, &q8h[wave]);
         lds_barrier();
-        stamp(l, 7);
+        stamp(l, 9);
         {
             // local row i = 8*block + r; a wave takes rows of one parity, so its rows
             // share their 4-byte alignment
@@ -497,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             }
         }
         lds_barrier();
-        stamp(l, 8);
+        stamp(l, 10);
 
         // -- y rows out (wave 7); next layer's rows in (waves 1-3); combine (wave 0) --
         if (wave == 7) {
@@ -538,7 +546,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 st_l2(a.X + (size_t)xcc * kEmbd + d, tag(o, seq + 3u));
             }
         }
-        stamp(l, 9);
+        stamp(l, 11);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
