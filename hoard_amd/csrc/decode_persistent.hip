@@ -103,6 +103,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     __shared__ int sh_rank, sh_fail;
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
+    __shared__ unsigned gu_done;   // gate/up row waves done, counted over layers
     __shared__ double red_d[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                                                   __HIP_MEMORY_SCOPE_AGENT);
         sh_rank = (int)(t % kPerXcd);
         sh_fail = 0;
+        gu_done = 0;
     }
     __syncthreads();
     const int rank = sh_rank;
@@ -372,28 +374,55 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             if (wave < kWaves / 2) __builtin_amdgcn_s_waitcnt(0);  // the gate/up chunks these waves issued
             lds_barrier();
             stamp(l, 6);
-            // the down rows are needed only after the h exchange: fetched now, after
-            // the gate/up rows, so that those did not share the bandwidth; issued by
-            // waves 6-7, which have no gate/up row when 2R <= 48
-            if (wave >= kWaves - 2)
-                for (int c = wave - (kWaves - 2); c < kDownChunks; c += 2)
-                    dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
-            {
-                // one 8-lane group per row, lane t holding Q8_K(x) block t
-                Q8Reg xr;
-                if (t8 < NB) load_q8reg(q8x[t8], xr);
+            // The down rows are needed only after the h exchange: fetched now, after
+            // the gate/up rows, so that those did not share the bandwidth.  With
+            // 2R <= 48 wave 6 has no gate/up row and copies them all, and wave 7
+            // publishes h once the row waves have counted themselves done: no
+            // barrier, so nothing waits for wave 6 to finish issuing its copies.
+            // Otherwise waves 6-7 copy them besides their rows and a barrier
+            // precedes the publish.
+            constexpr bool kCounted = 2 * kR <= 48;
+            constexpr int kGuWaves = (2 * kR + 7) / 8;
+            auto gateup_rows = [&]() {
+                // one 8-lane group per row; lane t reads Q8_K(x) block t as it goes
                 const int pr = grp;
                 if (pr < 2 * kR) {
                     const int mat = pr >= kR, row = pr - mat * kR;
                     const uint8_t *rp = mat ? smem + S.up + row * rbu : smem + S.gate + row * rbg;
-                    const float v = lpb_row_q4k<NB>(rp, xr, t8);
+                    const float v = lpb_row_q4k_mem<NB>(rp, q8x[t8 < NB ? t8 : 0], t8);
                     if (t8 == NB - 1) gu[pr] = v;
                 }
-            }
-            lds_barrier();
-            if (wave == kPublishWave && lane < R) {  // not a wave that polls h
-                const float g = gu[lane], uu = gu[R + lane];
-                st_l2(Hx + rank * R + lane, tag(g / (1.0f + expf(-g)) * uu, seq + 1u));
+            };
+            auto publish_h = [&]() {
+                if (lane < R) {
+                    const float g = gu[lane], uu = gu[R + lane];
+                    st_l2(Hx + rank * R + lane, tag(g / (1.0f + expf(-g)) * uu, seq + 1u));
+                }
+            };
+            if constexpr (kCounted) {
+                if (wave == kWaves - 2) {
+                    for (int c = 0; c < kDownChunks; ++c) dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+                } else if (wave < kGuWaves) {
+                    gateup_rows();
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's gu writes precede its count
+                    if (lane == 0) __hip_atomic_fetch_add(&gu_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                } else if (wave == kPublishWave) {  // not a wave that polls h
+                    const unsigned target = (unsigned)kGuWaves * (unsigned)(l - a.l0 + 1);
+                    const bool done = poll(
+                        [&]() {
+                            return __hip_atomic_load(&gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target;
+                        },
+                        a.err);
+                    if (!done) sh_fail = 1;
+                    publish_h();
+                }
+            } else {
+                if (wave >= kWaves - 2)
+                    for (int c = wave - (kWaves - 2); c < kDownChunks; c += 2)
+                        dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+                gateup_rows();
+                lds_barrier();
+                if (wave == kPublishWave) publish_h();  // not a wave that polls h
             }
             stamp(l, 7);
 
@@ -416,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
                 wave_quantize_q8l_regs(v, &q8h[wave]);
             }
-            __builtin_amdgcn_s_waitcnt(0);  // down rows landed (issued by waves 4-7)
+            __builtin_amdgcn_s_waitcnt(0);  // down rows landed
             lds_barrier();
             if (sh_fail) {
                 ok = false;
