@@ -40,8 +40,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--decode-kernel", default="auto", choices=["auto", "xcd", "spread"],
-                    help="one-launch decode kernel: expert-per-XCD, rows spread over all CUs, or auto")
+    ap.add_argument("--decode-kernel", default="auto", choices=["auto", "xcd", "spread", "launches"],
+                    help="one-launch decode kernel: expert-per-XCD, rows spread over all CUs, or auto; "
+                         "'launches' runs the per-layer kernels (hoard_moe_layer's path) instead")
     ap.add_argument("--phases", action="store_true", help="trace one-launch decode phases of one token")
     ap.add_argument("--pool", type=int, default=0, metavar="K",
                     help="slot-pool workload: K HBM slots per layer, all experts in pinned host memory, "
@@ -396,8 +397,12 @@ def main():
     cfg = shape.cfg(n_layer)
     h = ctypes.c_void_p()
     H.check(lib.hoard_moe_create(ctypes.byref(cfg), ctypes.byref(h)))
-    dk_opt = {"auto": H.DECODE_AUTO, "xcd": H.DECODE_XCD, "spread": H.DECODE_SPREAD}[args.decode_kernel]
-    H.check(lib.hoard_moe_set_option(h, H.OPT_DECODE_KERNEL, dk_opt))
+    if args.decode_kernel == "launches":
+        dk_opt = H.DECODE_AUTO
+        H.check(lib.hoard_moe_set_option(h, H.OPT_PERSISTENT_DECODE, 0))
+    else:
+        dk_opt = {"auto": H.DECODE_AUTO, "xcd": H.DECODE_XCD, "spread": H.DECODE_SPREAD}[args.decode_kernel]
+        H.check(lib.hoard_moe_set_option(h, H.OPT_DECODE_KERNEL, dk_opt))
     hl = W.make_layer(shape, args.seed, 0)
     for l in range(n_layer):
         if l:
@@ -486,7 +491,8 @@ def main():
     result["config"]["decode_path"] = (
         ("one cooperative launch per token, " + ("expert rows spread over all CUs" if spread
                                                  else "one expert per XCD"))
-        if persistent.value else "router, gate/up and down+combine launches per layer")
+        if persistent.value and args.decode_kernel != "launches"
+        else "router, gate/up and down+combine launches per layer")
     if args.phases:
         ph = phase_breakdown(lib, h, lambda: step(warm), H, PHASES_SPREAD if spread else PHASES)
         if ph:

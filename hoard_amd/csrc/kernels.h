@@ -153,6 +153,14 @@ struct SpreadArgs {
 bool spread_shape_compiled(const SpreadArgs &a);
 hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s);
 
+// Per-layer launches for the instantiated shapes (layer.hip); the *_ok tests
+// say whether they take the arguments, else the kernels above run.
+bool layer_route_ok(const RouterArgs &a);
+hipError_t launch_layer_route(const RouterArgs &a, hipStream_t s);
+bool layer_ffn_ok(const GateUpArgs &g, const DownArgs &d);
+hipError_t launch_layer_gateup(const GateUpArgs &g, hipStream_t s);
+hipError_t launch_layer_down(const DownArgs &d, hipStream_t s);
+
 size_t block_bytes(int type);
 
 }  // namespace hoard

@@ -99,6 +99,7 @@ struct hoard_moe {
     bool spread_ok = false;            // ... the rows-spread kernel
     int persistent_mode = 1;           // HOARD_OPT_PERSISTENT_DECODE value
     int decode_kernel = 0;             // HOARD_OPT_DECODE_KERNEL value
+    bool layer_kernels = true;         // HOARD_OPT_LAYER_KERNELS: instantiated per-layer kernels
     bool table_dirty = true;
     hoard::DecodeLayer *d_table = nullptr;
     uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
@@ -274,8 +275,10 @@ int run_route(hoard_moe *h, const Layer &L, const float *xin, int is_residual, f
     a.counters = h->counters;
     a.sel = sel;
     a.wsel = w;
+    const bool fast = h->layer_kernels && hoard::layer_route_ok(a) &&
+                      ((reinterpret_cast<uintptr_t>(xin) | reinterpret_cast<uintptr_t>(L.router)) & 15) == 0;
     KernelMark mark(h, HOARD_KERNEL_ROUTER, s);
-    HIP_TRY(hoard::launch_router(a, s));
+    HIP_TRY(fast ? hoard::launch_layer_route(a, s) : hoard::launch_router(a, s));
     return HOARD_OK;
 }
 
@@ -299,13 +302,6 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
     g.k = c.n_used;
     g.h = h->hbuf;
     g.hstride = h->hstride;
-    hipError_t e;
-    {
-        KernelMark mark(h, HOARD_KERNEL_GATEUP, s);
-        e = hoard::launch_gateup(g, s);
-    }
-    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "gate/up launch: %s", hipGetErrorString(e));
-
     hoard::DownArgs d{};
     d.h = h->hbuf;
     d.hstride = h->hstride;
@@ -318,9 +314,16 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
     d.k = c.n_used;
     d.res = res;
     d.out = out;
+    const bool fast = h->layer_kernels && hoard::layer_ffn_ok(g, d);
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_GATEUP, s);
+        e = fast ? hoard::launch_layer_gateup(g, s) : hoard::launch_gateup(g, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "gate/up launch: %s", hipGetErrorString(e));
     {
         KernelMark mark(h, HOARD_KERNEL_DOWN, s);
-        e = hoard::launch_down_combine(d, s);
+        e = fast ? hoard::launch_layer_down(d, s) : hoard::launch_down_combine(d, s);
     }
     if (e != hipSuccess) return fail(HOARD_ERR_HIP, "down/combine launch: %s", hipGetErrorString(e));
     return HOARD_OK;
@@ -971,6 +974,10 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
             return fail(HOARD_ERR_UNSUPPORTED, "decode kernel %d does not take this shape or device", value);
         h->decode_kernel = value;
         return HOARD_OK;
+    case HOARD_OPT_LAYER_KERNELS:
+        if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "layer kernels flag %d", value);
+        h->layer_kernels = value != 0;
+        return HOARD_OK;
     case HOARD_OPT_POOL_NAIVE:
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "pool naive flag %d", value);
         if (value && h->cfg.pool_k > 0) {
@@ -998,6 +1005,9 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
         return HOARD_OK;
     case HOARD_OPT_DECODE_KERNEL:
         *value = h->decode_kernel;
+        return HOARD_OK;
+    case HOARD_OPT_LAYER_KERNELS:
+        *value = h->layer_kernels ? 1 : 0;
         return HOARD_OK;
     case HOARD_OPT_DECODE_KERNELS_AVAILABLE:
         *value = (h->xcd_ok ? 1 : 0) | (h->spread_ok ? 2 : 0);

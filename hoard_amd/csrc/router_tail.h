@@ -114,6 +114,8 @@ __device__ inline void router_tail(const float *logits, int E, int k, int renorm
         router_tail_nt<AGENT, 2>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 256)
         router_tail_nt<AGENT, 4>(logits, E, k, renorm, sel, wsel, tok);
+    else if (E <= 512)
+        router_tail_nt<AGENT, 8>(logits, E, k, renorm, sel, wsel, tok);
     else
         router_tail_nt<AGENT, kMaxExpertsPerLane>(logits, E, k, renorm, sel, wsel, tok);
 }

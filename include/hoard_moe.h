@@ -186,6 +186,12 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
    bit 1 the second. */
 #define HOARD_OPT_DECODE_KERNEL 4
 #define HOARD_OPT_DECODE_KERNELS_AVAILABLE 5
+/* HOARD_OPT_LAYER_KERNELS: 1 (default) = the per-layer entry points (route,
+   ffn_combine, layer, and decode when it runs layer by layer) use kernels
+   compiled for the shape (n_embd 2048, Q4_K gate/up, Q6_K or Q4_K down, 16-byte
+   aligned tensors) where it matches; 0 = always the shape-generic kernels.
+   Both give the same bits. */
+#define HOARD_OPT_LAYER_KERNELS 6
 int hoard_moe_set_option(hoard_moe *h, int option, int value);
 int hoard_moe_get_option(hoard_moe *h, int option, int *value);
 

@@ -105,6 +105,27 @@ def test_deterministic(resident):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_layer_kernels_match_generic(resident):
+    """hoard_moe_layer through the kernels compiled for the shape gives the
+    shape-generic kernels' bits: output, selected experts and weights."""
+    import hoard_amd as H
+    shape, layers, st = resident
+    try:
+        for l in layers:
+            for t in range(4):
+                fx, res = W.make_hidden(shape, 3, l, t)
+                print(f"layer kernels {shape.name} layer {l} token {t}", flush=True)
+                st.set_option(H.OPT_LAYER_KERNELS, 1)
+                o1, s1, w1 = st.layer(l, fx, res)
+                st.set_option(H.OPT_LAYER_KERNELS, 0)
+                o0, s0, w0 = st.layer(l, fx, res)
+                assert np.array_equal(s1, s0), (s1, s0)
+                assert np.array_equal(w1.view(np.uint32), w0.view(np.uint32))
+                assert np.array_equal(o1.view(np.uint32), o0.view(np.uint32))
+    finally:
+        st.set_option(H.OPT_LAYER_KERNELS, 1)
+
+
 def test_olmoe_seeds_0_to_63(orc):
     """OLMoE-shaped layer, seeds 0..63, one token each (each seed its own weights)."""
     shape = W.OLMOE
