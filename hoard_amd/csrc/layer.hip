@@ -155,7 +155,7 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
         if (lane == 0) a.sgate[0] = 1.0f / (1.0f + expf(-acc));
     }
     __syncthreads();
-    if (wave < 4) {
+    if ((threadIdx.x >> 3) < 2 * kGuRows) {
         // one 8-lane group per row, lane t taking super-block t
         const int grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
         const int m = grp >= kGuRows, row = grp - m * kGuRows;

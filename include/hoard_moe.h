@@ -170,7 +170,9 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
 
 /* Options.  HOARD_OPT_PERSISTENT_DECODE selects how hoard_moe_decode runs:
    0 = one launch per kernel per layer, 1 = one cooperative launch per call
-   when the shape and device admit it (default), 2 = require that launch.
+   when the shape and device admit it and the range holds at least 3 layers
+   (default; shorter ranges are faster layer by layer), 2 = require that
+   launch.
    HOARD_OPT_PERSISTENT_AVAILABLE (read-only) reports whether they admit it. */
 #define HOARD_OPT_PERSISTENT_DECODE 1
 #define HOARD_OPT_PERSISTENT_AVAILABLE 2

@@ -152,12 +152,15 @@ def test_olmoe_seeds_0_to_63(orc):
 
 def test_decode_chain_per_layer(orc):
     """Stacked decode on device (fx = rms_norm(x) fused into the router) against the
-    oracle applied layer by layer to the device's own input of each layer."""
+    oracle applied layer by layer to the device's own input of each layer; one call
+    per layer runs the per-layer launches, the whole range one cooperative launch."""
+    import hoard_amd as H
     shape = W.QWEN3_30B
     nl = 3
     layers = {l: W.make_layer(shape, 0, l) for l in range(nl)}
     st = _stage(shape, layers)
     try:
+        assert st.get_option(H.OPT_PERSISTENT_DECODE) == 1
         _, x = W.make_hidden(shape, 0, 0, 0)
         xs = [x]
         for l in range(nl):
@@ -168,7 +171,8 @@ def test_decode_chain_per_layer(orc):
             ref, _, _ = orc.moe_layer(layers[l], fx, xs[l])
             parity.assert_parity(xs[l + 1], ref, f"decode layer {l}")
         whole = st.decode(xs[0], 0, nl, W.RMS_EPS)
-        assert np.array_equal(whole.view(np.uint32), xs[-1].view(np.uint32))
+        st.sync_check()
+        parity.assert_parity(whole, xs[-1], "one launch vs per-layer launches")
     finally:
         st.close()
 
