@@ -491,8 +491,7 @@ def main():
     result["config"]["decode_path"] = (
         ("one cooperative launch per token, " + ("expert rows spread over all CUs" if spread
                                                  else "one expert per XCD"))
-        if persistent.value and args.decode_kernel != "launches"
-        else "router, gate/up and down+combine launches per layer")
+        if "decode_persistent" in kernels else "router, gate/up and down+combine launches per layer")
     if args.phases:
         ph = phase_breakdown(lib, h, lambda: step(warm), H, PHASES_SPREAD if spread else PHASES)
         if ph:
