@@ -97,6 +97,14 @@ ABI = {
     "hoard_moe_forward_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "hoard_moe_get_stats": (_I, [_P, ctypes.POINTER(MoeStats)]),
     "hoard_moe_reset_stats": (_I, [_P]),
+    "hoard_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "hoard_gguf_close": (None, [_P]),
+    "hoard_gguf_arch": (ctypes.c_char_p, [_P]),
+    "hoard_gguf_moe_cfg": (_I, [_P, ctypes.POINTER(MoeCfg)]),
+    "hoard_gguf_rms_eps": (ctypes.c_float, [_P]),
+    "hoard_gguf_layer_weights": (_I, [_P, _I, ctypes.POINTER(LayerWeights)]),
+    "hoard_gguf_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64),
+                               ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(_P)]),
     "hoard_slot_lru_create": (_I, [_I, _I, _I, _I, ctypes.POINTER(_P)]),
     "hoard_slot_lru_access": (_I, [_P, _I, _P, _I, _P, _P]),
     "hoard_slot_lru_destroy": (None, [_P]),

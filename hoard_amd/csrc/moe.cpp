@@ -536,6 +536,32 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
     return HOARD_OK;
 }
 
+// The per-layer kernels over [l0, l1): route, slot fetch when pooled, experts and combine.
+int decode_layers(hoard_moe *h, int l0, int l1, float *x_dev, float eps, hipStream_t s) {
+    for (int l = l0; l < l1; ++l) {
+        int rc = 0;
+        const Layer &L = h->layers[l];
+        rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
+        if (rc) return rc;
+        const int32_t *ids = h->sel;
+        if (h->cfg.pool_k > 0) {
+            rc = pool_after_route(h, l, h->sel, h->slot_ids, s);
+            if (rc) return rc;
+            ids = h->slot_ids;
+        }
+        rc = run_ffn(h, L, h->fx, ids, h->wsel, x_dev, x_dev, s);
+        if (rc) return rc;
+        rc = pool_mark_use(h, l, s);
+        if (rc) return rc;
+    }
+    return HOARD_OK;
+}
+
+bool same_types(const Layer &a, const Layer &b) {
+    return a.gate_type == b.gate_type && a.up_type == b.up_type && a.down_type == b.down_type &&
+           a.sh_gate_type == b.sh_gate_type && a.sh_up_type == b.sh_up_type && a.sh_down_type == b.sh_down_type;
+}
+
 // Launches the one-launch decode when it applies; *used reports whether it did.
 // A cooperative launch costs about 22 us before its first layer (35.5 us for one
 // layer against 13.2 us for each further one), and the per-layer launches take
@@ -628,6 +654,13 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
 extern "C" {
 
 const char *hoard_last_error(void) { return g_err.c_str(); }
+
+// The error text other translation units of the library report through
+// hoard_last_error (host_error.h).
+int hoard_set_error(int code, const char *msg) {
+    g_err = msg ? msg : "";
+    return code;
+}
 
 int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     g_err.clear();
@@ -824,24 +857,24 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
         int rc = check_layer(h, l);
         if (rc) return rc;
     }
-    bool used = false;
-    int rc0 = persistent_decode(h, layer_begin, layer_end, x_dev, eps, s, &used);
-    if (rc0 || used) return rc0;
-    for (int l = layer_begin; l < layer_end; ++l) {
-        int rc = 0;
-        const Layer &L = h->layers[l];
-        rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
+    // Forced mode takes the range as one launch (or fails); automatic mode splits
+    // it into runs of layers with the same quant types (Q4_K_M files mix Q4_K and
+    // Q6_K down experts from layer to layer) and decodes each run with the
+    // one-launch kernel where it applies, else layer by layer.
+    if (h->persistent_mode == 2) {
+        bool used = false;
+        int rc0 = persistent_decode(h, layer_begin, layer_end, x_dev, eps, s, &used);
+        if (rc0 || used) return rc0;
+        return decode_layers(h, layer_begin, layer_end, x_dev, eps, s);
+    }
+    for (int r0 = layer_begin; r0 < layer_end;) {
+        int r1 = r0 + 1;
+        while (r1 < layer_end && same_types(h->layers[r0], h->layers[r1])) ++r1;
+        bool used = false;
+        int rc = persistent_decode(h, r0, r1, x_dev, eps, s, &used);
+        if (!rc && !used) rc = decode_layers(h, r0, r1, x_dev, eps, s);
         if (rc) return rc;
-        const int32_t *ids = h->sel;
-        if (h->cfg.pool_k > 0) {
-            rc = pool_after_route(h, l, h->sel, h->slot_ids, s);
-            if (rc) return rc;
-            ids = h->slot_ids;
-        }
-        rc = run_ffn(h, L, h->fx, ids, h->wsel, x_dev, x_dev, s);
-        if (rc) return rc;
-        rc = pool_mark_use(h, l, s);
-        if (rc) return rc;
+        r0 = r1;
     }
     return HOARD_OK;
 }

@@ -35,6 +35,25 @@ class MoEStage:
         for li, hl in (layers or {}).items():
             self.set_layer(li, hl)
 
+    @classmethod
+    def from_gguf(cls, path, layers=None, pool_k: int = 0, max_tokens: int = 1) -> "MoEStage":
+        """A stage holding the expert stage of every layer in `layers` (default:
+        all) of a GGUF file.  The weights are copied in, so the file is closed
+        before this returns."""
+        from .gguf import GGUFWeights
+        with GGUFWeights(path) as g:
+            shape = g.shape()
+            st = cls(shape, pool_k=pool_k, max_tokens=max_tokens)
+            try:
+                for l in range(shape.n_layer) if layers is None else layers:
+                    w = g.layer_weights(l)
+                    check(st.lib.hoard_moe_set_layer_weights(st.h, l, ctypes.byref(w)))
+            except Exception:
+                st.close()
+                raise
+            st.rms_eps = g.rms_eps()
+        return st
+
     def close(self):
         if self.h:
             self.lib.hoard_moe_destroy(self.h)

@@ -169,10 +169,11 @@ int hoard_moe_phase_trace(hoard_moe *h, int enable);
 int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, int *n_layers);
 
 /* Options.  HOARD_OPT_PERSISTENT_DECODE selects how hoard_moe_decode runs:
-   0 = one launch per kernel per layer, 1 = one cooperative launch per call
-   when the shape and device admit it and the range holds at least 3 layers
-   (default; shorter ranges are faster layer by layer), 2 = require that
-   launch.
+   0 = one launch per kernel per layer, 1 = one cooperative launch per run of
+   layers with the same quant types when the shape and device admit it and the
+   run holds at least 3 layers (default; shorter runs are faster layer by
+   layer, and a range whose types change is split into such runs), 2 = require
+   one launch for the whole range.
    HOARD_OPT_PERSISTENT_AVAILABLE (read-only) reports whether they admit it. */
 #define HOARD_OPT_PERSISTENT_DECODE 1
 #define HOARD_OPT_PERSISTENT_AVAILABLE 2

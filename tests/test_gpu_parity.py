@@ -273,3 +273,39 @@ def test_persistent_decode_unavailable_shape_falls_back():
             st.set_option(H.OPT_DECODE_KERNEL, 2)
     finally:
         st.close()
+
+
+def test_decode_splits_the_range_where_layer_types_change(orc):
+    """Layers 0-2 with Q6_K down experts and layer 3 with Q4_K (a Q4_K_M file's mix):
+    automatic mode decodes layers 0-2 in one launch and layer 3 with the per-layer
+    kernels, and the result matches the oracle layer by layer and the all-launches path."""
+    import ctypes
+    import dataclasses
+
+    import hoard_amd as H
+    shape = W.QWEN3_30B
+    shapes = [shape] * 3 + [dataclasses.replace(shape, down_type=H.TYPE_Q4_K)]
+    layers = {l: W.make_layer(shapes[l], 5, l) for l in range(4)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_PERSISTENT_DECODE) == 1
+        _, x = W.make_hidden(shape, 5, 0, 0)
+        H.check(st.lib.hoard_moe_profile(st.h, 1))
+        print("mixed-type decode of 4 layers", flush=True)
+        y = st.decode(x, 0, 4, W.RMS_EPS)
+        st.sync_check()
+        kt = H.KernelTimes()
+        H.check(st.lib.hoard_moe_profile_read(st.h, ctypes.byref(kt)))
+        H.check(st.lib.hoard_moe_profile(st.h, 0))
+        assert kt.launches[H.KERNEL_DECODE] == 1 and kt.launches[H.KERNEL_ROUTER] == 1, list(kt.launches)
+        xs = [x]
+        for l in range(4):  # the per-layer path, layer by layer, each checked against the oracle
+            xs.append(st.decode(xs[-1], l, l + 1, W.RMS_EPS))
+            ref, _, _ = orc.moe_layer(layers[l], orc.rms_norm(xs[l], W.RMS_EPS), xs[l])
+            parity.assert_parity(xs[-1], ref, f"mixed types layer {l}")
+        parity.assert_parity(y, xs[-1], "split range vs layer by layer")
+        st.set_option(H.OPT_PERSISTENT_DECODE, 0)
+        launched = st.decode(x, 0, 4, W.RMS_EPS)
+        assert np.array_equal(launched.view(np.uint32), xs[-1].view(np.uint32))
+    finally:
+        st.close()
