@@ -14,9 +14,11 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libhoard_moe.so"
 
 TYPE_F32 = 0
+TYPE_Q3_K = 11
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+BLOCK_BYTES = {TYPE_Q3_K: 110, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
 
 OK = 0
 ERR_INVALID = -1

@@ -23,9 +23,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kGateUpRows = 16;
 
-__device__ __forceinline__ int block_bytes_dev(int type) {
-    return type == kTypeQ4K ? kQ4KBytes : kQ6KBytes;
-}
+__device__ __forceinline__ int block_bytes_dev(int type) { return kquant_block_bytes(type); }
 
 template <class P>
 __device__ __forceinline__ void *align16(P *p) {
@@ -52,15 +50,17 @@ __device__ __forceinline__ int stage_issue(uint8_t *dst, const uint8_t *src, siz
 }
 
 __device__ __forceinline__ size_t row_bytes(int type, int cols) {
-    return (size_t)(cols / QK) * (type == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
+    return (size_t)(cols / QK) * (size_t)kquant_block_bytes(type);
 }
 
 __device__ __forceinline__ void terms_dyn(int type, const uint8_t *blk, const Q8Block &x, float &tm,
                                           float &tn) {
-    if (type == kTypeQ4K)
-        q4k_block_terms(blk, x, tm, tn);
-    else
-        q6k_block_terms(blk, x, tm, tn);
+    switch (type) {
+    case kTypeQ4K: q4k_block_terms(blk, x, tm, tn); break;
+    case kTypeQ5K: q5k_block_terms(blk, x, tm, tn); break;
+    case kTypeQ3K: q3k_block_terms(blk, x, tm, tn); break;
+    default: q6k_block_terms(blk, x, tm, tn); break;
+    }
 }
 
 __device__ __forceinline__ float row_sum_dyn(int type, const float2 *t, int nb) {
@@ -69,7 +69,7 @@ __device__ __forceinline__ float row_sum_dyn(int type, const float2 *t, int nb) 
         acc = acc + t[b].x;
         accm = accm + t[b].y;
     }
-    return type == kTypeQ4K ? acc - accm : acc;
+    return kquant_has_min(type) ? acc - accm : acc;
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -255,9 +255,7 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(DownArgs a, int 
 
 }  // namespace
 
-size_t block_bytes(int type) {
-    return type == kTypeQ4K ? kQ4KBytes : (type == kTypeQ6K ? kQ6KBytes : 0);
-}
+size_t block_bytes(int type) { return (size_t)kquant_block_bytes(type); }
 
 static size_t host_row_bytes(int type, int cols) { return (size_t)(cols / QK) * block_bytes(type); }
 

@@ -38,7 +38,9 @@ int fail(int code, const char *fmt, ...) {
 
 constexpr size_t kTailPad = 4096;  // kernels read whole 1 KB chunks past the end of a staged run
 
-bool quant_type_ok(int t) { return t == HOARD_TYPE_Q4_K || t == HOARD_TYPE_Q6_K; }
+bool quant_type_ok(int t) {
+    return t == HOARD_TYPE_Q4_K || t == HOARD_TYPE_Q6_K || t == HOARD_TYPE_Q5_K || t == HOARD_TYPE_Q3_K;
+}
 
 size_t mat_bytes(int type, int rows, int cols) {
     return (size_t)rows * (size_t)(cols / 256) * hoard::block_bytes(type);
@@ -727,7 +729,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
     const hoard_moe_cfg &c = h->cfg;
     if (!w->router || !w->gate || !w->up || !w->down) return fail(HOARD_ERR_INVALID, "missing tensor");
     if (!quant_type_ok(w->gate_type) || !quant_type_ok(w->up_type) || !quant_type_ok(w->down_type))
-        return fail(HOARD_ERR_UNSUPPORTED, "expert types %d/%d/%d: only Q4_K (12) and Q6_K (14)", w->gate_type,
+        return fail(HOARD_ERR_UNSUPPORTED, "expert types %d/%d/%d: Q3_K (11), Q4_K (12), Q5_K (13) and Q6_K (14) are taken", w->gate_type,
                     w->up_type, w->down_type);
     const bool sh = c.n_ff_shexp > 0;
     if (sh) {

@@ -1,6 +1,6 @@
 // Deterministic synthetic MoE layers (host only).  Counter-based splitmix64:
 // word i of a tensor is mix(key ^ (i * 0xD1B54A32D192ED03)), so generation is
-// order-free and parallel.  Block layouts are ggml's block_q4_K / block_q6_K.
+// order-free and parallel.  Block layouts are ggml's block_q{3,4,5,6}_K.
 #include "hoard_synth.h"
 
 #include <algorithm>
@@ -42,29 +42,39 @@ uint16_t to_half(float f) {
     return (uint16_t)(sign | h);
 }
 
-constexpr int kQ4K = 12, kQ6K = 14;
+constexpr int kQ3K = 11, kQ4K = 12, kQ5K = 13, kQ6K = 14;
 constexpr uint64_t kSaltD = 0x5bd1e9955bd1e995ull;
 constexpr uint64_t kSaltM = 0x27d4eb2f165667c5ull;
 
-size_t block_bytes(int type) { return type == kQ4K ? 144 : (type == kQ6K ? 210 : 0); }
+size_t block_bytes(int type) {
+    switch (type) {
+    case kQ3K: return 110;
+    case kQ4K: return 144;
+    case kQ5K: return 176;
+    case kQ6K: return 210;
+    default: return 0;
+    }
+}
 
 void fill_range(int type, uint64_t key, uint8_t *dst, size_t b0, size_t b1, float dstd) {
     const size_t bb = block_bytes(type);
     for (size_t b = b0; b < b1; ++b) {
         uint8_t *blk = dst + b * bb;
         uint64_t w[26];
-        const int nw = type == kQ4K ? 18 : 26;  // enough words for 140 / 208 random bytes
-        for (int i = 0; i < nw; ++i) w[i] = word(key, b * 32 + (uint64_t)i);
+        // random bytes: 140 (Q4_K scales + nibbles), 172 (Q5_K scales, qh, qs),
+        // 208 (Q6_K ql, qh, scales), 108 (Q3_K hmask, qs, scales)
+        const int nrand = type == kQ4K ? 140 : type == kQ5K ? 172 : type == kQ6K ? 208 : 108;
+        for (int i = 0; i < (nrand + 7) / 8; ++i) w[i] = word(key, b * 32 + (uint64_t)i);
         const uint8_t *rb = reinterpret_cast<const uint8_t *>(w);
         const uint16_t d = to_half((float)std::fabs(normal(key ^ kSaltD, b) * dstd));
-        if (type == kQ4K) {
+        if (type == kQ4K || type == kQ5K) {
             const uint16_t dm = to_half((float)std::fabs(normal(key ^ kSaltM, b) * dstd));
             std::memcpy(blk, &d, 2);
             std::memcpy(blk + 2, &dm, 2);
-            std::memcpy(blk + 4, rb, 140);  // 12 scale bytes + 128 nibble bytes
+            std::memcpy(blk + 4, rb, (size_t)nrand);
         } else {
-            std::memcpy(blk, rb, 208);      // ql, qh, scales
-            std::memcpy(blk + 208, &d, 2);
+            std::memcpy(blk, rb, (size_t)nrand);
+            std::memcpy(blk + nrand, &d, 2);
         }
     }
 }

@@ -18,7 +18,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import TYPE_Q4_K, TYPE_Q6_K, LayerWeights, MoeCfg, expert_bytes, load_library
+from . import TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, LayerWeights, MoeCfg, expert_bytes, load_library
 
 ROUTER, GATE, UP, DOWN, SH_GATE, SH_UP, SH_DOWN, SH_GATE_INP, HIDDEN = range(9)
 RMS_EPS = 1e-6
@@ -77,7 +77,12 @@ OLMOE = Shape("olmoe", 0, 2048, 64, 8, 1024, 0, TYPE_Q4_K, TYPE_Q4_K, TYPE_Q4_K,
 QWEN3_30B = Shape("qwen3_30b", 1, 2048, 128, 8, 768, 1, TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K, 48)
 QWEN3_NEXT = Shape("qwen3_next", 2, 2048, 512, 10, 512, 1, TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K, 48,
                    n_ff_shexp=512)
-SHAPES = {s.name: s for s in (OLMOE, QWEN3_30B, QWEN3_NEXT)}
+# Q5_K down experts: Qwen3.5-35B-A3B (qwen35moe; n_ff 512, 8 of 256 experts, 40 layers,
+# a 512-wide shared expert), and OLMoE in its Q3_K_M form (Q3_K gate/up, Q5_K down);
+# types and expert sizes as listed in the reference's notes/FEASIBILITY.md:75,77.
+QWEN35 = Shape("qwen35", 3, 2048, 256, 8, 512, 1, TYPE_Q4_K, TYPE_Q4_K, TYPE_Q5_K, 40, n_ff_shexp=512)
+OLMOE_Q3 = Shape("olmoe_q3", 4, 2048, 64, 8, 1024, 0, TYPE_Q3_K, TYPE_Q3_K, TYPE_Q5_K, 16)
+SHAPES = {s.name: s for s in (OLMOE, QWEN3_30B, QWEN3_NEXT, QWEN35, OLMOE_Q3)}
 
 
 @dataclass

@@ -34,7 +34,9 @@ extern "C" {
 
 /* ggml type ids accepted for expert tensors (ggml.h enum ggml_type). */
 #define HOARD_TYPE_F32 0
+#define HOARD_TYPE_Q3_K 11
 #define HOARD_TYPE_Q4_K 12
+#define HOARD_TYPE_Q5_K 13
 #define HOARD_TYPE_Q6_K 14
 
 typedef struct hoard_moe hoard_moe;

@@ -15,9 +15,11 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmoe_oracle.so"
 
+TYPE_Q3_K = 11
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+BLOCK_BYTES = {TYPE_Q3_K: 110, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
 assert Q8K_DTYPE.itemsize == 292
 
@@ -42,12 +44,17 @@ _SIGS = {
     "orc_nearest_int": (_I, [_F]),
     "orc_dequant_q4_K": (None, [_P, _P]),
     "orc_dequant_q6_K": (None, [_P, _P]),
+    "orc_dequant_q3_K": (None, [_P, _P]),
+    "orc_dequant_q5_K": (None, [_P, _P]),
     "orc_dequant_row": (None, [_I, _P, _I, _P]),
     "orc_quantize_q8_K": (None, [_P, _I, _P]),
     "orc_sizeof_q8_K": (ctypes.c_size_t, []),
     "orc_vec_dot_f32": (_F, [_I, _P, _P]),
     "orc_vec_dot_q4_K_q8_K": (_F, [_I, _P, _P]),
     "orc_vec_dot_q6_K_q8_K": (_F, [_I, _P, _P]),
+    "orc_vec_dot_q3_K_q8_K": (_F, [_I, _P, _P]),
+    "orc_vec_dot_q5_K_q8_K": (_F, [_I, _P, _P]),
+    "orc_vec_dot_q_q8_K": (_F, [_I, _I, _P, _P]),
     "orc_mul_mat_q": (None, [_I, _P, _I, _I, _P, _P]),
     "orc_mul_mat_q8": (None, [_I, _P, _I, _I, _P, _P]),
     "orc_silu": (_F, [_F]),
@@ -132,8 +139,7 @@ def vec_dot_f32(x: np.ndarray, y: np.ndarray) -> float:
 
 def vec_dot_q(qtype: int, row: np.ndarray, q8: np.ndarray) -> float:
     row = _u8(row)
-    fn = lib().orc_vec_dot_q4_K_q8_K if qtype == TYPE_Q4_K else lib().orc_vec_dot_q6_K_q8_K
-    return fn(q8.size * 256, _p(row), _p(q8))
+    return lib().orc_vec_dot_q_q8_K(qtype, q8.size * 256, _p(row), _p(q8))
 
 
 def mul_mat_q(qtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:

@@ -9,9 +9,9 @@
  *
  * Parity status per function (pins live in tests/test_oracle_*.py):
  *   orc_fp16_to_fp32 / orc_fp32_to_fp16  pinned: exhaustive / numpy float16
- *   orc_dequant_q4_K / orc_dequant_q6_K  pinned: independent encoder + known-answer blocks
+ *   orc_dequant_q{3,4,5,6}_K             pinned: independent encoder + known-answer blocks
  *   orc_quantize_q8_K                    pinned: closed-form special cases + bounds
- *   orc_vec_dot_q{4,6}_K_q8_K            pinned: fp64 brute force over dequantised operands
+ *   orc_vec_dot_q{3,4,5,6}_K_q8_K        pinned: fp64 brute force over dequantised operands
  *   orc_vec_dot_f32                      pinned: fp64 within bound + order-sensitive vector
  *   orc_route                            pinned: fp64 softmax, brute-force top-k, clamp
  *   orc_expert_ffn / orc_moe_*           pinned: fp64 composition of the pinned parts
@@ -83,7 +83,9 @@ static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] <
 
 size_t orc_type_block_bytes(int type) {
     switch (type) {
+    case ORC_TYPE_Q3_K: return ORC_Q3_K_BYTES;
     case ORC_TYPE_Q4_K: return ORC_Q4_K_BYTES;
+    case ORC_TYPE_Q5_K: return ORC_Q5_K_BYTES;
     case ORC_TYPE_Q6_K: return ORC_Q6_K_BYTES;
     default: return 0;
     }
@@ -161,11 +163,77 @@ void orc_dequant_q6_K(const uint8_t *blk, float *y) {
     for (int k = 0; k < 256; ++k) y[k] = d * (float)sc[k / 16] * (float)(q[k] - 32);
 }
 
+/* block_q5_K: [0..1] d fp16, [2..3] dmin fp16, [4..15] scales/mins packed as
+   in block_q4_K, [16..47] qh (fifth bits), [48..175] qs (low nibbles).
+   Chunk c (elements 64c..64c+63): element 64c+l takes the low nibble of
+   qs[32c+l] and bit 2c of qh[l]; element 64c+32+l the high nibble and bit
+   2c+1.  value = d*sc[s]*q - dmin*m[s], q in 0..31, s = element/32.         */
+static void q5k_unpack(const uint8_t *blk, int *q /* 256 values 0..31 */) {
+    const uint8_t *qh = blk + 16, *qs = blk + 48;
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) {
+            q[64 * c + l] = (qs[32 * c + l] & 0x0f) | (((qh[l] >> (2 * c)) & 1) << 4);
+            q[64 * c + 32 + l] = (qs[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+        }
+}
+
+/* ggml dequantize_row_q5_K, one block. */
+void orc_dequant_q5_K(const uint8_t *blk, float *y) {
+    const float d = orc_fp16_to_fp32(rd16(blk));
+    const float dmin = orc_fp16_to_fp32(rd16(blk + 2));
+    int q[256];
+    q5k_unpack(blk, q);
+    for (int s = 0; s < 8; ++s) {
+        int sc, m;
+        q4k_scale_min(s, blk + 4, &sc, &m);
+        const float ds = d * (float)sc, ms = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) y[32 * s + l] = ds * (float)q[32 * s + l] - ms;
+    }
+}
+
+/* block_q3_K: [0..31] hmask, [32..95] qs (2-bit pairs), [96..107] sixteen
+   6-bit scales, [108..109] d fp16.  Scale g (one per 16 elements): low 4 bits
+   are the low nibble of byte g (g < 8) or the high nibble of byte g-8, the top
+   2 bits are bits 2*(g/4)..+1 of byte 8 + g%4; the signed scale is that minus
+   32.  Half n (128 elements), pass j = 0..3: element 128n+32j+l (l < 32) takes
+   bits 2j..2j+1 of qs[32n+l] and hmask bit 4n+j of hmask[l]; q3 = q2 - 4 when
+   that bit is clear.  value = d * (sc[g] - 32) * q3, q3 in -4..3.           */
+static int q3k_scale(const uint8_t *sb, int g) {
+    const int lo = g < 8 ? (sb[g] & 0x0f) : (sb[g - 8] >> 4);
+    const int hi = (sb[8 + (g & 3)] >> (2 * (g >> 2))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+static void q3k_unpack(const uint8_t *blk, int *q /* 256 values -4..3 */) {
+    const uint8_t *hm = blk, *qs = blk + 32;
+    for (int n = 0; n < 2; ++n)
+        for (int j = 0; j < 4; ++j)
+            for (int l = 0; l < 32; ++l) {
+                const int q2 = (qs[32 * n + l] >> (2 * j)) & 3;
+                const int h = (hm[l] >> (4 * n + j)) & 1;
+                q[128 * n + 32 * j + l] = q2 - (h ? 0 : 4);
+            }
+}
+
+/* ggml dequantize_row_q3_K, one block: y = (d * sc) * q3. */
+void orc_dequant_q3_K(const uint8_t *blk, float *y) {
+    const float d = orc_fp16_to_fp32(rd16(blk + 108));
+    int q[256];
+    q3k_unpack(blk, q);
+    for (int k = 0; k < 256; ++k) y[k] = (d * (float)q3k_scale(blk + 96, k / 16)) * (float)q[k];
+}
+
 void orc_dequant_row(int type, const uint8_t *row, int n, float *y) {
     const size_t bb = orc_type_block_bytes(type);
     for (int i = 0; i < n / ORC_QK_K; ++i) {
-        if (type == ORC_TYPE_Q4_K) orc_dequant_q4_K(row + i * bb, y + i * ORC_QK_K);
-        else orc_dequant_q6_K(row + i * bb, y + i * ORC_QK_K);
+        const uint8_t *b = row + i * bb;
+        float *o = y + i * ORC_QK_K;
+        switch (type) {
+        case ORC_TYPE_Q3_K: orc_dequant_q3_K(b, o); break;
+        case ORC_TYPE_Q4_K: orc_dequant_q4_K(b, o); break;
+        case ORC_TYPE_Q5_K: orc_dequant_q5_K(b, o); break;
+        default: orc_dequant_q6_K(b, o); break;
+        }
     }
 }
 
@@ -280,6 +348,63 @@ float orc_vec_dot_q6_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y) 
     return acc;
 }
 
+/* ggml vec_dot_q5_K_q8_K: as Q4_K with the fifth bit from qh: per block
+   isum = sum_s sc[s] * sum_{32} q5*q8, msum = sum_s m[s]*(bsum pair);
+   acc += (d*dx)*isum, accm += (dmin*dx)*msum; result acc - accm. */
+float orc_vec_dot_q5_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y) {
+    float acc = 0.0f, accm = 0.0f;
+    int q[256];
+    for (int i = 0; i < n / ORC_QK_K; ++i) {
+        const uint8_t *b = row + (size_t)i * ORC_Q5_K_BYTES;
+        const int8_t *q8 = y[i].qs;
+        q5k_unpack(b, q);
+        int32_t isum = 0, msum = 0;
+        for (int s = 0; s < 8; ++s) {
+            int sc, m;
+            q4k_scale_min(s, b + 4, &sc, &m);
+            int32_t t = 0;
+            for (int l = 0; l < 32; ++l) t += q[32 * s + l] * q8[32 * s + l];
+            isum += sc * t;
+            msum += m * (y[i].bsums[2 * s] + y[i].bsums[2 * s + 1]);
+        }
+        const float d = orc_fp16_to_fp32(rd16(b)) * y[i].d;
+        const float dm = orc_fp16_to_fp32(rd16(b + 2)) * y[i].d;
+        acc = acc + d * (float)isum;
+        accm = accm + dm * (float)msum;
+    }
+    return acc - accm;
+}
+
+/* ggml vec_dot_q3_K_q8_K: per block isum = sum_g (sc[g]-32) * sum_{16} q3*q8,
+   then acc += (d*dx)*isum in fp32. */
+float orc_vec_dot_q3_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y) {
+    float acc = 0.0f;
+    int q[256];
+    for (int i = 0; i < n / ORC_QK_K; ++i) {
+        const uint8_t *b = row + (size_t)i * ORC_Q3_K_BYTES;
+        const int8_t *q8 = y[i].qs;
+        q3k_unpack(b, q);
+        int32_t isum = 0;
+        for (int g = 0; g < 16; ++g) {
+            int32_t s = 0;
+            for (int l = 0; l < 16; ++l) s += q[16 * g + l] * q8[16 * g + l];
+            isum += q3k_scale(b + 96, g) * s;
+        }
+        const float d = orc_fp16_to_fp32(rd16(b + 108)) * y[i].d;
+        acc = acc + d * (float)isum;
+    }
+    return acc;
+}
+
+float orc_vec_dot_q_q8_K(int type, int n, const uint8_t *row, const orc_block_q8_K *y) {
+    switch (type) {
+    case ORC_TYPE_Q3_K: return orc_vec_dot_q3_K_q8_K(n, row, y);
+    case ORC_TYPE_Q4_K: return orc_vec_dot_q4_K_q8_K(n, row, y);
+    case ORC_TYPE_Q5_K: return orc_vec_dot_q5_K_q8_K(n, row, y);
+    default: return orc_vec_dot_q6_K_q8_K(n, row, y);
+    }
+}
+
 void orc_mul_mat_q8(int type, const uint8_t *w, int nrows, int ncols, const orc_block_q8_K *qx,
                     float *out) {
     const size_t row_bytes = (size_t)(ncols / ORC_QK_K) * orc_type_block_bytes(type);
@@ -288,8 +413,7 @@ void orc_mul_mat_q8(int type, const uint8_t *w, int nrows, int ncols, const orc_
 #endif
     for (int r = 0; r < nrows; ++r) {
         const uint8_t *row = w + (size_t)r * row_bytes;
-        out[r] = type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K(ncols, row, qx)
-                                       : orc_vec_dot_q6_K_q8_K(ncols, row, qx);
+        out[r] = orc_vec_dot_q_q8_K(type, ncols, row, qx);
     }
 }
 

@@ -16,8 +16,10 @@
  *   batched      src/run_specloop.cpp:116-140, src/run_m1.cpp:93-108
  *
  * and the ggml block formats the expert bytes are copied in verbatim
- * (src/run_moe_stream.cpp:177-183): block_q4_K (144 B), block_q6_K (210 B)
- * and the activation format block_q8_K (ggml-cpu's vec_dot_type for both).
+ * (src/run_moe_stream.cpp:177-183): block_q4_K (144 B), block_q6_K (210 B),
+ * block_q5_K (176 B) and block_q3_K (110 B) -- the expert types of the
+ * reference's model table (notes/FEASIBILITY.md:73-77) -- and the activation
+ * format block_q8_K (ggml-cpu's vec_dot_type for all four).
  *
  * Pinning (see tests/test_oracle_*.py): block codecs by an independent
  * encoder written from the layout (decode(encode(v)) == v) and hand-built
@@ -38,8 +40,10 @@ extern "C" {
 #endif
 
 enum { ORC_QK_K = 256 };
-enum { ORC_TYPE_F32 = 0, ORC_TYPE_Q4_K = 12, ORC_TYPE_Q6_K = 14 };  /* ggml type ids */
-enum { ORC_Q4_K_BYTES = 144, ORC_Q6_K_BYTES = 210, ORC_Q8_K_BYTES = 292 };
+enum { ORC_TYPE_F32 = 0, ORC_TYPE_Q3_K = 11, ORC_TYPE_Q4_K = 12, ORC_TYPE_Q5_K = 13,
+       ORC_TYPE_Q6_K = 14 };  /* ggml type ids */
+enum { ORC_Q3_K_BYTES = 110, ORC_Q4_K_BYTES = 144, ORC_Q5_K_BYTES = 176, ORC_Q6_K_BYTES = 210,
+       ORC_Q8_K_BYTES = 292 };
 
 /* ggml block_q8_K: fp32 d, 256 int8 quants, 16 int16 group sums. */
 typedef struct {
@@ -57,6 +61,8 @@ int orc_nearest_int(float f);
 size_t orc_type_block_bytes(int type);
 void orc_dequant_q4_K(const uint8_t *blk, float *y);
 void orc_dequant_q6_K(const uint8_t *blk, float *y);
+void orc_dequant_q3_K(const uint8_t *blk, float *y);
+void orc_dequant_q5_K(const uint8_t *blk, float *y);
 void orc_dequant_row(int type, const uint8_t *row, int n, float *y);
 void orc_quantize_q8_K(const float *x, int n, orc_block_q8_K *y);
 size_t orc_sizeof_q8_K(void);
@@ -65,6 +71,10 @@ size_t orc_sizeof_q8_K(void);
 float orc_vec_dot_f32(int n, const float *x, const float *y);
 float orc_vec_dot_q4_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y);
 float orc_vec_dot_q6_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y);
+float orc_vec_dot_q3_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y);
+float orc_vec_dot_q5_K_q8_K(int n, const uint8_t *row, const orc_block_q8_K *y);
+/* the row dot of any supported type */
+float orc_vec_dot_q_q8_K(int type, int n, const uint8_t *row, const orc_block_q8_K *y);
 
 /* out[r] = row_r(W) . x for a quantised W of nrows x ncols, x quantised to Q8_K first. */
 void orc_mul_mat_q(int type, const uint8_t *w, int nrows, int ncols, const float *x, float *out);

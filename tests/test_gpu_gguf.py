@@ -2,7 +2,8 @@
 against the oracle on the same weights: Qwen3-Next-shaped layers with an f32, a
 bf16 and an f16 router and the bf16 shared-expert gate the reference
 upconverts (src/run_qwen35.cpp:219, :250-253), and Qwen3-30B-shaped layers
-whose down experts are Q6_K in one layer and Q4_K in the next.  Same bar as the other parity
+whose down experts are Q6_K in one layer and Q4_K in the next, and an OLMoE
+layer in its Q3_K_M form (Q3_K gate/up, Q5_K down, no renormalisation).  Same bar as the other parity
 tests: identical top-k, max|d| <= 2e-3*||y||_inf, cosine >= 0.9999."""
 import dataclasses
 
@@ -20,8 +21,9 @@ torch = pytest.importorskip("torch")
 
 
 @pytest.mark.parametrize("shape,arch,routers", [(W.QWEN3_NEXT, "qwen3next", (GGML_BF16, GGML_F16)),
-                                                (W.QWEN3_30B, "qwen3moe", (GGML_F32, GGML_BF16))],
-                         ids=["qwen3_next", "qwen3_30b"])
+                                                (W.QWEN3_30B, "qwen3moe", (GGML_F32, GGML_BF16)),
+                                                (W.OLMOE_Q3, "olmoe", (GGML_F32,))],
+                         ids=["qwen3_next", "qwen3_30b", "olmoe_q3"])
 def test_layers_from_gguf_match_oracle(orc, tmp_path, shape, arch, routers):
     from hoard_amd.runtime import MoEStage
     nl = len(routers)

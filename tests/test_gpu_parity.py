@@ -22,10 +22,11 @@ def _stage(shape, layers, **kw):
     return MoEStage(shape, n_layer=max(layers, default=0) + 1, layers=layers, **kw)
 
 
-@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.QWEN3_NEXT, W.OLMOE], ids=lambda s: s.name)
+@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.QWEN3_NEXT, W.OLMOE, W.QWEN35, W.OLMOE_Q3],
+                ids=lambda s: s.name)
 def resident(request):
     shape = request.param
-    nl = 1 if shape is W.OLMOE else 2
+    nl = 1 if shape in (W.OLMOE, W.OLMOE_Q3) else 2
     layers = {l: W.make_layer(shape, 0, l) for l in range(nl)}
     st = _stage(shape, layers)
     yield shape, layers, st

@@ -109,6 +109,68 @@ def test_q6_K_known_answers(orc):
     assert np.array_equal(y, want)
 
 
+def test_feasibility_expert_sizes_pin_q3_q5_block_bytes():
+    """Per-expert bytes from the reference's model table (notes/FEASIBILITY.md:75,77):
+    OLMoE Q3_K gate/up + Q5_K down at n_ff 1024 is 3.09 MB and Qwen3.5-35B-A3B Q4_K
+    gate/up + Q5_K down at n_ff 512 is 1.81 MB (MiB, n_embd 2048)."""
+    from hoard_amd import TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, expert_bytes
+    olmoe = 2 * expert_bytes(TYPE_Q3_K, 1024, 2048) + expert_bytes(TYPE_Q5_K, 2048, 1024)
+    qwen35 = 2 * expert_bytes(TYPE_Q4_K, 512, 2048) + expert_bytes(TYPE_Q5_K, 2048, 512)
+    assert round(olmoe / 2 ** 20, 2) == 3.09
+    assert round(qwen35 / 2 ** 20, 2) == 1.81
+
+
+def test_q5_K_decode_of_independent_encoding(orc):
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        f = qpack.random_q5_K(rng)
+        got = orc.dequant(orc.TYPE_Q5_K, qpack.pack_q5_K(*f), 256)
+        assert np.array_equal(got.view(np.uint32), qpack.expect_q5_K(*f).view(np.uint32))
+
+
+def test_q5_K_known_answers(orc):
+    z = orc.dequant(orc.TYPE_Q5_K, np.zeros(176, np.uint8), 256)
+    assert np.all(z == 0)
+    # only the fifth bit of element 64*2+32+7 (chunk 2, high half): qh[7] bit 5
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([qpack.fp16_bits(0.5)], np.uint16).view(np.uint8)
+    b[4 + 8 + 1] = 0x0f  # sub-block 5 scale low nibble 15 (byte s+4 = 9 for s = 5)
+    b[16 + 7] = 1 << 5
+    y = orc.dequant(orc.TYPE_Q5_K, b, 256)
+    want = np.zeros(256, np.float32); want[64 * 2 + 32 + 7] = 0.5 * 15 * 16
+    assert np.array_equal(y, want)
+    # q = 31 everywhere with all scales 63 and mins 0: d * 63 * 31
+    q = np.full(256, 31)
+    y = orc.dequant(orc.TYPE_Q5_K, qpack.pack_q5_K(0.25, 0.0, np.full(8, 63), np.zeros(8, int), q), 256)
+    assert np.all(y == np.float32(0.25 * 63 * 31))
+
+
+def test_q3_K_decode_of_independent_encoding(orc):
+    rng = np.random.default_rng(6)
+    for _ in range(200):
+        f = qpack.random_q3_K(rng)
+        got = orc.dequant(orc.TYPE_Q3_K, qpack.pack_q3_K(*f), 256)
+        assert np.array_equal(got.view(np.uint32), qpack.expect_q3_K(*f).view(np.uint32))
+
+
+def test_q3_K_known_answers(orc):
+    # all-zero bytes: scale 0 - 32 = -32 and q3 = 0 - 4 = -4 everywhere -> d * 128
+    b = np.zeros(110, np.uint8)
+    b[108:110] = np.array([qpack.fp16_bits(1.0)], np.uint16).view(np.uint8)
+    assert np.all(orc.dequant(orc.TYPE_Q3_K, b, 256) == 128.0)
+    # hmask all set, qs all zero, scales all +32 stored (=0 signed): all zero
+    b[0:32] = 0xff
+    b[96:104] = 0x00
+    b[104:108] = 0xaa  # top bits 2 of every scale -> stored 32 -> signed 0
+    assert np.all(orc.dequant(orc.TYPE_Q3_K, b, 256) == 0.0)
+    # extremes: scale g = 15 stored 63 (signed 31), q3 = 3 at element 255; scale 0 stored 0 (-32), q3 = -4 at 0
+    sc = np.zeros(16, int); sc[15] = 31; sc[0] = -32
+    q = np.zeros(256, int); q[255] = 3; q[0] = -4
+    y = orc.dequant(orc.TYPE_Q3_K, qpack.pack_q3_K(0.5, sc, q), 256)
+    want = np.zeros(256, np.float32); want[255] = 0.5 * 31 * 3; want[0] = 0.5 * -32 * -4
+    assert np.array_equal(y, want)
+
+
 def test_q8_K_special_cases(orc):
     # all-zero block: d = 0, q = 0
     q = orc.quantize_q8k(np.zeros(256, np.float32))

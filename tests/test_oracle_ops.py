@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import qpack
-from hoard_amd import TYPE_Q4_K, TYPE_Q6_K
+from hoard_amd import TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K
 from hoard_amd import workloads as W
 
 
@@ -19,21 +19,16 @@ def _fp64_dot_bound(terms):
     return 8 * np.finfo(np.float32).eps * np.sum(np.abs(terms)) + 1e-30
 
 
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", [TYPE_Q3_K, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
 def test_vec_dot_q_vs_fp64_brute_force(orc, qtype):
     rng = np.random.default_rng(10 + qtype)
     for trial in range(40):
         nb = int(rng.integers(1, 9))
         blocks, vals = [], []
         for _ in range(nb):
-            if qtype == TYPE_Q4_K:
-                f = qpack.random_q4_K(rng)
-                blocks.append(qpack.pack_q4_K(*f))
-                vals.append(qpack.fields_value_q4_K(*f))
-            else:
-                f = qpack.random_q6_K(rng)
-                blocks.append(qpack.pack_q6_K(*f))
-                vals.append(qpack.fields_value_q6_K(*f))
+            b, v = qpack.random_block(qtype, rng)
+            blocks.append(b)
+            vals.append(v)
         row = np.concatenate(blocks)
         wv = np.concatenate(vals)
         x = (rng.normal(0, 1, 256 * nb) * (10.0 ** rng.integers(-2, 4))).astype(np.float32)
@@ -53,6 +48,17 @@ def test_vec_dot_q4_K_min_term_matters(orc):
     xv = orc.dequant_q8k(q8)
     want = -0.5 * sum(mn[s] * xv[32 * s:32 * s + 32].sum() for s in range(8))
     assert np.isclose(orc.vec_dot_q(TYPE_Q4_K, row, q8), want, rtol=1e-6)
+
+
+def test_vec_dot_q5_K_min_and_fifth_bit(orc):
+    # quants 16 (fifth bit only) with unit scales: the dot is d*16*sum(x) - dmin*sum_s m_s*sum_s(x)
+    rng = np.random.default_rng(13)
+    mn = rng.integers(1, 64, 8)
+    row = qpack.pack_q5_K(0.125, 0.5, np.ones(8, int), mn, np.full(256, 16))
+    q8 = orc.quantize_q8k(rng.normal(0, 1, 256).astype(np.float32))
+    xv = orc.dequant_q8k(q8)
+    want = 0.125 * 16 * xv.sum() - 0.5 * sum(mn[s] * xv[32 * s:32 * s + 32].sum() for s in range(8))
+    assert np.isclose(orc.vec_dot_q(TYPE_Q5_K, row, q8), want, rtol=1e-6)
 
 
 def test_vec_dot_f32_vs_fp64(orc):
@@ -127,7 +133,8 @@ def _cmp(got, ref):
     return err, cos
 
 
-@pytest.mark.parametrize("shape", [W.OLMOE, W.QWEN3_30B, W.QWEN3_NEXT], ids=lambda s: s.name)
+@pytest.mark.parametrize("shape", [W.OLMOE, W.QWEN3_30B, W.QWEN3_NEXT, W.QWEN35, W.OLMOE_Q3],
+                         ids=lambda s: s.name)
 def test_moe_layer_vs_fp64_composition(orc, shape):
     hl = W.make_layer(shape, 0, 0)
     fx, res = W.make_hidden(shape, 0, 0)
