@@ -28,6 +28,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
+TYPE_NAMES = {11: "Q3_K", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}
 
 
 def parse():
@@ -35,7 +36,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--shape", default="qwen3_30b", choices=["qwen3_30b", "qwen3_next", "olmoe"])
+    ap.add_argument("--shape", default="qwen3_30b", choices=["qwen3_30b", "qwen3_next", "olmoe", "qwen35", "olmoe_q3"])
     ap.add_argument("--layers", type=int, default=None, help="stacked layers (default: the shape's)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
@@ -456,6 +457,7 @@ def main():
 
     layer_bytes = shape.bytes_per_token_layer()
     layer_gbps = layer_bytes / (us_layer * 1e3)
+    wtypes = "/".join(dict.fromkeys(TYPE_NAMES[t] for t in (shape.gate_type, shape.up_type, shape.down_type)))
     result = {
         "metric": "MoE-layer us/token + HBM GB/s (% of peak), Qwen3-30B-A3B-shape Q4_K decode",
         "value": round(us_layer, 3),
@@ -467,8 +469,8 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K/q6_K weights x q8_K activations (int8 dot), f32 router/accumulate",
-        "data": "synthetic (seeded random Q4_K/Q6_K super-blocks, f32 router, N(0,1) hidden)",
+        "dtype": f"{wtypes.replace('Q', 'q')} weights x q8_K activations (int8 dot), f32 router/accumulate",
+        "data": f"synthetic (seeded random {wtypes} super-blocks, f32 router, N(0,1) hidden)",
         "config": {"workload": f"{shape.name}: {n_layer} stacked MoE layers, batch-1 decode, "
                                f"hidden {shape.n_embd}, {shape.n_expert} experts top-{shape.n_used}, "
                                f"ff {shape.n_ff}, all experts resident in HBM",

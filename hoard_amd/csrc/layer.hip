@@ -170,16 +170,47 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
 }
 
 // -- down + combine -----------------------------------------------------------
+// Rows [0, n) of type T with NB super-blocks, row r at base + r * row bytes,
+// dotted with unit (u0 + r / 8)'s Q8_K(h); results to ys[u0 * 8 + r].
+template <int T, int NB>
+__device__ __forceinline__ void down_rows(const uint8_t *base, int n, int u0, const Q8L *q8h, float *ys) {
+    constexpr int kRowBytes = NB * QType<T>::bytes;
+    const int wave = threadIdx.x >> 6, grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
+    if constexpr (T == kTypeQ6K) {
+        // 8 lanes per row; a wave takes rows of one parity so that its 2-byte
+        // aligned rows share their 4-byte alignment
+        const int par = wave & 1, G = (wave >> 1) * 8 + (grp & 7);
+        for (int m = G; m < n / 2; m += 64) {
+            const int r = 2 * m + par, u = u0 + r / kDownRows;
+            const float y = g8_row_q6k_u<NB>(base + r * kRowBytes, q8h + u * NB, t8);
+            if (t8 == 0) ys[u0 * kDownRows + r] = y;
+        }
+    } else {
+        // one 8-lane group per row, lane t taking super-block t
+        for (int r = grp; r < n; r += 128) {
+            const int u = u0 + r / kDownRows;
+            const Q8L &xb = q8h[u * NB + (t8 < NB ? t8 : 0)];
+            float y;
+            if constexpr (T == kTypeQ5K)
+                y = lpb_row_q5k_mem<NB>(base + r * kRowBytes, xb, t8);
+            else
+                y = lpb_row_q4k_mem<NB>(base + r * kRowBytes, xb, t8);
+            if (t8 == NB - 1) ys[u0 * kDownRows + r] = y;
+        }
+    }
+}
+
 // grid = n_embd / 8, block = 1024.  Down rows of type TD with NBH super-blocks;
-// the shared expert (when present) has the routed experts' type and size.
+// the shared expert (when present) has rows of type TS and the same width.
 // Waves 0-7 copy the rows (expert u from wave u % 8: segments in different
 // pages do not wait for each other's address translation), waves 8-15 form
 // Q8_K(h) of every unit meanwhile.
-template <int TD, int NBH>
+template <int TD, int NBH, int TS>
 __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
     constexpr int kRowBytes = NBH * QType<TD>::bytes;
     constexpr int kSegBytes = kDownRows * kRowBytes;  // 8 rows of one expert
-    static_assert(kSegBytes % 16 == 0, "segments stay 16-byte aligned");
+    constexpr int kSegBytesS = kDownRows * NBH * QType<TS>::bytes;
+    static_assert(kSegBytes % 16 == 0 && kSegBytesS % 16 == 0, "segments stay 16-byte aligned");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float ys[17 * kDownRows];
     __shared__ int bad;
@@ -187,25 +218,24 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
     const bool has_sh = a.sh_down.base != nullptr;
     const int nu = k + (has_sh ? 1 : 0);
     uint8_t *wd = smem;
-    Q8L *q8h = reinterpret_cast<Q8L *>(smem + nu * kSegBytes);
+    Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes + (has_sh ? kSegBytesS : 0));
     const int wave = threadIdx.x >> 6;
     const int d0 = blockIdx.x * kDownRows;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
     if (wave < 8) {
         for (int u = wave; u < nu; u += 8) {
-            const uint8_t *src;
             if (u < k) {
                 const int id = a.ids[u];
                 if (id < 0 || id >= a.down.n_ids) {
                     bad = 1;
                     continue;
                 }
-                src = a.down.base + (size_t)id * a.down.stride;
+                wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kRowBytes,
+                          kSegBytes);
             } else {
-                src = a.sh_down.base;
+                wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kDownRows), kSegBytesS);
             }
-            wave_copy(wd + u * kSegBytes, src + (size_t)d0 * kRowBytes, kSegBytes);
         }
     } else {
         for (int q = wave - 8; q < nu * NBH; q += 8) {
@@ -219,23 +249,11 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
         if (threadIdx.x < kDownRows) a.out[d0 + threadIdx.x] = __builtin_nanf("");
         return;
     }
-    const int grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
-    if constexpr (TD == kTypeQ6K) {
-        // 8 lanes per row; a wave takes rows of one parity so that its 2-byte
-        // aligned rows share their 4-byte alignment
-        const int par = wave & 1, G = (wave >> 1) * 8 + (grp & 7);
-        for (int m = G; m < nu * kDownRows / 2; m += 64) {
-            const int rho = 2 * m + par, u = rho / kDownRows;
-            const float y = g8_row_q6k_u<NBH>(wd + rho * kRowBytes, q8h + u * NBH, t8);
-            if (t8 == 0) ys[rho] = y;
-        }
+    if constexpr (TS == TD) {
+        down_rows<TD, NBH>(wd, nu * kDownRows, 0, q8h, ys);  // the shared segment follows the routed ones
     } else {
-        // one 8-lane group per row, lane t taking super-block t
-        for (int rho = grp; rho < nu * kDownRows; rho += 128) {
-            const int u = rho / kDownRows;
-            const float y = lpb_row_q4k_mem<NBH>(wd + rho * kRowBytes, q8h[u * NBH + (t8 < NBH ? t8 : 0)], t8);
-            if (t8 == NBH - 1) ys[rho] = y;
-        }
+        down_rows<TD, NBH>(wd, k * kDownRows, 0, q8h, ys);
+        if (has_sh) down_rows<TS, NBH>(wd + k * kSegBytes, kDownRows, k, q8h, ys);
     }
     __syncthreads();
     if (threadIdx.x < kDownRows) {
@@ -249,7 +267,8 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 }  // namespace
 
 // Instantiated shapes: router n_embd 2048; gate/up Q4_K with 8 super-blocks
-// per row; down Q6_K with 2-4 or Q4_K with 4 super-blocks per row.
+// per row; down Q6_K with 2-4, Q5_K with 2 or 4, or Q4_K with 4 super-blocks
+// per row.
 bool layer_route_ok(const RouterArgs &a) { return a.n == 2048 && a.E <= 1024 && a.M == 1; }
 
 hipError_t launch_layer_route(const RouterArgs &a, hipStream_t s) {
@@ -265,10 +284,14 @@ bool layer_ffn_ok(const GateUpArgs &g, const DownArgs &d) {
     const int nbh = d.down.cols / QK;
     const bool q6 = d.down.type == kTypeQ6K && nbh >= 2 && nbh <= 4;
     const bool q4 = d.down.type == kTypeQ4K && nbh == 4;
-    if (!q6 && !q4) return false;
+    const bool q5 = d.down.type == kTypeQ5K && (nbh == 2 || nbh == 4);
+    if (!q6 && !q4 && !q5) return false;
     if (g.sh_gate.base) {
         if (g.sh_gate.type != kTypeQ4K || g.sh_up.type != kTypeQ4K || g.sh_gate.rows != g.gate.rows) return false;
-        if (!d.sh_down.base || d.sh_down.type != d.down.type || d.sh_down.cols != d.down.cols) return false;
+        if (!d.sh_down.base || d.sh_down.cols != d.down.cols) return false;
+        // a Q5_K routed down may have a Q6_K shared one; otherwise the types agree
+        if (d.sh_down.type != d.down.type && !(d.down.type == kTypeQ5K && d.sh_down.type == kTypeQ6K && nbh == 2))
+            return false;
     }
     // every copy source 16-byte aligned
     uintptr_t al = reinterpret_cast<uintptr_t>(g.gate.base) | reinterpret_cast<uintptr_t>(g.up.base) |
@@ -287,21 +310,27 @@ hipError_t launch_layer_gateup(const GateUpArgs &g, hipStream_t s) {
 }
 
 hipError_t launch_layer_down(const DownArgs &d, hipStream_t s) {
-    const int nu = d.k + (d.sh_down.base ? 1 : 0);
+    const bool has_sh = d.sh_down.base != nullptr;
+    const int nu = d.k + (has_sh ? 1 : 0);
     const int nbh = d.down.cols / QK;
+    const int ts = has_sh ? d.sh_down.type : d.down.type;
     const size_t seg = (size_t)kDownRows * nbh * block_bytes(d.down.type);
-    const size_t lds = nu * seg + (size_t)nu * nbh * sizeof(Q8L);
+    const size_t seg_s = has_sh ? (size_t)kDownRows * nbh * block_bytes(ts) : 0;
+    const size_t lds = d.k * seg + seg_s + (size_t)nu * nbh * sizeof(Q8L);
     if (lds > 65536) return hipErrorInvalidConfiguration;
     const dim3 dg((unsigned)(d.n_embd / kDownRows));
-#define HOARD_DOWN(TD, NBH)                                                                     \
-    if (d.down.type == TD && nbh == NBH) {                                                      \
-        hipLaunchKernelGGL((layer_down_kernel<TD, NBH>), dg, dim3(1024), lds, s, d);            \
+#define HOARD_DOWN(TD, NBH, TS)                                                                 \
+    if (d.down.type == TD && nbh == NBH && ts == TS) {                                          \
+        hipLaunchKernelGGL((layer_down_kernel<TD, NBH, TS>), dg, dim3(1024), lds, s, d);        \
         return hipGetLastError();                                                               \
     }
-    HOARD_DOWN(kTypeQ6K, 2)
-    HOARD_DOWN(kTypeQ6K, 3)
-    HOARD_DOWN(kTypeQ6K, 4)
-    HOARD_DOWN(kTypeQ4K, 4)
+    HOARD_DOWN(kTypeQ6K, 2, kTypeQ6K)
+    HOARD_DOWN(kTypeQ6K, 3, kTypeQ6K)
+    HOARD_DOWN(kTypeQ6K, 4, kTypeQ6K)
+    HOARD_DOWN(kTypeQ4K, 4, kTypeQ4K)
+    HOARD_DOWN(kTypeQ5K, 2, kTypeQ5K)
+    HOARD_DOWN(kTypeQ5K, 4, kTypeQ5K)
+    HOARD_DOWN(kTypeQ5K, 2, kTypeQ6K)
 #undef HOARD_DOWN
     return hipErrorInvalidConfiguration;
 }

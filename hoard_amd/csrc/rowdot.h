@@ -364,6 +364,78 @@ __device__ __forceinline__ float lpb_row_q4k_mem(const uint8_t *row, const Q8L &
     return acc - accm;
 }
 
+// Q5_K super-block (16-byte aligned: d/dmin and the Q4_K-packed scales in the
+// first 16 bytes, qh[32], qs[128]) against an activation block in memory: the
+// Q4_K sums with each quant's fifth bit taken from qh (bit 2j of qh[l] for
+// the low nibbles of chunk j, bit 2j+1 for the high ones).
+__device__ __forceinline__ void q5k_block_sums_mem(const uint8_t *blk, const Q8L &x, uint32_t &dm_bits, int &isum,
+                                                   int &msum) {
+    const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+    const uint4 h0 = *reinterpret_cast<const uint4 *>(blk + 16);
+    const uint4 h1 = *reinterpret_cast<const uint4 *>(blk + 32);
+    const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    dm_bits = hd.x;
+    const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+    auto byte = [&](int i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+    const uint4 *xq = reinterpret_cast<const uint4 *>(x.qs);
+    isum = 0;
+    msum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(blk + 48 + 32 * j);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(blk + 64 + 32 * j);
+        const uint4 x0 = xq[4 * j], x1 = xq[4 * j + 1], x2 = xq[4 * j + 2], x3 = xq[4 * j + 3];
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t ql = (qw[k] & 0x0f0f0f0fu) | (((qh[k] >> (2 * j)) & 0x01010101u) << 4);
+            const uint32_t qu = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((qh[k] >> (2 * j + 1)) & 0x01010101u) << 4);
+            lo = sdot4(ql, xl[k], lo);
+            hi = sdot4(qu, xh[k], hi);
+        }
+        const uint32_t bw = *reinterpret_cast<const uint32_t *>(&x.bsums[4 * j]);
+        const uint32_t bw1 = *reinterpret_cast<const uint32_t *>(&x.bsums[4 * j + 2]);
+        const int bsl = (int)(int16_t)(bw & 0xffffu) + (int)(int16_t)(bw >> 16);
+        const int bsh = (int)(int16_t)(bw1 & 0xffffu) + (int)(int16_t)(bw1 >> 16);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int s = 2 * j + h;
+            int sc, mn;
+            if (s < 4) {
+                sc = byte(s) & 63;
+                mn = byte(s + 4) & 63;
+            } else {
+                sc = (byte(s + 4) & 0x0f) | ((byte(s - 4) >> 6) << 4);
+                mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+            }
+            isum += sc * (h ? hi : lo);
+            msum += mn * (h ? bsh : bsl);
+        }
+    }
+}
+
+// One Q5_K row of NB super-blocks (16-byte aligned), one lane per block with
+// the lane's activation block xb read from memory; valid in lane NB-1.
+template <int NB>
+__device__ __forceinline__ float lpb_row_q5k_mem(const uint8_t *row, const Q8L &xb, int t) {
+    float p = 0.0f, pm = 0.0f;
+    if (t < NB) {
+        uint32_t dm;
+        int isum, msum;
+        q5k_block_sums_mem(row + t * kQ5KBytes, xb, dm, isum, msum);
+        const float d = half_bits_to_float(dm & 0xffffu) * xb.d;
+        const float dmin = half_bits_to_float(dm >> 16) * xb.d;
+        p = d * (float)isum;
+        pm = dmin * (float)msum;
+    }
+    const float acc = group_chain_sum<NB>(p, t);
+    const float accm = group_chain_sum<NB>(pm, t);
+    return acc - accm;
+}
+
 // Q8_K quantisation of 256 values held 4 per lane (lane l: elements 4l..4l+3).
 // The scale comes from the first element (lowest index) of largest magnitude:
 // a wave max of |x|, then the lowest lane holding it and its first component.
