@@ -26,6 +26,7 @@ ERR_UNSUPPORTED = -2
 ERR_HIP = -3
 ERR_OOM = -4
 ERR_STATE = -5
+ERR_IO = -6
 
 
 class HoardError(RuntimeError):
@@ -76,6 +77,19 @@ class KernelTimes(ctypes.Structure):
     _fields_ = [("launches", ctypes.c_uint64 * 8), ("total_ms", ctypes.c_double * 8)]
 
 
+class StoreLayer(ctypes.Structure):
+    _fields_ = [("off", ctypes.c_uint64 * 3), ("stride", ctypes.c_uint64 * 3)]
+
+
+class StoreCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("readers", "ram_experts", "direct", "pinned")]
+
+
+class StoreStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("requests", "ram_hits", "file_reads", "bytes_read", "read_ns")] + \
+               [("direct", ctypes.c_int32), ("ram_experts", ctypes.c_int32)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 # name -> (restype, argtypes); every symbol the public headers declare
@@ -107,6 +121,14 @@ ABI = {
     "hoard_gguf_layer_weights": (_I, [_P, _I, ctypes.POINTER(LayerWeights)]),
     "hoard_gguf_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64),
                                ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(_P)]),
+    "hoard_gguf_store_layers": (_I, [_P, ctypes.POINTER(StoreLayer), _I]),
+    "hoard_store_open": (_I, [ctypes.c_char_p, _I, _I, ctypes.POINTER(StoreLayer), ctypes.POINTER(StoreCfg),
+                              ctypes.POINTER(_P)]),
+    "hoard_store_close": (None, [_P]),
+    "hoard_store_fetch": (_I, [_P, _I, _I, _P, _P, _P]),
+    "hoard_store_get_stats": (_I, [_P, ctypes.POINTER(StoreStats)]),
+    "hoard_store_reset_stats": (_I, [_P]),
+    "hoard_moe_attach_store": (_I, [_P, _P]),
     "hoard_slot_lru_create": (_I, [_I, _I, _I, _I, ctypes.POINTER(_P)]),
     "hoard_slot_lru_access": (_I, [_P, _I, _P, _I, _P, _P]),
     "hoard_slot_lru_destroy": (None, [_P]),

@@ -441,4 +441,24 @@ int hoard_gguf_layer_weights(hoard_gguf *g, int layer, hoard_layer_weights *w) {
     return HOARD_OK;
 }
 
+int hoard_gguf_store_layers(const hoard_gguf *g, hoard_store_layer *layers, int n_layer) {
+    if (!g || !layers) return fail_fmt(HOARD_ERR_INVALID, "null argument");
+    hoard_moe_cfg c;
+    if (int rc = hoard_gguf_moe_cfg(g, &c)) return rc;
+    if (n_layer != c.n_layer) return fail_fmt(HOARD_ERR_INVALID, "%d layers asked of a file of %d", n_layer, c.n_layer);
+    const uint8_t *base = static_cast<const uint8_t *>(g->map);
+    static const char *kParts[3] = {"ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"};
+    for (int l = 0; l < n_layer; ++l)
+        for (int i = 0; i < 3; ++i) {
+            const std::string name = "blk." + std::to_string(l) + "." + kParts[i] + ".weight";
+            const Tensor *t = g->tensor(name);
+            if (!t) return fail_fmt(HOARD_ERR_INVALID, "no tensor %s", name.c_str());
+            if (t->nbytes == 0 || t->ne[2] != c.n_expert || t->nbytes % (size_t)c.n_expert)
+                return fail_fmt(HOARD_ERR_INVALID, "%s is not %d experts of a known type", name.c_str(), c.n_expert);
+            layers[l].off[i] = (uint64_t)(static_cast<const uint8_t *>(g->ptr(*t)) - base);
+            layers[l].stride[i] = (uint64_t)(t->nbytes / (size_t)c.n_expert);
+        }
+    return HOARD_OK;
+}
+
 }  // extern "C"

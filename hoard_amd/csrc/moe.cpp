@@ -15,6 +15,7 @@
 #include "hoard_moe.h"
 #include "kernels.h"
 #include "slot_lru.h"
+#include "store_impl.h"
 
 namespace {
 
@@ -117,6 +118,8 @@ struct hoard_moe {
     int32_t *pin_sel = nullptr;     // pinned [n_used]: device-routed ids read back on the on-demand path
     int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
     hipStream_t copy2 = nullptr;    // second upload stream: two copies in flight hide per-copy set-up
+    hoard::Store *store = nullptr;  // storage tier serving slot misses (attached), else pinned masters
+    bool weights_set = false;       // a layer's weights were set (a store attaches before that)
     // batched path (allocated on first use)
     uint8_t *b_q8x = nullptr, *b_q8h = nullptr;
     float *b_h = nullptr, *b_y = nullptr;
@@ -354,16 +357,52 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host,
     if (n_miss && L.used)
         for (int i = 0; i < n_up; ++i) HIP_TRY(hipStreamWaitEvent(up[i], L.last_use, 0));
     int m = 0;
-    for (int j = 0; j < n; ++j) {
-        h->stats.reqs += 1;
-        if (!miss[j]) {
-            h->stats.hits += 1;
-            continue;
+    if (h->store) {
+        // storage tier: the RAM tier serves or reads the missed experts (reads in
+        // parallel, on the host), then each is uploaded from its RAM entry,
+        // which is fenced until the upload is done
+        int32_t mids[16];
+        int mj[16], nm = 0;
+        for (int j = 0; j < n; ++j)
+            if (miss[j]) {
+                mj[nm] = j;
+                mids[nm++] = sel[j];
+            }
+        hoard::StoreEntry ent[16];
+        if (nm) {
+            if (int rc = h->store->fetch(layer, nm, mids, ent, nullptr)) {
+                h->lru.reset_layer(layer);  // the missed slots were not filled: forget the layer's residency
+                return rc;                  // the store has set the error text
+            }
         }
-        const size_t e = (size_t)sel[j], sl = (size_t)slots[j], rec = L.gstride;  // one [g|u|d] record
-        HIP_TRY(hipMemcpyAsync(L.slots + sl * rec, L.host_experts + e * rec, rec, hipMemcpyHostToDevice, up[m++ % n_up]));
-        h->stats.misses += 1;
-        h->stats.bytes_h2d += rec;
+        const size_t rec = L.gstride;
+        for (int i = 0; i < nm; ++i) {
+            uint8_t *dst = L.slots + (size_t)slots[mj[i]] * rec;
+            hipStream_t us = up[m++ % n_up];
+            HIP_TRY(hipMemcpyAsync(dst, ent[i].part[0], L.gbytes, hipMemcpyHostToDevice, us));
+            HIP_TRY(hipMemcpyAsync(dst + L.gbytes, ent[i].part[1], L.ubytes, hipMemcpyHostToDevice, us));
+            HIP_TRY(hipMemcpyAsync(dst + L.gbytes + L.ubytes, ent[i].part[2], L.dbytes, hipMemcpyHostToDevice, us));
+            if (int rc = h->store->fence(ent[i].slot, us)) return rc;
+        }
+        for (int j = 0; j < n; ++j) {
+            h->stats.reqs += 1;
+            h->stats.hits += miss[j] ? 0 : 1;
+            h->stats.misses += miss[j] ? 1 : 0;
+            h->stats.bytes_h2d += miss[j] ? rec : 0;
+        }
+    } else {
+        for (int j = 0; j < n; ++j) {
+            h->stats.reqs += 1;
+            if (!miss[j]) {
+                h->stats.hits += 1;
+                continue;
+            }
+            const size_t e = (size_t)sel[j], sl = (size_t)slots[j], rec = L.gstride;  // one [g|u|d] record
+            HIP_TRY(hipMemcpyAsync(L.slots + sl * rec, L.host_experts + e * rec, rec, hipMemcpyHostToDevice,
+                                   up[m++ % n_up]));
+            h->stats.misses += 1;
+            h->stats.bytes_h2d += rec;
+        }
     }
     if (n_miss) {
         hipEvent_t ev[2] = {L.copied, L.copied2};
@@ -727,7 +766,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
     if (!h || !w) return fail(HOARD_ERR_INVALID, "null argument");
     if (layer < 0 || layer >= h->cfg.n_layer) return fail(HOARD_ERR_INVALID, "layer %d out of range", layer);
     const hoard_moe_cfg &c = h->cfg;
-    if (!w->router || !w->gate || !w->up || !w->down) return fail(HOARD_ERR_INVALID, "missing tensor");
+    if (!w->router || (!h->store && (!w->gate || !w->up || !w->down))) return fail(HOARD_ERR_INVALID, "missing tensor");
     if (!quant_type_ok(w->gate_type) || !quant_type_ok(w->up_type) || !quant_type_ok(w->down_type))
         return fail(HOARD_ERR_UNSUPPORTED, "expert types %d/%d/%d: Q3_K (11), Q4_K (12), Q5_K (13) and Q6_K (14) are taken", w->gate_type,
                     w->up_type, w->down_type);
@@ -740,6 +779,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
                         w->sh_down_type);
     }
     HIP_TRY(hipSetDevice(h->device));
+    h->weights_set = true;
     Layer &L = h->layers[layer];
     hoard_moe::free_layer(L);
     L.gate_type = w->gate_type;
@@ -765,12 +805,19 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
             L.down = L.slots + L.gbytes + L.ubytes;
             L.gstride = L.ustride = L.dstride = rec;
         }
-        if (!rc && hipHostMalloc((void **)&L.host_experts, E * rec, hipHostMallocDefault) != hipSuccess) {
+        if (h->store) {  // expert bytes come from the storage tier on each miss
+            const hoard_store_layer &sl = h->store->layers[(size_t)layer];
+            if (!rc && (sl.stride[0] != L.gbytes || sl.stride[1] != L.ubytes || sl.stride[2] != L.dbytes))
+                rc = fail(HOARD_ERR_INVALID, "layer %d: the store's expert strides %llu/%llu/%llu are not the %zu/%zu/%zu "
+                          "bytes of types %d/%d/%d", layer, (unsigned long long)sl.stride[0],
+                          (unsigned long long)sl.stride[1], (unsigned long long)sl.stride[2], L.gbytes, L.ubytes,
+                          L.dbytes, L.gate_type, L.up_type, L.down_type);
+        } else if (!rc && hipHostMalloc((void **)&L.host_experts, E * rec, hipHostMallocDefault) != hipSuccess) {
             L.host_experts = nullptr;
             (void)hipGetLastError();
             rc = fail(HOARD_ERR_OOM, "hipHostMalloc(%zu) for the expert masters", E * rec);
         }
-        if (!rc) {
+        if (!rc && !h->store) {
             const uint8_t *g = static_cast<const uint8_t *>(w->gate), *u = static_cast<const uint8_t *>(w->up),
                           *d = static_cast<const uint8_t *>(w->down);
             for (size_t e = 0; e < E; ++e) {
@@ -889,6 +936,21 @@ int hoard_moe_pool_ensure(hoard_moe *h, int layer, const int32_t *sel_host, int3
     if (!sel_host || (!slot_host && !slot_dev)) return fail(HOARD_ERR_INVALID, "null argument");
     return pool_ensure(h, layer, sel_host, slot_host, slot_dev, (hipStream_t)stream,
                        copy_stream ? (hipStream_t)copy_stream : (hipStream_t)stream);
+}
+
+int hoard_moe_attach_store(hoard_moe *h, hoard_store *st) {
+    if (!h || !st) return fail(HOARD_ERR_INVALID, "null argument");
+    const hoard_moe_cfg &c = h->cfg;
+    if (c.pool_k == 0) return fail(HOARD_ERR_STATE, "a store serves a slot pool: the handle has pool_k == 0");
+    if (h->weights_set) return fail(HOARD_ERR_STATE, "attach the store before setting layer weights");
+    if (h->store) return fail(HOARD_ERR_STATE, "a store is attached already");
+    const hoard::Store &s = st->s;
+    if (s.n_layer != c.n_layer || s.n_expert != c.n_expert)
+        return fail(HOARD_ERR_INVALID, "store of %d layers x %d experts for a stage of %d x %d", s.n_layer, s.n_expert,
+                    c.n_layer, c.n_expert);
+    if (s.cap < c.n_used) return fail(HOARD_ERR_INVALID, "RAM tier of %d experts below n_used %d", s.cap, c.n_used);
+    h->store = &st->s;
+    return HOARD_OK;
 }
 
 int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,

@@ -36,15 +36,20 @@ class MoEStage:
             self.set_layer(li, hl)
 
     @classmethod
-    def from_gguf(cls, path, layers=None, pool_k: int = 0, max_tokens: int = 1) -> "MoEStage":
+    def from_gguf(cls, path, layers=None, pool_k: int = 0, max_tokens: int = 1, store=None) -> "MoEStage":
         """A stage holding the expert stage of every layer in `layers` (default:
         all) of a GGUF file.  The weights are copied in, so the file is closed
-        before this returns."""
+        before this returns.  With `store` (a hoard_amd.store.ExpertStore over
+        the same file) and pool_k > 0, slot misses stream from the store instead
+        of a pinned copy of every expert; the store must outlive the stage."""
         from .gguf import GGUFWeights
         with GGUFWeights(path) as g:
             shape = g.shape()
             st = cls(shape, pool_k=pool_k, max_tokens=max_tokens)
             try:
+                if store is not None:
+                    check(st.lib.hoard_moe_attach_store(st.h, store.h))
+                    st.store = store
                 for l in range(shape.n_layer) if layers is None else layers:
                     w = g.layer_weights(l)
                     check(st.lib.hoard_moe_set_layer_weights(st.h, l, ctypes.byref(w)))

@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "hoard_moe.h"
+#include "hoard_store.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -53,6 +54,11 @@ int hoard_gguf_layer_weights(hoard_gguf *g, int layer, hoard_layer_weights *w);
    pointer into the mapping.  HOARD_ERR_INVALID when absent. */
 int hoard_gguf_tensor(const hoard_gguf *g, const char *name, int32_t *type, int64_t ne[4], size_t *nbytes,
                       const void **data);
+
+/* Where each layer's gate, up and down expert tensors lie in the file, for
+   hoard_store_open: layers[0..n_layer) with n_layer from hoard_gguf_moe_cfg
+   (the offsets and strides load_model records, src/run_moe_stream.cpp:171-179). */
+int hoard_gguf_store_layers(const hoard_gguf *g, hoard_store_layer *layers, int n_layer);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,7 @@ extern "C" {
 #define HOARD_ERR_HIP (-3)         /* HIP runtime error */
 #define HOARD_ERR_OOM (-4)         /* device or pinned host allocation failed */
 #define HOARD_ERR_STATE (-5)       /* call not valid in the handle's state */
+#define HOARD_ERR_IO (-6)          /* reading the model file failed */
 
 /* ggml type ids accepted for expert tensors (ggml.h enum ggml_type). */
 #define HOARD_TYPE_F32 0
