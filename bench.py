@@ -48,6 +48,12 @@ def parse():
     ap.add_argument("--pool", type=int, default=0, metavar="K",
                     help="slot-pool workload: K HBM slots per layer, all experts in pinned host memory, "
                          "routing from the seeded 512-token Zipf(0.8)+reuse trace")
+    ap.add_argument("--store", action="store_true",
+                    help="with --pool: experts streamed from a GGUF file on local disk through the storage tier "
+                         "(RAM tier of --ram experts, --readers parallel O_DIRECT reads) instead of pinned masters")
+    ap.add_argument("--ram", type=int, default=256, help="storage tier: RAM-tier capacity in experts")
+    ap.add_argument("--readers", type=int, default=8, help="storage tier: reads in flight")
+    ap.add_argument("--store-dir", default="/tmp", help="storage tier: directory for the model file")
     ap.add_argument("--batch", type=int, default=0, metavar="M",
                     help="batched workload: M tokens per step (4, 8 or 16), routed independently, "
                          "grouped by expert on int8 MFMA")
@@ -160,13 +166,37 @@ def run_pool(args, shape, n_layer):
     cfg = shape.cfg(n_layer, K, 1)
     h = ctypes.c_void_p()
     H.check(lib.hoard_moe_create(ctypes.byref(cfg), ctypes.byref(h)))
-    hl = W.make_layer(shape, args.seed, 0)
-    for l in range(n_layer):
-        if l:
-            W.fill_layer(hl, args.seed, l)
-        H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(hl.weights())))
-    del hl
-    log(f"[bench] pool K={K}: {n_layer} layers of {shape.name} in pinned host memory "
+    store = path = None
+    if args.store:
+        import tempfile
+
+        sys.path.insert(0, str(ROOT / "tests"))
+        from gguf_writer import write_stage_streaming
+
+        from hoard_amd.gguf import GGUFWeights
+        from hoard_amd.store import ExpertStore
+        tmpdir = tempfile.mkdtemp(prefix="hoard_store_", dir=args.store_dir)
+        path = Path(tmpdir) / f"{shape.name}_{n_layer}l.gguf"
+        hl = W.make_layer(shape, args.seed, 0)
+        write_stage_streaming(path, shape, n_layer, lambda l: W.fill_layer(hl, args.seed, l) if l else hl,
+                              "qwen3moe" if shape.renorm else "olmoe")
+        del hl
+        log(f"[bench] wrote {path} ({path.stat().st_size / 1e9:.1f} GB, fsynced) in {time.perf_counter() - t0:.1f} s")
+        store = ExpertStore.from_gguf(path, readers=args.readers, ram_experts=args.ram, direct=True, pinned=True)
+        H.check(lib.hoard_moe_attach_store(h, store.h))
+        with GGUFWeights(path) as g:
+            for l in range(n_layer):
+                H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(g.layer_weights(l))))
+        where = f"streamed from {path} through a RAM tier of {store.stats().ram_experts} experts"
+    else:
+        hl = W.make_layer(shape, args.seed, 0)
+        for l in range(n_layer):
+            if l:
+                W.fill_layer(hl, args.seed, l)
+            H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(hl.weights())))
+        del hl
+        where = "in pinned host memory"
+    log(f"[bench] pool K={K}: {n_layer} layers of {shape.name} {where} "
         f"({n_layer * shape.n_expert * shape.expert_bytes() / 1e9:.1f} GB), "
         f"{n_layer * K * shape.expert_bytes() / 1e9:.2f} GB of HBM slots, in {time.perf_counter() - t0:.1f} s")
     trace = W.routing_trace(shape, args.seed, tokens=512, n_layer=n_layer)
@@ -199,6 +229,8 @@ def run_pool(args, shape, n_layer):
         token(t)
     torch.cuda.synchronize()
     H.check(lib.hoard_moe_reset_stats(h))
+    if store is not None:
+        store.reset_stats()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for t in range(warm, warm + steps):
@@ -209,6 +241,12 @@ def run_pool(args, shape, n_layer):
     st = H.MoeStats()
     H.check(lib.hoard_moe_get_stats(h, ctypes.byref(st)))
     lib.hoard_moe_destroy(h)
+    sst = None
+    if store is not None:
+        sst = store.stats()
+        store.close()
+        import shutil
+        shutil.rmtree(path.parent, ignore_errors=True)
     probe = h2d_probe_gbps()
     bytes_tok = st.bytes_h2d / steps
     result = {
@@ -228,6 +266,19 @@ def run_pool(args, shape, n_layer):
         "h2d_probe_gbps": round(probe, 2),
         "link_frac": round(bytes_tok / (ms * 1e-3) / 1e9 / probe, 4),
     }
+    if sst is not None:
+        result["metric"] = ("slot-pool decode tokens/s, Qwen3-30B-A3B-shape Q4_K, K-slot HBM LRU over a RAM tier "
+                            "streamed from the model file")
+        result["config"]["workload"] = (f"{shape.name}: {n_layer} layers, K={K} slots per layer, RAM tier of "
+                                        f"{sst.ram_experts} experts, the rest read from a GGUF on local disk")
+        result["config"].update(ram_experts=int(sst.ram_experts), readers=args.readers)
+        result["store"] = {
+            "requests": int(sst.requests), "ram_hits": int(sst.ram_hits), "file_reads": int(sst.file_reads),
+            "ram_hit_rate": round(sst.ram_hits / max(1, sst.requests), 4),
+            "read_gbps": round(sst.bytes_read / max(1, sst.read_ns), 3),
+            "read_ms_per_token": round(sst.read_ns / 1e6 / steps, 3),
+            "direct": int(sst.direct),
+        }
     print(json.dumps(result), flush=True)
 
 

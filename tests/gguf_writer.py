@@ -102,3 +102,52 @@ def write_layers(path, shape, layers: dict, arch: str, router_types=None, eps: f
         held[l] = (rf.ravel(), gi)
     write_gguf(path, kv, tensors)
     return held
+
+
+def write_stage_streaming(path, shape, n_layer: int, make_layer, arch: str, eps: float = 1e-6,
+                          alignment: int = 32):
+    """The expert stage of n_layer layers, layer by layer: make_layer(l) returns
+    layer l's HostLayer (same quant types in every layer), which is written and
+    dropped before the next is made.  f32 routers, bf16 shared gate rows."""
+    import os
+    from hoard_amd import expert_bytes
+    D, F, E, S = shape.n_embd, shape.n_ff, shape.n_expert, shape.n_ff_shexp
+    kv = [("general.architecture", STRING, arch), ("general.alignment", U32, alignment),
+          (f"{arch}.block_count", U32, n_layer), (f"{arch}.embedding_length", U32, D),
+          (f"{arch}.expert_feed_forward_length", U32, F), (f"{arch}.expert_count", U32, E),
+          (f"{arch}.expert_used_count", U32, shape.n_used),
+          (f"{arch}.attention.layer_norm_rms_epsilon", F32, eps)]
+    if S:
+        kv.append((f"{arch}.expert_shared_feed_forward_length", U32, S))
+    per_layer = [("ffn_gate_inp", GGML_F32, [D, E], 4 * D * E),
+                 ("ffn_gate_exps", shape.gate_type, [D, F, E], E * expert_bytes(shape.gate_type, F, D)),
+                 ("ffn_up_exps", shape.up_type, [D, F, E], E * expert_bytes(shape.up_type, F, D)),
+                 ("ffn_down_exps", shape.down_type, [F, D, E], E * expert_bytes(shape.down_type, D, F))]
+    if S:
+        per_layer += [("ffn_gate_shexp", shape.sh_gate_type, [D, S], expert_bytes(shape.sh_gate_type, S, D)),
+                      ("ffn_up_shexp", shape.sh_up_type, [D, S], expert_bytes(shape.sh_up_type, S, D)),
+                      ("ffn_down_shexp", shape.sh_down_type, [S, D], expert_bytes(shape.sh_down_type, D, S)),
+                      ("ffn_gate_inp_shexp", GGML_BF16, [D], 2 * D)]
+    infos, off = [], 0
+    for l in range(n_layer):
+        for name, t, ne, nb in per_layer:
+            infos.append(_str(f"blk.{l}.{name}.weight") + struct.pack("<I", len(ne))
+                         + b"".join(struct.pack("<Q", d) for d in ne) + struct.pack("<IQ", t, off))
+            off += nb + (-nb) % alignment
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(infos), len(kv))
+    head += b"".join(_str(k) + struct.pack("<I", t) + _value(t, v) for k, t, v in kv) + b"".join(infos)
+    head += b"\0" * ((-len(head)) % alignment)
+    with open(path, "wb") as f:
+        f.write(head)
+        for l in range(n_layer):
+            hl = make_layer(l)
+            blobs = [np.asarray(hl.router, np.float32).tobytes(), hl.gate, hl.up, hl.down]
+            if S:
+                blobs += [hl.sh_gate, hl.sh_up, hl.sh_down, bf16(hl.sh_gate_inp)]
+            for b, (_, _, _, nb) in zip(blobs, per_layer):
+                mv = memoryview(b).cast("B") if not isinstance(b, bytes) else b
+                assert len(mv) == nb
+                f.write(mv)
+                f.write(b"\0" * ((-nb) % alignment))
+        f.flush()
+        os.fsync(f.fileno())

@@ -256,3 +256,22 @@ def test_stage_layers_round_trip(tmp_path):
             assert np.array_equal(f32_at(w.router, 4 * 512), held[l][0])
             assert np.array_equal(f32_at(w.sh_gate_inp, 512), held[l][1])
         assert np.array_equal(held[0][0], layers[0].router.ravel())
+
+
+def test_streaming_writer_matches_layers(tmp_path):
+    """The layer-by-layer writer bench.py uses for its storage-tier workload."""
+    from gguf_writer import write_stage_streaming
+    from hoard_amd import workloads as W
+    shape = W.Shape("tiny", 0, 512, 4, 2, 256, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 3, n_ff_shexp=256)
+    layers = {l: W.make_layer(shape, 9, l) for l in range(3)}
+    p = tmp_path / "s.gguf"
+    write_stage_streaming(p, shape, 3, lambda l: layers[l], "qwen3next")
+    with GGUFWeights(p) as g:
+        c = g.cfg()
+        assert (c.n_layer, c.n_ff_shexp, c.n_expert) == (3, 256, 4)
+        for l, hl in layers.items():
+            w = g.layer_weights(l)
+            for name in ("gate", "up", "down", "sh_gate", "sh_up", "sh_down"):
+                a = getattr(hl, name)
+                assert read(getattr(w, name), a.nbytes) == a.tobytes(), (l, name)
+            assert np.array_equal(f32_at(w.router, 4 * 512), hl.router.ravel())
