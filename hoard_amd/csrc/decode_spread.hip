@@ -55,7 +55,7 @@ constexpr int kFlagStride = 32;   // ticket counters one 128-byte line apart
 constexpr int align16(int v) { return (v + 15) & ~15; }
 
 // Shape constants and LDS layout of one instantiation (byte offsets, 16-byte aligned).
-template <int NB, int NBH, int K, int E, bool SH>
+template <int NB, int NBH, int K, int E, bool SH, int TD, int TS>
 struct SpreadShape {
     static constexpr int kEmbd = NB * QK;
     static constexpr int kFF = NBH * QK;
@@ -69,7 +69,9 @@ struct SpreadShape {
     static constexpr int NDR = U * BLK;                 // down rows per workgroup (U blocks)
     static constexpr int RC = kEmbd / kPerXcd;          // combined rows per workgroup
     static constexpr int RBG = NB * kQ4KBytes;          // gate/up row bytes
-    static constexpr int RBD = NBH * kQ6KBytes;         // down row bytes
+    static constexpr int RBD = NBH * QType<TD>::bytes;  // routed down row bytes
+    static constexpr int RBDS = NBH * QType<TS>::bytes; // shared down row bytes
+    static constexpr int RBDM = RBD > RBDS ? RBD : RBDS;
     static constexpr int NGU = 2 * HR;                  // routed gate/up rows dotted per workgroup
     static constexpr int kGuWaves = (NGU + 7) / 8;      // waves with gate/up rows (8 per wave)
     static constexpr bool kTwoCopyWaves = kGuWaves <= 5;  // wave 5 free to copy a second down segment
@@ -85,7 +87,9 @@ struct SpreadShape {
     static_assert(HR <= 64 && 2 * HS <= 8, "h published by one wave; shared rows on one wave");
     static_assert(RC == 64 && U <= 16, "one combined row per lane of one wave");
     static_assert(2 * NBH <= 6, "Q8_K(h) of two units on waves 0-5");
-    static_assert((BLK * RBD) % 16 == 0, "down segments start 16-byte aligned");
+    static_assert((BLK * RBD) % 16 == 0 && (BLK * RBDS) % 16 == 0, "down segments start 16-byte aligned");
+    static_assert((TD == kTypeQ6K || TD == kTypeQ5K) && (TS == kTypeQ6K || TS == kTypeQ5K) && (SH || TS == TD),
+                  "Q6_K or Q5_K down rows");
 
     static constexpr int oXS = 0;
     static constexpr int oWR = oXS + 4 * kEmbd;
@@ -93,7 +97,7 @@ struct SpreadShape {
     static constexpr int oSHGU = oSGR + (SH ? 4 * kEmbd : 0);
     static constexpr int oGU = align16(oSHGU + 2 * HS * RBG);
     static constexpr int oDN = align16(oGU + 2 * HR * RBG);
-    static constexpr int oQ8X = align16(oDN + NDR * RBD);
+    static constexpr int oQ8X = align16(oDN + NDR * RBDM);
     static constexpr int oQ8H = oQ8X + (int)sizeof(Q8L) * NB;
     static constexpr int oHB = oQ8H + (int)sizeof(Q8L) * 2 * NBH;
     static constexpr int oLG = oHB + 4 * 2 * kFF;
@@ -139,12 +143,26 @@ __device__ __forceinline__ float half_wave_dot(const float *w, const float *x, f
     return row16_ggml_fold(acc);
 }
 
-template <int NB, int NBH, int K, int E, bool SH>
+// One down row of type T (NBH super-blocks) against unit lu's Q8_K(h): Q6_K
+// rows take 8 lanes per super-block (valid in lane 0 of the group), Q5_K rows
+// one lane per super-block (valid in lane NBH-1).
+template <int T, int NBH>
+__device__ __forceinline__ void down_row(const uint8_t *row, const Q8L *q8h, int lu, int t8, float *out) {
+    if constexpr (T == kTypeQ6K) {
+        const float y = g8_row_q6k_u<NBH>(row, q8h + lu * NBH, t8);
+        if (t8 == 0) *out = y;
+    } else {
+        const float y = lpb_row_q5k_mem<NBH>(row, q8h[lu * NBH + (t8 < NBH ? t8 : 0)], t8);
+        if (t8 == NBH - 1) *out = y;
+    }
+}
+
+template <int NB, int NBH, int K, int E, bool SH, int TD, int TS>
 __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
-    using S = SpreadShape<NB, NBH, K, E, SH>;
+    using S = SpreadShape<NB, NBH, K, E, SH, TD, TS>;
     constexpr int kEmbd = S::kEmbd, kFF = S::kFF, U = S::U, HR = S::HR, HS = S::HS, RR = S::RR;
     constexpr int BLK = S::BLK, NBLK = S::NBLK, NDR = S::NDR, RC = S::RC;
-    constexpr int RBG = S::RBG, RBD = S::RBD, NGU = S::NGU, kCand = S::kCand;
+    constexpr int RBG = S::RBG, NGU = S::NGU, kCand = S::kCand;
 
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red_mx[kWaves];
@@ -186,6 +204,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     const int q0 = g * U, ua = q0 / NBLK, ba = q0 % NBLK;
     const int na = U < NBLK - ba ? U : NBLK - ba, nbb = U - na;
     const int nunits = nbb ? 2 : 1;  // units whose h this workgroup needs
+    const int RBa = ua < K ? S::RBD : S::RBDS, RBb = ua + 1 < K ? S::RBD : S::RBDS;  // row bytes of the two units
     const int rrow0 = g * RR;
     const bool has_router = rrow0 < E;
 
@@ -431,10 +450,10 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         const uint8_t *srcA = ua < K ? L.down + (size_t)expert(ua) * L.dstride : L.sh_down;
         const uint8_t *srcB = ua + 1 < K ? L.down + (size_t)expert(ua + 1) * L.dstride : L.sh_down;
         if (wave == 6) {
-            const int b = dma_seg(smem + S::oDN, srcA + (size_t)ba * BLK * RBD, na * BLK * RBD, 0, 0, 1);
-            if (nbb && !S::kTwoCopyWaves) dma_seg(smem + S::oDN + na * BLK * RBD, srcB, nbb * BLK * RBD, b, 0, 1);
+            const int b = dma_seg(smem + S::oDN, srcA + (size_t)ba * BLK * RBa, na * BLK * RBa, 0, 0, 1);
+            if (nbb && !S::kTwoCopyWaves) dma_seg(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, b, 0, 1);
         } else if (S::kTwoCopyWaves && wave == 5) {
-            if (nbb) dma_seg(smem + S::oDN + na * BLK * RBD, srcB, nbb * BLK * RBD, 0, 0, 1);
+            if (nbb) dma_seg(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, 0, 0, 1);
         } else if (wave < S::kGuWaves) {
             if (grp < NGU) {
                 // one row per 8-lane group: the lane reads its activation block as it goes
@@ -499,8 +518,16 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                 if (m < NDR / 2) {
                     const int i = 2 * m + par;
                     const int lu = (q0 + i / BLK) / NBLK - ua;  // 0 or 1
-                    const float y = g8_row_q6k_u<NBH>(smem + S::oDN + i * RBD, q8h + lu * NBH, t8);
-                    if (t8 == 0) ys[i] = y;
+                    const int ia = na * BLK;                    // rows of the first unit
+                    const uint8_t *row = smem + S::oDN + (i < ia ? i * RBa : ia * RBa + (i - ia) * RBb);
+                    if constexpr (TS == TD) {
+                        down_row<TD, NBH>(row, q8h, lu, t8, &ys[i]);
+                    } else {
+                        if (ua + lu == K)
+                            down_row<TS, NBH>(row, q8h, lu, t8, &ys[i]);
+                        else
+                            down_row<TD, NBH>(row, q8h, lu, t8, &ys[i]);
+                    }
                 }
             }
         }
@@ -555,19 +582,22 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
 
 }  // namespace
 
-// The shapes with an instantiated kernel: {n_embd/256, n_ff/256, k, E, shared expert}.
-#define HOARD_SPREAD_SHAPES(X) \
-    X(8, 2, 10, 512, true)     \
-    X(8, 3, 8, 128, false)
+// The shapes with an instantiated kernel: {n_embd/256, n_ff/256, k, E, shared expert,
+// routed down type, shared down type}: Qwen3-Next, the Qwen3-30B shape, Qwen3.5.
+#define HOARD_SPREAD_SHAPES(X)                   \
+    X(8, 2, 10, 512, true, kTypeQ6K, kTypeQ6K)   \
+    X(8, 3, 8, 128, false, kTypeQ6K, kTypeQ6K)   \
+    X(8, 2, 8, 256, true, kTypeQ5K, kTypeQ6K)
 
 using SpreadFn = void (*)(SpreadArgs);
 
 static SpreadFn spread_fn(const SpreadArgs &a, size_t *lds) {
-#define HOARD_PICK(P_NB, P_NBH, P_K, P_E, P_SH)                                                 \
+#define HOARD_PICK(P_NB, P_NBH, P_K, P_E, P_SH, P_TD, P_TS)                                     \
     if (a.n_embd == P_NB * QK && a.n_ff == P_NBH * QK && a.k == P_K && a.E == P_E &&                \
-        (a.shared != 0) == P_SH) {                                                                  \
-        *lds = SpreadShape<P_NB, P_NBH, P_K, P_E, P_SH>::kBytes;                                    \
-        return spread_kernel<P_NB, P_NBH, P_K, P_E, P_SH>;                                          \
+        (a.shared != 0) == P_SH && (a.d_type < 0 || a.d_type == P_TD) &&                            \
+        (a.sh_d_type < 0 || !P_SH || a.sh_d_type == P_TS)) {                                        \
+        *lds = SpreadShape<P_NB, P_NBH, P_K, P_E, P_SH, P_TD, P_TS>::kBytes;                        \
+        return spread_kernel<P_NB, P_NBH, P_K, P_E, P_SH, P_TD, P_TS>;                              \
     }
     HOARD_SPREAD_SHAPES(HOARD_PICK)
 #undef HOARD_PICK

@@ -140,6 +140,7 @@ struct SpreadArgs {
     float eps;
     int renorm;
     int n_embd, n_ff, E, k, shared;  // select the instantiation (shared: n_ff_shexp == n_ff)
+    int d_type, sh_d_type;           // down types of the routed and shared experts (-1: any)
     // exchanged values carry their sequence number: {float bits, seq} per 64-bit word
     uint64_t *LG;               // [256][E]             router logits, one mailbox per workgroup
     uint64_t *H;                // [(k+shared)*n_ff]    h of the routed experts, then the shared one

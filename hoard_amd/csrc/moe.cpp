@@ -453,6 +453,7 @@ hoard::SpreadArgs spread_shape(const hoard_moe_cfg &c) {
     a.E = c.n_expert;
     a.k = c.n_used;
     a.shared = c.n_ff_shexp > 0 ? 1 : 0;
+    a.d_type = a.sh_d_type = -1;  // any: the layers' types are checked at launch
     return a;
 }
 
@@ -533,14 +534,14 @@ template <class Skip>
 int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t s, bool *used, Skip skip) {
     const hoard_moe_cfg &c = h->cfg;
     const bool sh = c.n_ff_shexp > 0;
+    const int d_type = h->layers[l0].down_type, sh_d_type = sh ? h->layers[l0].sh_down_type : d_type;
     for (int l = l0; l < l1; ++l) {
         const Layer &L = h->layers[l];
-        if (L.gate_type != HOARD_TYPE_Q4_K || L.down_type != HOARD_TYPE_Q6_K)
-            return skip("rows-spread decode takes Q4_K gate/up and Q6_K down");
+        if (L.gate_type != HOARD_TYPE_Q4_K || L.up_type != HOARD_TYPE_Q4_K || L.down_type != d_type)
+            return skip("rows-spread decode takes Q4_K gate/up and one down type over the range");
         if (sh) {
-            if (L.sh_gate_type != HOARD_TYPE_Q4_K || L.sh_up_type != HOARD_TYPE_Q4_K ||
-                L.sh_down_type != HOARD_TYPE_Q6_K)
-                return skip("rows-spread decode takes a Q4_K/Q4_K/Q6_K shared expert");
+            if (L.sh_gate_type != HOARD_TYPE_Q4_K || L.sh_up_type != HOARD_TYPE_Q4_K || L.sh_down_type != sh_d_type)
+                return skip("rows-spread decode takes a Q4_K/Q4_K shared expert of one down type over the range");
             const uintptr_t al = reinterpret_cast<uintptr_t>(L.sh_gate) | reinterpret_cast<uintptr_t>(L.sh_up) |
                                  reinterpret_cast<uintptr_t>(L.sh_down) | reinterpret_cast<uintptr_t>(L.sh_gate_inp);
             if (al & 15) return skip("shared expert tensors are not 16-byte aligned");
@@ -548,6 +549,9 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
         if (reinterpret_cast<uintptr_t>(L.router) & 15) return skip("router is not 16-byte aligned");
     }
     hoard::SpreadArgs a = spread_shape(c);
+    a.d_type = d_type;
+    a.sh_d_type = sh_d_type;
+    if (!hoard::spread_shape_compiled(a)) return skip("no rows-spread kernel for these down types");
     a.layers = h->d_table;
     a.l0 = l0;
     a.l1 = l1;

@@ -213,8 +213,8 @@ def test_persistent_decode_matches_oracle_and_launch_path(orc, shape):
         st.close()
 
 
-@pytest.mark.parametrize("shape,kernel", [(W.QWEN3_NEXT, 0), (W.QWEN3_30B, 2)],
-                         ids=["qwen3_next-auto", "qwen3_30b-spread"])
+@pytest.mark.parametrize("shape,kernel", [(W.QWEN3_NEXT, 0), (W.QWEN3_30B, 2), (W.QWEN35, 0)],
+                         ids=["qwen3_next-auto", "qwen3_30b-spread", "qwen35-auto"])
 def test_spread_decode_matches_oracle_and_launch_path(orc, shape, kernel):
     """One-launch decode with every expert's rows spread over all CUs (router over all
     E, top-k of up to 512, shared expert, combine, rms_norm) against the oracle layer by
@@ -308,5 +308,9 @@ def test_decode_splits_the_range_where_layer_types_change(orc):
         st.set_option(H.OPT_PERSISTENT_DECODE, 0)
         launched = st.decode(x, 0, 4, W.RMS_EPS)
         assert np.array_equal(launched.view(np.uint32), xs[-1].view(np.uint32))
+        st.set_option(H.OPT_PERSISTENT_DECODE, 2)  # one launch over mixed types: refused before any launch
+        with pytest.raises(H.HoardError) as ei:
+            st.decode(x, 0, 4, W.RMS_EPS)
+        assert ei.value.code == H.ERR_UNSUPPORTED
     finally:
         st.close()
