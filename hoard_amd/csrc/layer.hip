@@ -103,13 +103,15 @@ __global__ __launch_bounds__(128) void layer_route_kernel(RouterArgs a) {
 }
 
 // -- gate/up + SwiGLU ---------------------------------------------------------
-// grid = (n_ff / 16, k + shared), block = 512.  Q4_K rows of NB super-blocks.
+// grid = (n_ff / 16, k + shared), block = 512.  Rows of NB super-blocks of type
+// TG (Q4_K or Q3_K), the same for the routed and the shared expert.
 // Waves 0-3 copy the rows, waves 4-7 form Q8_K(fx) meanwhile: the compiler
 // cannot see the copies, so a wave that issued them would wait for them at
 // its first use of a loaded value.
-template <int NB>
+template <int NB, int TG>
 __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
-    constexpr int kRowBytes = NB * kQ4KBytes;
+    constexpr int kRowBytes = NB * QType<TG>::bytes;
+    static_assert(kRowBytes % 16 == 0, "rows stay 16-byte aligned");
     __shared__ __align__(16) uint8_t wt[2][kGuRows * kRowBytes];
     __shared__ __align__(16) Q8L q8[NB];
     __shared__ float gu[2 * kGuRows];
@@ -159,7 +161,11 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
         // one 8-lane group per row, lane t taking super-block t
         const int grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
         const int m = grp >= kGuRows, row = grp - m * kGuRows;
-        const float v = lpb_row_q4k_mem<NB>(wt[m] + row * kRowBytes, q8[t8], t8);
+        float v;
+        if constexpr (TG == kTypeQ3K)
+            v = lpb_row_q3k_mem<NB>(wt[m] + row * kRowBytes, q8[t8 < NB ? t8 : 0], t8);
+        else
+            v = lpb_row_q4k_mem<NB>(wt[m] + row * kRowBytes, q8[t8], t8);
         if (t8 == NB - 1) gu[grp] = v;
     }
     __syncthreads();
@@ -266,9 +272,9 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 
 }  // namespace
 
-// Instantiated shapes: router n_embd 2048; gate/up Q4_K with 8 super-blocks
-// per row; down Q6_K with 2-4, Q5_K with 2 or 4, or Q4_K with 4 super-blocks
-// per row.
+// Instantiated shapes: router n_embd 2048; gate/up Q4_K or Q3_K with 8
+// super-blocks per row; down Q6_K with 2-4, Q5_K with 2 or 4, or Q4_K with 4
+// super-blocks per row.
 bool layer_route_ok(const RouterArgs &a) { return a.n == 2048 && a.E <= 1024 && a.M == 1; }
 
 hipError_t launch_layer_route(const RouterArgs &a, hipStream_t s) {
@@ -279,7 +285,8 @@ hipError_t launch_layer_route(const RouterArgs &a, hipStream_t s) {
 }
 
 bool layer_ffn_ok(const GateUpArgs &g, const DownArgs &d) {
-    if (g.n_embd != 2048 || g.gate.type != kTypeQ4K || g.up.type != kTypeQ4K || g.gate.rows % kGuRows) return false;
+    const bool gu_type = (g.gate.type == kTypeQ4K || g.gate.type == kTypeQ3K) && g.up.type == g.gate.type;
+    if (g.n_embd != 2048 || !gu_type || g.gate.rows % kGuRows) return false;
     if (d.k > 16 || d.n_embd % kDownRows) return false;
     const int nbh = d.down.cols / QK;
     const bool q6 = d.down.type == kTypeQ6K && nbh >= 2 && nbh <= 4;
@@ -287,7 +294,7 @@ bool layer_ffn_ok(const GateUpArgs &g, const DownArgs &d) {
     const bool q5 = d.down.type == kTypeQ5K && (nbh == 2 || nbh == 4);
     if (!q6 && !q4 && !q5) return false;
     if (g.sh_gate.base) {
-        if (g.sh_gate.type != kTypeQ4K || g.sh_up.type != kTypeQ4K || g.sh_gate.rows != g.gate.rows) return false;
+        if (g.sh_gate.type != g.gate.type || g.sh_up.type != g.gate.type || g.sh_gate.rows != g.gate.rows) return false;
         if (!d.sh_down.base || d.sh_down.cols != d.down.cols) return false;
         // a Q5_K routed down may have a Q6_K shared one; otherwise the types agree
         if (d.sh_down.type != d.down.type && !(d.down.type == kTypeQ5K && d.sh_down.type == kTypeQ6K && nbh == 2))
@@ -305,7 +312,10 @@ bool layer_ffn_ok(const GateUpArgs &g, const DownArgs &d) {
 
 hipError_t launch_layer_gateup(const GateUpArgs &g, hipStream_t s) {
     const dim3 gg((unsigned)(g.gate.rows / kGuRows), (unsigned)(g.k + (g.sh_gate.base ? 1 : 0)));
-    hipLaunchKernelGGL(layer_gateup_kernel<8>, gg, dim3(512), 0, s, g);
+    if (g.gate.type == kTypeQ3K)
+        hipLaunchKernelGGL((layer_gateup_kernel<8, kTypeQ3K>), gg, dim3(512), 0, s, g);
+    else
+        hipLaunchKernelGGL((layer_gateup_kernel<8, kTypeQ4K>), gg, dim3(512), 0, s, g);
     return hipGetLastError();
 }
 
