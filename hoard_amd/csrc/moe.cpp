@@ -38,6 +38,10 @@ int fail(int code, const char *fmt, ...) {
     } while (0)
 
 constexpr size_t kTailPad = 4096;  // kernels read whole 1 KB chunks past the end of a staged run
+// Slot uploads in flight at once (the caller's copy stream and two more): on
+// the 128-expert pool workload 3 streams move 46.9 GB/s of host-to-HBM traffic
+// against 45.5 for 2; a fourth adds nothing.
+constexpr int kUpStreams = 3;
 
 bool quant_type_ok(int t) {
     return t == HOARD_TYPE_Q4_K || t == HOARD_TYPE_Q6_K || t == HOARD_TYPE_Q5_K || t == HOARD_TYPE_Q3_K;
@@ -63,8 +67,7 @@ struct Layer {
     // reference's RAM tier, here never evicted)
     uint8_t *slots = nullptr;
     uint8_t *host_experts = nullptr;
-    hipEvent_t copied = nullptr;    // last uploads into this layer's slots (copy stream)
-    hipEvent_t copied2 = nullptr;   // the same on the second copy stream
+    hipEvent_t copied[kUpStreams] = {};  // last uploads into this layer's slots, per upload stream
     hipEvent_t last_use = nullptr;  // last FFN reading this layer's slots (compute stream)
     bool used = false;              // last_use has been recorded
     int32_t *slot_stage = nullptr;  // pinned staging of the slot ids handed to the device
@@ -117,7 +120,8 @@ struct hoard_moe {
     bool pool_naive = false;
     int32_t *pin_sel = nullptr;     // pinned [n_used]: device-routed ids read back on the on-demand path
     int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
-    hipStream_t copy2 = nullptr;    // second upload stream: two copies in flight hide per-copy set-up
+    hipStream_t copy_x[kUpStreams - 1] = {};  // upload streams besides the caller's: copies in flight
+                                              // together hide each one's set-up
     hoard::Store *store = nullptr;  // storage tier serving slot misses (attached), else pinned masters
     bool weights_set = false;       // a layer's weights were set (a store attaches before that)
     // batched path (allocated on first use)
@@ -160,7 +164,8 @@ struct hoard_moe {
         hipFree(ptrace);
         hipHostFree(pin_sel);
         hipFree(slot_ids);
-        if (copy2) hipStreamDestroy(copy2);
+        for (auto cx : copy_x)
+            if (cx) hipStreamDestroy(cx);
         hipFree(b_q8x);
         hipFree(b_q8h);
         hipFree(b_h);
@@ -170,8 +175,8 @@ struct hoard_moe {
         hipFree(b_counters);
     }
     static void free_layer(Layer &L) {
-        if (L.copied) hipEventDestroy(L.copied);
-        if (L.copied2) hipEventDestroy(L.copied2);
+        for (auto ev : L.copied)
+            if (ev) hipEventDestroy(ev);
         if (L.last_use) hipEventDestroy(L.last_use);
         if (L.staged) hipEventDestroy(L.staged);
         hipHostFree(L.host_experts);
@@ -350,10 +355,12 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host,
     h->lru.access(layer, sel, n, h->pool_naive, slots, miss);
     int n_miss = 0;
     for (int j = 0; j < n; ++j) n_miss += miss[j];
-    // misses alternate between the caller's copy stream and a second one; both
-    // first wait until the last FFN reading this layer's slots is done
-    hipStream_t up[2] = {cs, h->copy2};
-    const int n_up = n_miss > 1 ? 2 : 1;
+    // misses are dealt round-robin to the caller's copy stream and the internal
+    // ones; each first waits until the last FFN reading this layer's slots is done
+    hipStream_t up[kUpStreams];
+    up[0] = cs;
+    for (int i = 1; i < kUpStreams; ++i) up[i] = h->copy_x[i - 1];
+    const int n_up = n_miss < kUpStreams ? (n_miss > 0 ? n_miss : 1) : kUpStreams;
     if (n_miss && L.used)
         for (int i = 0; i < n_up; ++i) HIP_TRY(hipStreamWaitEvent(up[i], L.last_use, 0));
     int m = 0;
@@ -405,10 +412,9 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host,
         }
     }
     if (n_miss) {
-        hipEvent_t ev[2] = {L.copied, L.copied2};
         for (int i = 0; i < n_up; ++i) {
-            HIP_TRY(hipEventRecord(ev[i], up[i]));
-            HIP_TRY(hipStreamWaitEvent(s, ev[i], 0));
+            HIP_TRY(hipEventRecord(L.copied[i], up[i]));
+            HIP_TRY(hipStreamWaitEvent(s, L.copied[i], 0));
         }
     }
     if (slot_host) std::memcpy(slot_host, slots, sizeof(int32_t) * n);
@@ -747,8 +753,9 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
         if (hipHostMalloc((void **)&h->pin_sel, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
             rc = fail(HOARD_ERR_OOM, "pinned selection buffer");
         rc = rc ? rc : dev_alloc((void **)&h->slot_ids, sizeof(int32_t) * c.n_used);
-        if (!rc && hipStreamCreateWithFlags(&h->copy2, hipStreamNonBlocking) != hipSuccess)
-            rc = fail(HOARD_ERR_HIP, "second copy stream");
+        for (int i = 0; !rc && i < kUpStreams - 1; ++i)
+            if (hipStreamCreateWithFlags(&h->copy_x[i], hipStreamNonBlocking) != hipSuccess)
+                rc = fail(HOARD_ERR_HIP, "upload stream");
     }
     if (!rc) rc = persistent_setup(h);
     if (rc) {
@@ -833,8 +840,9 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
         }
         if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
             rc = fail(HOARD_ERR_OOM, "pinned slot staging");
-        if (!rc && (hipEventCreateWithFlags(&L.copied, hipEventDisableTiming) != hipSuccess ||
-                    hipEventCreateWithFlags(&L.copied2, hipEventDisableTiming) != hipSuccess ||
+        for (int i = 0; !rc && i < kUpStreams; ++i)
+            if (hipEventCreateWithFlags(&L.copied[i], hipEventDisableTiming) != hipSuccess) rc = fail(HOARD_ERR_HIP, "pool events");
+        if (!rc && (
                     hipEventCreateWithFlags(&L.last_use, hipEventDisableTiming) != hipSuccess ||
                     hipEventCreateWithFlags(&L.staged, hipEventDisableTiming) != hipSuccess))
             rc = fail(HOARD_ERR_HIP, "pool events");
