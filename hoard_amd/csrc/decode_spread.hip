@@ -143,17 +143,16 @@ __device__ __forceinline__ float half_wave_dot(const float *w, const float *x, f
     return row16_ggml_fold(acc);
 }
 
-// One down row of type T (NBH super-blocks) against unit lu's Q8_K(h): Q6_K
-// rows take 8 lanes per super-block (valid in lane 0 of the group), Q5_K rows
-// one lane per super-block (valid in lane NBH-1).
+// One down row of type T (NBH super-blocks) against unit lu's Q8_K(h), by an
+// 8-lane group (each lane an eighth of every super-block); valid in lane 0.
 template <int T, int NBH>
 __device__ __forceinline__ void down_row(const uint8_t *row, const Q8L *q8h, int lu, int t8, float *out) {
     if constexpr (T == kTypeQ6K) {
         const float y = g8_row_q6k_u<NBH>(row, q8h + lu * NBH, t8);
         if (t8 == 0) *out = y;
     } else {
-        const float y = lpb_row_q5k_mem<NBH>(row, q8h[lu * NBH + (t8 < NBH ? t8 : 0)], t8);
-        if (t8 == NBH - 1) *out = y;
+        const float y = g8_row_q5k(row, q8h + lu * NBH, NBH, t8);
+        if (t8 == 0) *out = y;
     }
 }
 

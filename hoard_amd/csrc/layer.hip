@@ -197,11 +197,13 @@ __device__ __forceinline__ void down_rows(const uint8_t *base, int n, int u0, co
             const int u = u0 + r / kDownRows;
             const Q8L &xb = q8h[u * NB + (t8 < NB ? t8 : 0)];
             float y;
-            if constexpr (T == kTypeQ5K)
-                y = lpb_row_q5k_mem<NB>(base + r * kRowBytes, xb, t8);
-            else
+            if constexpr (T == kTypeQ5K) {
+                y = g8_row_q5k(base + r * kRowBytes, q8h + u * NB, NB, t8);  // 8 lanes per super-block
+                if (t8 == 0) ys[u0 * kDownRows + r] = y;
+            } else {
                 y = lpb_row_q4k_mem<NB>(base + r * kRowBytes, xb, t8);
-            if (t8 == NB - 1) ys[u0 * kDownRows + r] = y;
+                if (t8 == NB - 1) ys[u0 * kDownRows + r] = y;
+            }
         }
     }
 }

@@ -73,6 +73,47 @@ __device__ __forceinline__ float g8_row_q4k(const uint8_t *row, const Q8L *x, in
     return acc - accm;
 }
 
+// One Q5_K row of nb super-blocks (16-byte aligned in LDS) dotted with x:
+// g8_row_q4k with the fifth bit of each quant from qh.  Lane t covers quant
+// bytes [16t, 16t+16) (chunk t/2, positions l = 16(t&1) .. +15) and the qh
+// bytes of the same positions, bits 2(t/2) and 2(t/2)+1.
+__device__ __forceinline__ float g8_row_q5k(const uint8_t *row, const Q8L *x, int nb, int t) {
+    const int c = t >> 1, h = t & 1;
+    float acc = 0.0f, accm = 0.0f;
+#pragma unroll
+    for (int b = 0; b < nb; ++b) {
+        const uint8_t *blk = row + b * kQ5KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qh = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * h);
+        const uint4 q = *reinterpret_cast<const uint4 *>(blk + 48 + 16 * t);
+        const Q8L &xb = x[b];
+        const uint4 xl = *reinterpret_cast<const uint4 *>(&xb.qs[16 * c + 4 * h]);
+        const uint4 xh = *reinterpret_cast<const uint4 *>(&xb.qs[16 * c + 8 + 4 * h]);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+        const uint32_t xlw[4] = {xl.x, xl.y, xl.z, xl.w}, xhw[4] = {xh.x, xh.y, xh.z, xh.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lo = sdot4((qw[k] & 0x0f0f0f0fu) | (((hw[k] >> (2 * c)) & 0x01010101u) << 4), xlw[k], lo);
+            hi = sdot4(((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> (2 * c + 1)) & 0x01010101u) << 4), xhw[k], hi);
+        }
+        int sc0, m0, sc1, m1;
+        q4k_scale_min(2 * c, hd.y, hd.z, hd.w, sc0, m0);
+        q4k_scale_min(2 * c + 1, hd.y, hd.z, hd.w, sc1, m1);
+        int isum = sc0 * lo + sc1 * hi;
+        int msum = h ? 0
+                     : m0 * ((int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
+                           m1 * ((int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
+        isum = group8_sum(isum);
+        msum = group8_sum(msum);
+        const float d = half_bits_to_float(hd.x & 0xffffu) * xb.d;
+        const float dm = half_bits_to_float(hd.x >> 16) * xb.d;
+        acc = acc + d * (float)isum;
+        accm = accm + dm * (float)msum;
+    }
+    return acc - accm;
+}
+
 // One Q6_K row of nb super-blocks (2-byte aligned in LDS) dotted with x.
 // Lane t covers positions l in [8*(t&3), +8) of half t>>2 for all four
 // 32-element quarters: 32 of the block's 256 elements.
