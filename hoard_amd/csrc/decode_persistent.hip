@@ -131,7 +131,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     const int rw = E / kPerXcd;  // router rows per workgroup
     constexpr int nb = NB, nbh = NBH;
     constexpr int kEmbd = NB * QK;
-    static_assert(TGU == kTypeQ4K, "gate/up rows are Q4_K");
+    static_assert(TGU == kTypeQ4K || TGU == kTypeQ3K, "gate/up rows are Q4_K or Q3_K");
+    static_assert(TD == kTypeQ6K || TD == kTypeQ5K || TD == kTypeQ4K, "down rows are Q6_K, Q5_K or Q4_K");
     static_assert(2 * (NBH * QK / kPerXcd) <= kThreads / 8, "one 8-lane group per gate/up row");
     const int R = a.rows_gu, RD = a.rows_d;
     const bool has_expert = (int)xcc < k;
@@ -389,7 +390,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 if (pr < 2 * kR) {
                     const int mat = pr >= kR, row = pr - mat * kR;
                     const uint8_t *rp = mat ? smem + S.up + row * rbu : smem + S.gate + row * rbg;
-                    const float v = lpb_row_q4k_mem<NB>(rp, q8x[t8 < NB ? t8 : 0], t8);
+                    float v;
+                    if constexpr (TGU == kTypeQ3K)
+                        v = lpb_row_q3k_mem<NB, true>(rp, q8x[t8 < NB ? t8 : 0], t8);
+                    else
+                        v = lpb_row_q4k_mem<NB>(rp, q8x[t8 < NB ? t8 : 0], t8);
                     if (t8 == NB - 1) gu[pr] = v;
                 }
             };
@@ -452,12 +457,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 break;
             }
             stamp(l, 8);
-            if constexpr (TD == kTypeQ6K) {
+            if constexpr (TD == kTypeQ6K || TD == kTypeQ5K) {
                 // 8 lanes per row; a wave takes rows of one parity so that its rows
                 // share their 4-byte alignment when the row size is 2 mod 4
                 const int row = 16 * (wave >> 1) + 2 * (grp & 7) + (wave & 1);
                 if (row < RD) {
-                    const float y = g8_row_q6k_u<NBH>(smem + S.down + row * rbd, q8h, t8);
+                    float y;
+                    if constexpr (TD == kTypeQ6K)
+                        y = g8_row_q6k_u<NBH>(smem + S.down + row * rbd, q8h, t8);
+                    else
+                        y = g8_row_q5k(smem + S.down + row * rbd, q8h, NBH, t8);
                     if (t8 == 0) ys[row] = y;
                 }
             } else {
@@ -535,7 +544,8 @@ size_t persistent_lds_bytes(const PersistentArgs &a) {
     X(kTypeQ4K, 2048, kTypeQ6K, 768)    \
     X(kTypeQ4K, 2048, kTypeQ4K, 1024)   \
     X(kTypeQ4K, 2048, kTypeQ6K, 512)    \
-    X(kTypeQ4K, 2048, kTypeQ6K, 1024)
+    X(kTypeQ4K, 2048, kTypeQ6K, 1024)   \
+    X(kTypeQ3K, 2048, kTypeQ5K, 1024)
 
 using KernelFn = void (*)(PersistentArgs);
 

@@ -480,18 +480,20 @@ __device__ __forceinline__ float lpb_row_q5k_mem(const uint8_t *row, const Q8L &
 // Q3_K super-block (2-byte aligned: hmask[32], qs[64], 12 scale bytes, d)
 // against an activation block in memory: isum = sum_g (sc_g - 32) *
 // sum_{16} q3*q8, with q3 = q2 + 4*h - 4 and sum q3*q8 = sum (q2 + 4h)*q8 - 4*bsum.
+// kRolled: the halves one after the other (fewer live registers, for kernels
+// that keep it beside wait loops); otherwise both unrolled.
+template <bool kRolled>
 __device__ __forceinline__ int q3k_block_isum_mem(const uint8_t *blk, const Q8L &x) {
     const uint32_t s0 = lds_u32(blk + 96), s1 = lds_u32(blk + 100), s2 = lds_u32(blk + 104);
-    uint32_t hm[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) hm[t] = lds_u32(blk + 4 * t);
     const uint4 *xq = reinterpret_cast<const uint4 *>(x.qs);
     int isum = 0;
+    auto half = [&](int n) {  // elements 128n .. 128n + 127
+        uint32_t qw[8], hm[8];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        uint32_t qw[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) qw[t] = lds_u32(blk + 32 + 32 * n + 4 * t);
+        for (int t = 0; t < 8; ++t) {
+            qw[t] = lds_u32(blk + 32 + 32 * n + 4 * t);
+            hm[t] = lds_u32(blk + 4 * t);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // elements 128n + 32j + l: quant words 32n + 8j + t
             const uint4 x0 = xq[8 * n + 2 * j], x1 = xq[8 * n + 2 * j + 1];
@@ -508,18 +510,25 @@ __device__ __forceinline__ int q3k_block_isum_mem(const uint8_t *blk, const Q8L 
                 isum += q3k_scale(g, s0, s1, s2) * (sd - 4 * (int)x.bsums[g]);
             }
         }
+    };
+    if constexpr (kRolled) {
+#pragma unroll 1
+        for (int n = 0; n < 2; ++n) half(n);
+    } else {
+        half(0);
+        half(1);
     }
     return isum;
 }
 
 // One Q3_K row of NB super-blocks, one lane per block with the lane's
 // activation block xb read from memory; valid in lane NB-1.
-template <int NB>
+template <int NB, bool kRolled = false>
 __device__ __forceinline__ float lpb_row_q3k_mem(const uint8_t *row, const Q8L &xb, int t) {
     float p = 0.0f;
     if (t < NB) {
         const uint8_t *blk = row + t * kQ3KBytes;
-        const int isum = q3k_block_isum_mem(blk, xb);
+        const int isum = q3k_block_isum_mem<kRolled>(blk, xb);
         const uint32_t dbits = (uint32_t)blk[108] | ((uint32_t)blk[109] << 8);
         p = (half_bits_to_float(dbits) * xb.d) * (float)isum;
     }

@@ -178,7 +178,7 @@ def test_decode_chain_per_layer(orc):
         st.close()
 
 
-@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE], ids=lambda s: s.name)
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE, W.OLMOE_Q3], ids=lambda s: s.name)
 def test_persistent_decode_matches_oracle_and_launch_path(orc, shape):
     """One-launch stacked decode (router, experts per XCD, combine, rms_norm) against the
     oracle layer by layer, and against the per-layer launch path on the same input."""
