@@ -15,11 +15,12 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module")
-def model(tmp_path_factory):
-    shape, nl = W.QWEN3_30B, 2
+@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.QWEN35], ids=lambda s: s.name)
+def model(tmp_path_factory, request):
+    """Two layers in a GGUF; Qwen3.5's add a shared expert and Q5_K down rows."""
+    shape, nl = request.param, 2
     layers = {l: W.make_layer(shape, 6, l) for l in range(nl)}
-    path = tmp_path_factory.mktemp("store") / "qwen3_30b_2l.gguf"
+    path = tmp_path_factory.mktemp("store") / f"{shape.name}_2l.gguf"
     write_layers(path, shape, layers, "qwen3moe")
     return shape, nl, path
 
