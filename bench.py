@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--batch", type=int, default=0, metavar="M",
                     help="batched workload: M tokens per step (4, 8 or 16), routed independently, "
                          "grouped by expert on int8 MFMA")
+    ap.add_argument("--batch-same", action="store_true",
+                    help="with --batch: the M tokens of a step share one hidden, so every expert group holds "
+                         "M tokens and runs on MFMA (the skewed end of the verify workload)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -283,6 +286,7 @@ def run_pool(args, shape, n_layer):
 
 
 MFMA_MIN_TOKENS = 12  # smallest expert group the batched kernels run on MFMA (kMfmaMinTokens)
+MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA ops/s
 
 
 def run_batched(args, shape, n_layer):
@@ -310,7 +314,8 @@ def run_batched(args, shape, n_layer):
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     n_groups = 8
-    toks = [[W.make_hidden(shape, args.seed, 0, g * M + t) for t in range(M)] for g in range(n_groups)]
+    toks = [[W.make_hidden(shape, args.seed, 0, g * M + (0 if args.batch_same else t)) for t in range(M)]
+            for g in range(n_groups)]
     fx_d = torch.stack([torch.stack([torch.from_numpy(f) for f, _ in grp]) for grp in toks]).to(dev)
     x_d = torch.stack([torch.stack([torch.from_numpy(r) for _, r in grp]) for grp in toks]).to(dev)
     sel_d = torch.empty((n_layer, M, shape.n_used), dtype=torch.int32, device=dev)
@@ -348,6 +353,9 @@ def run_batched(args, shape, n_layer):
     bat_us = kt.total_ms[kb] / max(1, kt.launches[kb]) * 1000.0
     bat_bytes = float(uniq.mean()) * eb + M * 4 * shape.n_embd * 2
     gbps = bat_bytes / bat_us / 1e3
+    macs_per_pair = 3 * shape.n_ff * shape.n_embd
+    int8_ops = 2 * macs_per_pair * int(hist.sum())
+    mfma_ops = 2 * macs_per_pair * int(hist[hist >= MFMA_MIN_TOKENS].sum())
     result = {
         "metric": f"batched MoE-layer us per step of {M} tokens + HBM GB/s, Qwen3-30B-A3B-shape Q4_K",
         "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -369,7 +377,16 @@ def run_batched(args, shape, n_layer):
         # the per-token int8 dot (MFMA_MIN_TOKENS in the batched kernels)
         "expert_groups": {"per_token_dot": int(((hist > 0) & (hist < MFMA_MIN_TOKENS)).sum()),
                           "mfma": int((hist >= MFMA_MIN_TOKENS).sum())},
+        # int8 operations of the expert products (2 per multiply-add: gate, up and
+        # down of every (token, expert) pair), the MFMA share of them, and that
+        # share's rate against MI355X's dense int8 peak of 5.0 POP/s
+        "mfma": {"int8_ops_per_step": int(int8_ops), "mfma_ops_per_step": int(mfma_ops),
+                 "mfma_tops": round(mfma_ops / (ms * 1e-3) / 1e12, 2),
+                 "utilization": round(mfma_ops / (ms * 1e-3) / MFMA_INT8_PEAK, 5), "peak_tops": MFMA_INT8_PEAK / 1e12},
     }
+    if args.batch_same:
+        result["data"] = "synthetic weights; the M tokens of a step share one N(0,1) hidden (every group M tokens)"
+        result["config"]["workload"] += ", tokens sharing one hidden"
     print(json.dumps(result), flush=True)
 
 
