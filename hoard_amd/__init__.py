@@ -111,6 +111,8 @@ ABI = {
     "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
     "hoard_moe_pool_ensure": (_I, [_P, _I, _P, _P, _P, _P, _P]),
     "hoard_moe_forward_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "hoard_moe_ffn_combine_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "hoard_moe_pool_ensure_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "hoard_moe_get_stats": (_I, [_P, ctypes.POINTER(MoeStats)]),
     "hoard_moe_reset_stats": (_I, [_P]),
     "hoard_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),

@@ -234,14 +234,22 @@ constexpr int kRouteN = 2048;  // n_embd of the batched path
 // this).  A token selects an expert at most once, so a per-expert bitmask of
 // tokens orders each group by token; groups are numbered in ascending expert
 // id.
-__device__ void group_by_expert(const BatchedArgs &a) {
+// With caller ids (ysrc, bad: the grouping workgroup's LDS copies) a pair that
+// repeats an earlier id of its token, or whose token has an id out of range,
+// joins no group.
+__device__ __forceinline__ bool pair_computed(const BatchedArgs &a, const int *ysrc, const int *bad, int p) {
+    return !ysrc || (ysrc[p] == p % a.k && !bad[p / a.k]);
+}
+
+__device__ void group_by_expert(const BatchedArgs &a, const int *ysrc = nullptr, const int *bad = nullptr) {
     __shared__ unsigned mask[kMaxExperts];
     __shared__ int uidx[kMaxExperts];
     __shared__ int wave_total;
-    const int tid = threadIdx.x, nt = blockDim.x, E = a.E, P = a.M * a.k;
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k;
     for (int e = tid; e < E; e += nt) mask[e] = 0u;
     __syncthreads();
     for (int p = tid; p < P; p += nt) {
+        if (!pair_computed(a, ysrc, bad, p)) continue;
         int e = __hip_atomic_load(a.sel + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (e < 0 || e >= E) e = 0;  // out-of-range selections count as expert 0
         atomicOr(&mask[e], 1u << (p / a.k));
@@ -273,6 +281,7 @@ __device__ void group_by_expert(const BatchedArgs &a) {
     }
     __syncthreads();
     for (int p = tid; p < P; p += nt) {
+        if (!pair_computed(a, ysrc, bad, p)) continue;
         const int t = p / a.k, j = p % a.k;
         int e = __hip_atomic_load(a.sel + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (e < 0 || e >= E) e = 0;
@@ -351,6 +360,41 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     group_by_expert(a);
     if (threadIdx.x == 0)
         __hip_atomic_store(&a.counters[kBatchedCounters - 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// -- caller ids: Q8_K of fx (workgroups 0..M-1, a wave per block) and the
+// grouping (workgroup M): each pair's first occurrence of its id within the
+// token, tokens with an id out of range, then the groups as for routed ids.
+// The counterpart of the verify step's mul_mat_id over the slot pool with the
+// host's ids (src/run_specloop.cpp:116-139), where a token's padding repeats an
+// id with weight 0.
+__global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
+    constexpr int nb = kRouteN / QK;
+    const int wave = threadIdx.x >> 6;
+    if ((int)blockIdx.x < a.M) {
+        const int t = blockIdx.x;
+        for (int b = wave; b < nb; b += 8)
+            wave_quantize_q8l(a.fx + (size_t)t * kRouteN + b * QK, q8(a.q8x) + (size_t)t * nb + b);
+        return;
+    }
+    __shared__ int bad_s[kMaxTok];
+    __shared__ int ysrc_s[kMaxTok * kMaxK];
+    const int tid = threadIdx.x, P = a.M * a.k;
+    if (tid < kMaxTok) bad_s[tid] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += blockDim.x) {
+        const int t = p / a.k, j = p % a.k;
+        const int e = a.sel[p];
+        if (e < 0 || e >= a.n_ids) bad_s[t] = 1;
+        int first = j;
+        for (int i = j - 1; i >= 0; --i)
+            if (a.sel[t * a.k + i] == e) first = i;
+        ysrc_s[p] = first;
+        a.ysrc[p] = first;  // for the combine launch
+    }
+    __syncthreads();
+    if (tid < a.M) a.bad[tid] = bad_s[tid];
+    group_by_expert(a, ysrc_s, bad_s);
 }
 
 // Expert groups are computed two ways.  A group of fewer than kMfmaMinTokens
@@ -529,9 +573,15 @@ __global__ __launch_bounds__(256) void combine_kernel(BatchedArgs a) {
     const int t = blockIdx.y;
     const int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= a.n_embd) return;
+    if (a.bad && a.bad[t]) {  // an id outside the pool or expert set: the token's row is poisoned
+        a.out[(size_t)t * a.n_embd + d] = __builtin_nanf("");
+        return;
+    }
     float acc = 0.0f;
-    for (int j = 0; j < a.k; ++j)
-        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * a.k + j) * a.n_embd + d];
+    for (int j = 0; j < a.k; ++j) {
+        const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
+        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * a.k + js) * a.n_embd + d];
+    }
     a.out[(size_t)t * a.n_embd + d] = acc + a.res[(size_t)t * a.n_embd + d];
 }
 
@@ -542,14 +592,12 @@ bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff) {
            (d_type == kTypeQ4K || d_type == kTypeQ6K);
 }
 
-hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
-    if (a.M < 1 || a.M > kMaxTok || a.n_embd != 2048 || a.gu_type != kTypeQ4K) return hipErrorInvalidValue;
-    const int nb = a.n_embd / QK, nbh = a.n_ff / QK;
-    const int umax = a.E < a.M * a.k ? a.E : a.M * a.k;
-    if ((a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1 || a.E > kMaxExperts || a.k > kMaxK)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(route_kernel, dim3((a.E + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
-                       dim3(256), 0, s, a);
+namespace {
+
+// The launches after the grouping: gate/up, Q8_K(h), down, combine.
+hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
+    const int nbh = a.n_ff / QK;
+    const int umax = a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k;
     hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, kMaxTok, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
@@ -562,6 +610,27 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
 #undef HOARD_DOWN
     hipLaunchKernelGGL(combine_kernel, dim3((a.n_embd + 255) / 256, a.M), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+bool args_ok(const BatchedArgs &a) {
+    return a.M >= 1 && a.M <= kMaxTok && a.n_embd == kRouteN && a.gu_type == kTypeQ4K && a.k <= kMaxK &&
+           a.n_ids >= 1 && a.n_ids <= kMaxExperts && a.E <= kMaxExperts;
+}
+
+}  // namespace
+
+hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
+    if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(route_kernel, dim3((a.E + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
+                       dim3(256), 0, s, a);
+    return launch_groups(a, s);
+}
+
+hipError_t launch_batched_ids(const BatchedArgs &a, hipStream_t s) {
+    if (!args_ok(a) || !a.ysrc || !a.bad) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prep_ids_kernel, dim3((unsigned)a.M + 1), dim3(512), 0, s, a);
+    return launch_groups(a, s);
 }
 
 }  // namespace hoard

@@ -87,12 +87,18 @@ struct BatchedArgs {
     int *slot_of;           // [E] scratch
     int *uexp, *ucount;     // [umax] expert of each group, tokens in it
     int *utok, *uslot;      // [umax][16] token and slot of each member
-    unsigned *hist;         // [E] tokens per expert in the call
+    unsigned *hist;         // [n_ids] tokens per expert (or slot) in the call
+    int n_ids;              // id space the groups are formed over: E, or the slots of a pool
+    int *ysrc;              // [M][k] caller ids only: the slot j' <= j whose output pair (t, j) takes
+                            // (its first occurrence of the same id), else null
+    int *bad;               // [M] caller ids only: 1 for a token with an id outside [0, n_ids), else null
 };
 constexpr int kBatchedMaxTokens = 16;
 constexpr int kBatchedCounters = 8;
 constexpr size_t kQ8LBytes = 304;
 hipError_t launch_batched(const BatchedArgs &a, hipStream_t s);
+// The same expert products and combine for the caller's ids (a.sel) and weights (a.wsel).
+hipError_t launch_batched_ids(const BatchedArgs &a, hipStream_t s);
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
 
 // Persistent stacked decode (one cooperative launch per token).

@@ -343,16 +343,20 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
 // missed experts on copy_stream (after the previous FFN that read this layer's
 // slots), and `stream` made to wait for them.  slot_dev (optional) receives
 // the slot ids through a pinned staging copy on `stream`.
-int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host, int32_t *slot_dev,
-                hipStream_t s, hipStream_t cs) {
+constexpr int kMaxPoolIds = 16 * 16;  // ids one pool step takes: up to 16 tokens x 16 experts
+
+int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequential, int32_t *slot_host,
+                int32_t *slot_dev, hipStream_t s, hipStream_t cs) {
     const hoard_moe_cfg &c = h->cfg;
     Layer &L = h->layers[layer];
-    const int n = c.n_used;
     for (int j = 0; j < n; ++j)
         if (sel[j] < 0 || sel[j] >= c.n_expert) return fail(HOARD_ERR_INVALID, "expert id %d out of range", sel[j]);
-    int32_t slots[16];
-    uint8_t miss[16];
-    h->lru.access(layer, sel, n, h->pool_naive, slots, miss);
+    int32_t slots[kMaxPoolIds];
+    uint8_t miss[kMaxPoolIds];
+    if (sequential)
+        h->lru.access_sequential(layer, sel, n, slots, miss);
+    else
+        h->lru.access(layer, sel, n, h->pool_naive, slots, miss);
     int n_miss = 0;
     for (int j = 0; j < n; ++j) n_miss += miss[j];
     // misses are dealt round-robin to the caller's copy stream and the internal
@@ -368,16 +372,16 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int32_t *slot_host,
         // storage tier: the RAM tier serves or reads the missed experts (reads in
         // parallel, on the host), then each is uploaded from its RAM entry,
         // which is fenced until the upload is done
-        int32_t mids[16];
-        int mj[16], nm = 0;
+        int32_t mids[kMaxPoolIds];
+        int mj[kMaxPoolIds], nm = 0;
         for (int j = 0; j < n; ++j)
             if (miss[j]) {
                 mj[nm] = j;
                 mids[nm++] = sel[j];
             }
-        hoard::StoreEntry ent[16];
+        std::vector<hoard::StoreEntry> ent((size_t)n);
         if (nm) {
-            if (int rc = h->store->fetch(layer, nm, mids, ent, nullptr)) {
+            if (int rc = h->store->fetch(layer, nm, mids, ent.data(), nullptr)) {
                 h->lru.reset_layer(layer);  // the missed slots were not filled: forget the layer's residency
                 return rc;                  // the store has set the error text
             }
@@ -442,7 +446,7 @@ int pool_mark_use(hoard_moe *h, int layer, hipStream_t s) {
 int pool_after_route(hoard_moe *h, int layer, const int32_t *sel_dev, int32_t *slot_dev, hipStream_t s) {
     HIP_TRY(hipMemcpyAsync(h->pin_sel, sel_dev, sizeof(int32_t) * h->cfg.n_used, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
-    return pool_ensure(h, layer, h->pin_sel, nullptr, slot_dev, s, s);
+    return pool_ensure(h, layer, h->pin_sel, h->cfg.n_used, false, nullptr, slot_dev, s, s);
 }
 
 // The one-launch decodes need 8 XCDs x 32 CUs (one workgroup per CU).  The
@@ -838,7 +842,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
                 std::memcpy(r + L.gbytes + L.ubytes, d + e * L.dbytes, L.dbytes);
             }
         }
-        if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
+        if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * kMaxPoolIds, hipHostMallocDefault) != hipSuccess)
             rc = fail(HOARD_ERR_OOM, "pinned slot staging");
         for (int i = 0; !rc && i < kUpStreams; ++i)
             if (hipEventCreateWithFlags(&L.copied[i], hipEventDisableTiming) != hipSuccess) rc = fail(HOARD_ERR_HIP, "pool events");
@@ -946,7 +950,7 @@ int hoard_moe_pool_ensure(hoard_moe *h, int layer, const int32_t *sel_host, int3
     if (rc) return rc;
     if (h->cfg.pool_k == 0) return fail(HOARD_ERR_STATE, "handle has no slot pool (pool_k == 0)");
     if (!sel_host || (!slot_host && !slot_dev)) return fail(HOARD_ERR_INVALID, "null argument");
-    return pool_ensure(h, layer, sel_host, slot_host, slot_dev, (hipStream_t)stream,
+    return pool_ensure(h, layer, sel_host, h->cfg.n_used, false, slot_host, slot_dev, (hipStream_t)stream,
                        copy_stream ? (hipStream_t)copy_stream : (hipStream_t)stream);
 }
 
@@ -965,8 +969,15 @@ int hoard_moe_attach_store(hoard_moe *h, hoard_store *st) {
     return HOARD_OK;
 }
 
-int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
-                              float *out_dev, int32_t *sel_dev, float *w_dev, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks and buffers common to the batched entry points, and their arguments
+// but the selection: the shapes and types the kernels are built for, 16-byte
+// aligned fx and weights, and the scratch allocated on first use.
+int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev, float *out_dev,
+                  bool pooled_ok, hoard::BatchedArgs *out) {
     int rc = check_layer(h, layer);
     if (rc) return rc;
     const hoard_moe_cfg &c = h->cfg;
@@ -974,7 +985,8 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     if (M < 1 || M > c.max_tokens || M > hoard::kBatchedMaxTokens)
         return fail(HOARD_ERR_INVALID, "M %d outside 1..min(max_tokens %d, %d)", M, c.max_tokens,
                     hoard::kBatchedMaxTokens);
-    if (c.pool_k > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path needs every expert resident (pool_k 0)");
+    if (c.pool_k > 0 && !pooled_ok)
+        return fail(HOARD_ERR_UNSUPPORTED, "batched routing needs every expert resident (pool_k 0)");
     if (c.n_ff_shexp > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path has no shared expert");
     const Layer &L = h->layers[layer];
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
@@ -986,7 +998,7 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
          (uintptr_t)L.dstride) & 15)
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: expert matrices must be 16-byte aligned");
     const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
-    const int umax = std::min(c.n_expert, T * c.n_used);
+    const int umax = std::min(c.n_expert, T * c.n_used);  // pool_k <= n_expert: slots never exceed it
     const int nb = c.n_embd / 256, nbh = c.n_ff / 256;
     if (!h->b_q8x) {
         rc = rc ? rc : dev_alloc((void **)&h->b_q8x, (size_t)T * nb * hoard::kQ8LBytes);
@@ -994,21 +1006,20 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
         rc = rc ? rc : dev_alloc((void **)&h->b_h, (size_t)umax * hoard::kBatchedMaxTokens * c.n_ff * sizeof(float));
         rc = rc ? rc : dev_alloc((void **)&h->b_y, (size_t)T * c.n_used * c.n_embd * sizeof(float));
         rc = rc ? rc : dev_alloc((void **)&h->b_ints,
-                                 sizeof(int) * (1 + c.n_expert + 2 * umax + 2 * umax * hoard::kBatchedMaxTokens));
+                                 sizeof(int) * (1 + c.n_expert + 2 * umax + 2 * umax * hoard::kBatchedMaxTokens +
+                                                T * c.n_used + T));
         rc = rc ? rc : dev_alloc((void **)&h->b_hist, sizeof(unsigned) * c.n_expert);
         rc = rc ? rc : dev_alloc((void **)&h->b_counters, sizeof(unsigned) * hoard::kBatchedCounters);
         if (rc) return rc;
         HIP_TRY(hipMemset(h->b_counters, 0, sizeof(unsigned) * hoard::kBatchedCounters));
     }
-    hipStream_t s = (hipStream_t)stream;
-    int32_t *sel = sel_dev ? sel_dev : h->sel;
-    float *w = w_dev ? w_dev : h->wsel;
     hoard::BatchedArgs a{};
     a.M = M;
     a.n_embd = c.n_embd;
     a.n_ff = c.n_ff;
     a.E = c.n_expert;
     a.k = c.n_used;
+    a.n_ids = c.pool_k > 0 ? c.pool_k : c.n_expert;
     a.gu_type = L.gate_type;
     a.d_type = L.down_type;
     a.fx = fx_dev;
@@ -1018,8 +1029,6 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     a.renorm = c.renorm;
     a.logits = h->logits;
     a.counters = h->b_counters;
-    a.sel = sel;
-    a.wsel = w;
     a.gate = L.gate;
     a.up = L.up;
     a.down = L.down;
@@ -1038,6 +1047,21 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     a.utok = a.ucount + umax;
     a.uslot = a.utok + umax * hoard::kBatchedMaxTokens;
     a.hist = h->b_hist;
+    *out = a;
+    return HOARD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
+                              float *out_dev, int32_t *sel_dev, float *w_dev, void *stream) {
+    hoard::BatchedArgs a;
+    if (int rc = batched_setup(h, layer, M, fx_dev, res_dev, out_dev, false, &a)) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    a.sel = sel_dev ? sel_dev : h->sel;
+    a.wsel = w_dev ? w_dev : h->wsel;
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_BATCHED, s);
@@ -1047,6 +1071,48 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     h->stats.tokens += (uint64_t)M;
     h->hist_pending = true;
     return HOARD_OK;
+}
+
+int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const int32_t *ids_dev,
+                                  const float *w_dev, const float *res_dev, float *out_dev, void *stream) {
+    if (!ids_dev || !w_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
+    hoard::BatchedArgs a;
+    if (int rc = batched_setup(h, layer, M, fx_dev, res_dev, out_dev, true, &a)) return rc;
+    const hoard_moe_cfg &c = h->cfg;
+    const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
+    hipStream_t s = (hipStream_t)stream;
+    a.sel = const_cast<int32_t *>(ids_dev);
+    a.wsel = const_cast<float *>(w_dev);
+    a.ysrc = a.uslot + std::min(c.n_expert, T * c.n_used) * hoard::kBatchedMaxTokens;
+    a.bad = a.ysrc + T * c.n_used;
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_BATCHED, s);
+        e = hoard::launch_batched_ids(a, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "batched launch: %s", hipGetErrorString(e));
+    h->stats.tokens += (uint64_t)M;
+    return pool_mark_use(h, layer, s);
+}
+
+int hoard_moe_pool_ensure_batched(hoard_moe *h, int layer, int n, const int32_t *sel_host, int32_t *slot_host,
+                                  int32_t *slot_dev, void *stream, void *copy_stream) {
+    int rc = check_layer(h, layer);
+    if (rc) return rc;
+    const hoard_moe_cfg &c = h->cfg;
+    if (c.pool_k == 0) return fail(HOARD_ERR_STATE, "handle has no slot pool (pool_k == 0)");
+    if (h->pool_naive) return fail(HOARD_ERR_STATE, "naive pool mode places one token's experts; not a batch");
+    if (!sel_host || (!slot_host && !slot_dev)) return fail(HOARD_ERR_INVALID, "null argument");
+    if (n < 1 || n > kMaxPoolIds || n > c.max_tokens * c.n_used)
+        return fail(HOARD_ERR_INVALID, "%d ids outside 1..max_tokens * n_used (%d)", n, c.max_tokens * c.n_used);
+    // every distinct expert of the batch must hold a slot at once
+    std::vector<int32_t> u(sel_host, sel_host + n);
+    std::sort(u.begin(), u.end());
+    const int distinct = (int)(std::unique(u.begin(), u.end()) - u.begin());
+    if (distinct > c.pool_k)
+        return fail(HOARD_ERR_INVALID, "%d distinct experts for %d slots", distinct, c.pool_k);
+    return pool_ensure(h, layer, sel_host, n, true, slot_host, slot_dev, (hipStream_t)stream,
+                       copy_stream ? (hipStream_t)copy_stream : (hipStream_t)stream);
 }
 
 int hoard_moe_get_stats(hoard_moe *h, hoard_moe_stats *out) {

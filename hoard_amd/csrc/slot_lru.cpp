@@ -9,7 +9,7 @@
 
 struct hoard_slot_lru {
     hoard::SlotLru lru;
-    bool naive = false;
+    int mode = 0;  // 0 hits first, 1 naive, 2 one id after the other (the verify loop's ensure)
 };
 
 extern "C" {
@@ -17,22 +17,25 @@ extern "C" {
 int hoard_slot_lru_create(int n_layer, int n_expert, int k, int naive, hoard_slot_lru **out) {
     if (!out) return HOARD_ERR_INVALID;
     *out = nullptr;
-    if (n_layer <= 0 || n_expert <= 0 || k <= 0 || k > n_expert) return HOARD_ERR_INVALID;
+    if (n_layer <= 0 || n_expert <= 0 || k <= 0 || k > n_expert || naive < 0 || naive > 2) return HOARD_ERR_INVALID;
     hoard_slot_lru *p = new (std::nothrow) hoard_slot_lru();
     if (!p) return HOARD_ERR_OOM;
     p->lru.reset(n_layer, n_expert, k);
-    p->naive = naive != 0;
+    p->mode = naive;
     *out = p;
     return HOARD_OK;
 }
 
 int hoard_slot_lru_access(hoard_slot_lru *p, int layer, const int32_t *sel, int n, int32_t *slot_out,
                           uint8_t *miss_out) {
-    if (!p || !sel || !slot_out || n <= 0 || n > p->lru.k()) return HOARD_ERR_INVALID;
+    if (!p || !sel || !slot_out || n <= 0 || (p->mode != 2 && n > p->lru.k())) return HOARD_ERR_INVALID;
     for (int j = 0; j < n; ++j)
         if (sel[j] < 0 || sel[j] >= p->lru.n_expert()) return HOARD_ERR_INVALID;
     if (layer < 0 || layer >= p->lru.n_layer()) return HOARD_ERR_INVALID;
-    p->lru.access(layer, sel, n, p->naive, slot_out, miss_out);
+    if (p->mode == 2)
+        p->lru.access_sequential(layer, sel, n, slot_out, miss_out);
+    else
+        p->lru.access(layer, sel, n, p->mode == 1, slot_out, miss_out);
     return HOARD_OK;
 }
 

@@ -77,6 +77,31 @@ class SlotLru {
         }
     }
 
+    // The verify loop's ensure (src/run_specloop.cpp:59-67), one id after the
+    // other with no hits-first pass: a hit moves to the front, a miss takes the
+    // back slot.  A repeated id is a hit on its earlier slot.
+    void access_sequential(int layer, const int32_t *sel, int n, int32_t *slot_out, uint8_t *miss_out) {
+        std::vector<int> &se = slot_expert_[layer];
+        std::vector<int> &es = expert_slot_[layer];
+        std::list<int> &lru = lru_[layer];
+        for (int j = 0; j < n; ++j) {
+            int s = es[sel[j]];
+            const bool hit = s >= 0;
+            if (hit) {
+                lru.remove(s);
+            } else {
+                s = lru.back();
+                lru.pop_back();
+                if (se[s] >= 0) es[se[s]] = -1;
+                se[s] = sel[j];
+                es[sel[j]] = s;
+            }
+            lru.push_front(s);
+            slot_out[j] = s;
+            if (miss_out) miss_out[j] = hit ? 0 : 1;
+        }
+    }
+
     int slot_of(int layer, int expert) const { return expert_slot_[layer][expert]; }
     int expert_in(int layer, int slot) const { return slot_expert_[layer][slot]; }
 

@@ -136,6 +136,25 @@ class MoEStage:
         torch.cuda.synchronize()
         return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
 
+    def ffn_combine_batched(self, layer: int, fx, ids, w, res):
+        """Caller's selection for M tokens: fx, res [M][n_embd]; ids, w [M][n_used]."""
+        torch = _torch()
+        fx_d, res_d = self.dev(fx), self.dev(res)
+        ids_d, w_d = self.dev(ids, torch.int32), self.dev(w)
+        out = torch.empty_like(res_d)
+        check(self.lib.hoard_moe_ffn_combine_batched(self.h, layer, fx_d.shape[0], self.ptr(fx_d), self.ptr(ids_d),
+                                                     self.ptr(w_d), self.ptr(res_d), self.ptr(out), self.stream()))
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def pool_ensure_batched(self, layer: int, sel):
+        """Slots for the ids sel (token-major), taken one after the other."""
+        sel_h = np.ascontiguousarray(np.ravel(sel), dtype=np.int32)
+        slots_h = np.zeros(sel_h.size, dtype=np.int32)
+        check(self.lib.hoard_moe_pool_ensure_batched(self.h, layer, sel_h.size, sel_h.ctypes.data,
+                                                     slots_h.ctypes.data, None, self.stream(), None))
+        return slots_h.reshape(np.shape(sel))
+
     def pool_ensure(self, layer: int, sel, copy_stream=None):
         """Makes the experts sel resident in this layer's slots; returns the slots
         (host) and a device tensor holding them, ordered on the current stream."""

@@ -145,6 +145,26 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
 int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
                               float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 
+/* The batched expert products and combine for the caller's selection, the
+   counterpart of the verify step's mul_mat_id over the slot pool with the host's
+   ids and weights and the sum over views (src/run_specloop.cpp:116-139):
+   ids_dev[M][n_used] are expert ids, or slot indices from
+   hoard_moe_pool_ensure_batched when pool_k > 0; w_dev[M][n_used] are used as
+   given (no renormalisation).  out[t] = res[t] + sum_j w[t][j] y(ids[t][j]), j
+   ascending.  A token may repeat an id (the verify loop pads with a repeated id
+   of weight 0); a token with an id outside the pool or expert set gets a NaN
+   row.  Each token's result equals hoard_moe_ffn_combine's for that token. */
+int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const int32_t *ids_dev,
+                                  const float *w_dev, const float *res_dev, float *out_dev, void *stream);
+
+/* Slot-pool step for a batch (pool_k > 0): the n ids sel_host[] of up to
+   max_tokens tokens (token-major, n_used per token), taken one after the other
+   as the verify loop's ensure does (src/run_specloop.cpp:59-67; no hits-first
+   pass), uploads as hoard_moe_pool_ensure.  The distinct experts must fit the
+   K slots.  slot_host / slot_dev (either optional) receive n slots. */
+int hoard_moe_pool_ensure_batched(hoard_moe *h, int layer, int n, const int32_t *sel_host, int32_t *slot_host,
+                                  int32_t *slot_dev, void *stream, void *copy_stream);
+
 /* Per-kernel timing, the device counterpart of the reference's phase timers
    (tA/tFetch/tB, src/run_moe_stream.cpp:291,311,377,422,448): while enabled,
    every kernel launch is bracketed by a pair of hipEvents on its stream.
@@ -228,8 +248,10 @@ int hoard_moe_reset_stats(hoard_moe *h);
 
 /* Host replay of the slot pool's LRU bookkeeping, with no device: the same
    placement decisions hoard_moe_pool_ensure makes, for trace studies (the
-   reference's simulators, bench/profiler.py:65-91).  naive != 0 reproduces the
-   reference's "naive" mode (:417): request j goes to slot j, always a miss.
+   reference's simulators, bench/profiler.py:65-91).  naive = 1 reproduces the
+   reference's "naive" mode (:417): request j goes to slot j, always a miss;
+   naive = 2 takes the ids one after the other as hoard_moe_pool_ensure_batched
+   does (src/run_specloop.cpp:59-67), any number of them per call.
    slot_out[n] receives the slots, miss_out[n] (optional) 1 per miss. */
 typedef struct hoard_slot_lru hoard_slot_lru;
 int hoard_slot_lru_create(int n_layer, int n_expert, int k, int naive, hoard_slot_lru **out);

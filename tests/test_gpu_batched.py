@@ -96,3 +96,87 @@ def test_batched_rejects_too_many_tokens(stage):
     fx, res = _tokens(shape, 17, 900)
     with pytest.raises(H.HoardError):
         st.forward_batched(0, fx, res)
+
+
+def _routing(orc, shape, hl, fx):
+    sel, w = zip(*(orc.route(hl.router, f, shape.n_expert, shape.n_used, shape.renorm)[:2] for f in fx))
+    return np.stack(sel).astype(np.int32), np.stack(w).astype(np.float32)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_caller_ids_match_single_token(orc, stage, M):
+    """hoard_moe_ffn_combine_batched over the oracle's routing, and over a verify-loop
+    style selection (raw probabilities, one token padded with a repeated id of weight
+    0), gives each token the single-token ffn_combine's bits."""
+    shape, hl, st = stage
+    fx, res = _tokens(shape, M, 7 * M + 3)
+    ids, w = _routing(orc, shape, hl, fx)
+    if M > 1:
+        ids[1, -2:] = ids[1, 0]  # padding: fewer candidates than n_used
+        w[1, -2:] = 0.0
+        w[2] *= 1.7  # weights as given: no renormalisation
+    print(f"caller ids {shape.name} M={M}", flush=True)
+    out = st.ffn_combine_batched(0, fx, ids, w, res)
+    for t in range(M):
+        one = st.ffn_combine(0, fx[t], ids[t], w[t], res[t])
+        assert np.array_equal(one.view(np.uint32), out[t].view(np.uint32)), f"token {t}"
+    ref = orc.moe_ffn_combine(hl, fx[0], ids[0], w[0], res[0])
+    parity.assert_parity(out[0], ref, "caller ids token 0 vs oracle")
+
+
+def test_caller_ids_bad_id_poisons_its_token(stage):
+    shape, hl, st = stage
+    M = 4
+    fx, res = _tokens(shape, M, 500)
+    ids = np.tile(np.arange(shape.n_used, dtype=np.int32), (M, 1))
+    w = np.full((M, shape.n_used), 0.125, np.float32)
+    ids[2, 3] = shape.n_expert + 5
+    print(f"caller ids bad id {shape.name}", flush=True)
+    out = st.ffn_combine_batched(0, fx, ids, w, res)
+    assert np.all(np.isnan(out[2]))
+    for t in (0, 1, 3):
+        one = st.ffn_combine(0, fx[t], ids[t], w[t], res[t])
+        assert np.array_equal(one.view(np.uint32), out[t].view(np.uint32))
+
+
+def test_verify_step_over_the_slot_pool(orc):
+    """The verify loop's step on a K-slot pool (src/run_specloop.cpp:116-139): ensure
+    every (token, expert) in order, then the batched products over the slots.  Bit-
+    identical to the all-resident handle on expert ids; hits and misses as the host
+    replay of the same order gives; more distinct experts than slots is refused."""
+    import ctypes
+
+    from hoard_amd.runtime import MoEStage
+    shape, K, M = W.QWEN3_30B, 40, 4
+    hl = W.make_layer(shape, 9, 0)
+    ref = MoEStage(shape, n_layer=1, layers={0: hl}, max_tokens=16)
+    st = MoEStage(shape, n_layer=1, layers={0: hl}, pool_k=K, max_tokens=16)
+    lib = H.load_library()
+    rp = ctypes.c_void_p()
+    H.check(lib.hoard_slot_lru_create(1, shape.n_expert, K, 2, ctypes.byref(rp)))
+    try:
+        want_miss = 0
+        for step in range(6):
+            fx, res = _tokens(shape, M, 1000 + 3 * step)  # overlapping token sets give hits
+            ids, w = _routing(orc, shape, hl, fx)
+            print(f"verify step {step}: {len(np.unique(ids))} distinct experts", flush=True)
+            slots = st.pool_ensure_batched(0, ids)
+            rs = np.zeros(ids.size, np.int32)
+            rm = np.zeros(ids.size, np.uint8)
+            flat = np.ascontiguousarray(ids.ravel())
+            H.check(lib.hoard_slot_lru_access(rp, 0, flat.ctypes.data, flat.size, rs.ctypes.data, rm.ctypes.data))
+            assert np.array_equal(slots.ravel(), rs)
+            want_miss += int(rm.sum())
+            got = st.ffn_combine_batched(0, fx, slots, w, res)
+            exp = ref.ffn_combine_batched(0, fx, ids, w, res)
+            assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), step
+        ps = st.stats()
+        assert ps.misses == want_miss and ps.hits + ps.misses == ps.reqs
+        many = np.arange(K + 1, dtype=np.int32)
+        with pytest.raises(H.HoardError) as ei:
+            st.pool_ensure_batched(0, many)
+        assert ei.value.code == H.ERR_INVALID
+    finally:
+        lib.hoard_slot_lru_destroy(rp)
+        st.close()
+        ref.close()

@@ -126,3 +126,53 @@ def test_bad_arguments(hlib):
         assert hlib.hoard_slot_lru_access(p, 1, sel.ctypes.data, 1, slots.ctypes.data, None) != 0
     finally:
         hlib.hoard_slot_lru_destroy(p)
+
+
+def _verify_loop_restatement(n_layer, n_expert, k, trace):
+    """The verify loop's ensure (src/run_specloop.cpp:59-67), id after id: a hit
+    moves its slot to the front; a miss pops the back slot, drops its expert,
+    takes the id and goes to the front."""
+    slot_expert = [[-1] * k for _ in range(n_layer)]
+    expert_slot = [dict() for _ in range(n_layer)]
+    lru = [list(range(k)) for _ in range(n_layer)]
+    out = []
+    for layer, sel in trace:
+        slots, miss = [], []
+        for e in sel:
+            if e in expert_slot[layer]:
+                s = expert_slot[layer][e]
+                lru[layer].remove(s)
+                miss.append(0)
+            else:
+                s = lru[layer].pop()
+                old = slot_expert[layer][s]
+                if old >= 0:
+                    del expert_slot[layer][old]
+                slot_expert[layer][s] = e
+                expert_slot[layer][e] = s
+                miss.append(1)
+            lru[layer].insert(0, s)
+            slots.append(s)
+        out.append((slots, miss))
+    return out
+
+
+def test_sequential_order_matches_verify_loop(hlib):
+    """Batches of several tokens' ids (repeats included) against the restatement;
+    with a batch whose distinct ids exceed K the two orders part ways, which the
+    engine order would hide."""
+    rng = np.random.default_rng(21)
+    n_layer, n_expert, k = 3, 40, 12
+    trace = []
+    for _ in range(300):
+        m = int(rng.integers(1, 5))
+        sel = []
+        for _ in range(m):  # m tokens of 4 distinct experts each, Zipf-ish
+            sel += list(rng.choice(n_expert, 4, replace=False, p=np.arange(n_expert, 0, -1) / np.arange(n_expert, 0, -1).sum()))
+        trace.append((int(rng.integers(0, n_layer)), [int(e) for e in sel]))
+    got = _replay(hlib, n_layer, n_expert, k, 2, trace)
+    want = _verify_loop_restatement(n_layer, n_expert, k, trace)
+    assert got == want
+    # a repeated id in one call is a hit on the slot it just took
+    g = _replay(hlib, 1, 8, 4, 2, [(0, [5, 5, 1, 5])])
+    assert g == [([3, 3, 2, 3], [1, 0, 1, 0])]
