@@ -260,6 +260,15 @@ int Store::fetch(int layer, int n, const int32_t *ids, StoreEntry *out, uint8_t 
     const hoard_store_layer &L = layers[(size_t)layer];
     std::vector<ReadJob> jobs;
     std::vector<int> filled;
+    // On any failure the entries this call reserved hold no data: unmap them and
+    // put them at the back, so no later call takes them for hits.
+    auto drop_filled = [&]() {
+        for (int slot : filled) {
+            if (slot2key_[(size_t)slot] >= 0) key2slot_.erase(slot2key_[(size_t)slot]);
+            slot2key_[(size_t)slot] = -1;
+            lru_.splice(lru_.end(), lru_, pos_[(size_t)slot]);
+        }
+    };
     for (int j = 0; j < n; ++j) {
         const int64_t key = (int64_t)layer * n_expert + ids[j];
         stats.requests += 1;
@@ -276,14 +285,16 @@ int Store::fetch(int layer, int n, const int32_t *ids, StoreEntry *out, uint8_t 
             if (slot2key_[(size_t)slot] >= 0) key2slot_.erase(slot2key_[(size_t)slot]);
             slot2key_[(size_t)slot] = key;
             key2slot_[key] = slot;
+            filled.push_back(slot);
             if (fenced_[(size_t)slot]) {  // a device copy out of this entry may still run
-                if (hipEventSynchronize(fence_[(size_t)slot]) != hipSuccess)
+                if (hipEventSynchronize(fence_[(size_t)slot]) != hipSuccess) {
+                    drop_filled();
                     return fail_fmt(HOARD_ERR_HIP, "waiting on a copy out of the RAM tier");
+                }
                 fenced_[(size_t)slot] = 0;
             }
             if (int rc = ensure_chunk(slot)) {
-                key2slot_.erase(key);
-                slot2key_[(size_t)slot] = -1;
+                drop_filled();
                 return rc;
             }
             uint8_t *base = slot_base(slot);
@@ -299,7 +310,6 @@ int Store::fetch(int layer, int n, const int32_t *ids, StoreEntry *out, uint8_t 
                 stats.bytes_read += rsize;
             }
             stats.file_reads += 1;
-            filled.push_back(slot);
             if (hit) hit[j] = 0;
         }
         uint8_t *base = slot_base(slot);
@@ -317,11 +327,7 @@ int Store::fetch(int layer, int n, const int32_t *ids, StoreEntry *out, uint8_t 
                              std::chrono::steady_clock::now() - t0).count();
         stats.direct = pool_->direct() ? (pool_->bounced() ? 2 : 1) : 0;
         if (rc) {  // drop the entries this batch was filling
-            for (int slot : filled) {
-                key2slot_.erase(slot2key_[(size_t)slot]);
-                slot2key_[(size_t)slot] = -1;
-                lru_.splice(lru_.end(), lru_, pos_[(size_t)slot]);
-            }
+            drop_filled();
             const int en = pool_->last_errno();
             if (en) return fail_fmt(HOARD_ERR_IO, "expert read of layer %d failed: %s", layer, strerror(en));
             return fail_fmt(HOARD_ERR_IO, "expert read of layer %d failed: the file is shorter than its tensor "
