@@ -140,6 +140,28 @@ bool read_scalar(Cursor &c, uint32_t t, Value &v) {
     return c.ok;
 }
 
+// Skips one array value (element type, count, elements); arrays may nest.
+bool skip_array(Cursor &c, int depth) {
+    const uint32_t et = c.get<uint32_t>();
+    const uint64_t n = c.get<uint64_t>();
+    if (!c.ok || depth > 8) return c.ok = false;
+    if (et == kString) {
+        for (uint64_t i = 0; i < n && c.ok; ++i) {
+            const uint64_t len = c.get<uint64_t>();
+            if (c.ok && len <= c.n - c.at) c.at += (size_t)len;
+            else c.ok = false;
+        }
+        return c.ok;
+    }
+    if (et == kArray) {
+        for (uint64_t i = 0; i < n && c.ok; ++i) skip_array(c, depth + 1);
+        return c.ok;
+    }
+    const size_t sb = scalar_bytes(et);
+    if (!sb || n > (c.n - c.at) / sb) return c.ok = false;
+    return c.skip((size_t)(n * sb));
+}
+
 float half_to_float(uint16_t h) {
     const uint32_t sign = (uint32_t)(h >> 15) << 31;
     uint32_t exp = (h >> 10) & 0x1f, man = h & 0x3ff, bits;
@@ -245,20 +267,8 @@ int parse(hoard_gguf *g, const char *path) {
         const uint32_t t = c.get<uint32_t>();
         Value v;
         if (t == kArray) {
-            const uint32_t et = c.get<uint32_t>();
-            const uint64_t n = c.get<uint64_t>();
             v.type = kArray;
-            v.u = n;
-            if (et == kString) {
-                for (uint64_t i = 0; i < n && c.ok; ++i) {
-                    std::string s;
-                    c.str(s);
-                }
-            } else {
-                const size_t sb = scalar_bytes(et);
-                if (!sb || n > (c.n - c.at) / sb) c.ok = false;
-                else c.skip((size_t)(n * sb));
-            }
+            skip_array(c, 0);
         } else {
             read_scalar(c, t, v);
         }

@@ -27,7 +27,7 @@ def _value(t: int, v) -> bytes:
     if t == ARRAY:
         et, items = v
         out = struct.pack("<IQ", et, len(items))
-        return out + b"".join(_str(x) if et == STRING else struct.pack(_SCALAR[et], x) for x in items)
+        return out + b"".join(_value(et, x) for x in items)
     return struct.pack(_SCALAR[t], v)
 
 

@@ -30,6 +30,7 @@ def model(arch="qwen3moe", n_layer=2, shared=False, router_type=GGML_F32, seed=0
           ("general.name", STRING, "synthetic"),
           ("tokenizer.ggml.tokens", ARRAY, (STRING, ["a", "bb", "ccc"])),
           ("tokenizer.ggml.scores", ARRAY, (F32, [0.5, 1.5, 2.5])),
+          ("general.nested", ARRAY, (ARRAY, [(U32, [1, 2]), (STRING, ["x"]), (ARRAY, [(I32, [-1])])])),
           ("general.flag", BOOL, True),
           ("general.small", U8, 7),
           ("general.signed", I32, -3),
