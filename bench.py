@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--decode-kernel", default="auto", choices=["auto", "xcd", "spread", "launches"],
                     help="one-launch decode kernel: expert-per-XCD, rows spread over all CUs, or auto; "
                          "'launches' runs the per-layer kernels (hoard_moe_layer's path) instead")
+    ap.add_argument("--decode-launch", default="cooperative", choices=["cooperative", "plain"],
+                    help="how the one-launch decode is launched (plain: for a device holding no other work)")
     ap.add_argument("--phases", action="store_true", help="trace one-launch decode phases of one token")
     ap.add_argument("--pool", type=int, default=0, metavar="K",
                     help="slot-pool workload: K HBM slots per layer, all experts in pinned host memory, "
@@ -472,6 +474,7 @@ def main():
     else:
         dk_opt = {"auto": H.DECODE_AUTO, "xcd": H.DECODE_XCD, "spread": H.DECODE_SPREAD}[args.decode_kernel]
         H.check(lib.hoard_moe_set_option(h, H.OPT_DECODE_KERNEL, dk_opt))
+    H.check(lib.hoard_moe_set_option(h, H.OPT_DECODE_LAUNCH, 1 if args.decode_launch == "plain" else 0))
     hl = W.make_layer(shape, args.seed, 0)
     for l in range(n_layer):
         if l:
@@ -559,8 +562,8 @@ def main():
     H.check(lib.hoard_moe_get_option(h, H.OPT_DECODE_KERNELS_AVAILABLE, ctypes.byref(avail)))
     spread = dk_opt == H.DECODE_SPREAD or (dk_opt == H.DECODE_AUTO and not avail.value & 1)
     result["config"]["decode_path"] = (
-        ("one cooperative launch per token, " + ("expert rows spread over all CUs" if spread
-                                                 else "one expert per XCD"))
+        (f"one {args.decode_launch} launch per token, " + ("expert rows spread over all CUs" if spread
+                                                           else "one expert per XCD"))
         if "decode_persistent" in kernels else "router, gate/up and down+combine launches per layer")
     if args.phases:
         ph = phase_breakdown(lib, h, lambda: step(warm), H, PHASES_SPREAD if spread else PHASES)

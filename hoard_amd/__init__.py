@@ -70,6 +70,7 @@ OPT_POOL_NAIVE = 3
 OPT_DECODE_KERNEL = 4
 OPT_DECODE_KERNELS_AVAILABLE = 5
 OPT_LAYER_KERNELS = 6
+OPT_DECODE_LAUNCH = 7
 DECODE_AUTO, DECODE_XCD, DECODE_SPREAD = 0, 1, 2
 
 

@@ -561,7 +561,7 @@ bool persistent_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff) {
     return persistent_kernel(gu_type, n_embd, d_type, n_ff) != nullptr;
 }
 
-hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s) {
+hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s, bool cooperative) {
     const KernelFn fn = persistent_kernel(a.gu_type, a.n_embd, a.d_type, a.n_ff);
     if (!fn) return hipErrorInvalidConfiguration;
     const size_t lds = persistent_lds_bytes(a);
@@ -579,6 +579,8 @@ hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s) {
     }
     PersistentArgs args = a;
     void *params[] = {&args};
+    if (!cooperative)
+        return hipLaunchKernel((const void *)fn, dim3(kXcds * kPerXcd), dim3(kThreads), params, (unsigned)lds, s);
     return hipLaunchCooperativeKernel((const void *)fn, dim3(kXcds * kPerXcd), dim3(kThreads), params, (unsigned)lds, s);
 }
 

@@ -609,7 +609,7 @@ bool spread_shape_compiled(const SpreadArgs &a) {
     return spread_fn(a, &lds) != nullptr;
 }
 
-hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s) {
+hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s, bool cooperative) {
     size_t lds = 0;
     const SpreadFn fn = spread_fn(a, &lds);
     if (!fn || lds > kPersistentMaxLds) return hipErrorInvalidConfiguration;
@@ -623,6 +623,7 @@ hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s) {
     }
     SpreadArgs args = a;
     void *params[] = {&args};
+    if (!cooperative) return hipLaunchKernel((const void *)fn, dim3(kGroups), dim3(kThreads), params, (unsigned)lds, s);
     return hipLaunchCooperativeKernel((const void *)fn, dim3(kGroups), dim3(kThreads), params, (unsigned)lds, s);
 }
 

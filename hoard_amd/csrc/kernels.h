@@ -133,7 +133,11 @@ struct PersistentArgs {
 constexpr int kTracePhases = 12;
 constexpr size_t kPersistentMaxLds = 163840 - 1024;
 size_t persistent_lds_bytes(const PersistentArgs &a);
-hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s);
+// cooperative: launched with the runtime's co-residency guarantee (every
+// workgroup resident at once); otherwise as a plain launch, which costs about
+// 18 us less but relies on the device holding no other work (the kernels'
+// waits are bounded, so a workgroup left waiting ends with the error flag).
+hipError_t launch_persistent_decode(const PersistentArgs &a, hipStream_t s, bool cooperative = true);
 bool persistent_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
 
 // One-launch decode with each selected expert's rows spread over all 256
@@ -158,7 +162,7 @@ struct SpreadArgs {
     unsigned long long *trace;  // optional [layer][256 workgroups][kTracePhases] wall-clock stamps
 };
 bool spread_shape_compiled(const SpreadArgs &a);
-hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s);
+hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s, bool cooperative = true);
 
 // Per-layer launches for the instantiated shapes (layer.hip); the *_ok tests
 // say whether they take the arguments, else the kernels above run.

@@ -106,6 +106,7 @@ struct hoard_moe {
     int persistent_mode = 1;           // HOARD_OPT_PERSISTENT_DECODE value
     int decode_kernel = 0;             // HOARD_OPT_DECODE_KERNEL value
     bool layer_kernels = true;         // HOARD_OPT_LAYER_KERNELS: instantiated per-layer kernels
+    bool coop_launch = true;           // HOARD_OPT_DECODE_LAUNCH 0: cooperative one-launch decode
     bool table_dirty = true;
     hoard::DecodeLayer *d_table = nullptr;
     uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
@@ -579,7 +580,7 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_DECODE, s);
-        e = hoard::launch_spread_decode(a, s);
+        e = hoard::launch_spread_decode(a, s, h->coop_launch);
     }
     if (e != hipSuccess) {
         (void)hipGetLastError();
@@ -692,7 +693,7 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_DECODE, s);
-        e = hoard::launch_persistent_decode(a, s);
+        e = hoard::launch_persistent_decode(a, s, h->coop_launch);
     }
     if (e != hipSuccess) {
         (void)hipGetLastError();
@@ -1159,6 +1160,10 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "layer kernels flag %d", value);
         h->layer_kernels = value != 0;
         return HOARD_OK;
+    case HOARD_OPT_DECODE_LAUNCH:
+        if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "decode launch %d", value);
+        h->coop_launch = value == 0;
+        return HOARD_OK;
     case HOARD_OPT_POOL_NAIVE:
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "pool naive flag %d", value);
         if (value && h->cfg.pool_k > 0) {
@@ -1189,6 +1194,9 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
         return HOARD_OK;
     case HOARD_OPT_LAYER_KERNELS:
         *value = h->layer_kernels ? 1 : 0;
+        return HOARD_OK;
+    case HOARD_OPT_DECODE_LAUNCH:
+        *value = h->coop_launch ? 0 : 1;
         return HOARD_OK;
     case HOARD_OPT_DECODE_KERNELS_AVAILABLE:
         *value = (h->xcd_ok ? 1 : 0) | (h->spread_ok ? 2 : 0);

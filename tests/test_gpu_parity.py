@@ -209,6 +209,11 @@ def test_persistent_decode_matches_oracle_and_launch_path(orc, shape):
             launched = st.decode(xs[0], 0, nl, W.RMS_EPS)
             st.set_option(H.OPT_PERSISTENT_DECODE, 2)
             parity.assert_parity(whole, launched, "persistent vs per-layer launches")
+            st.set_option(H.OPT_DECODE_LAUNCH, 1)  # plain launch of the same kernel: the same bits
+            plain = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.sync_check()
+            st.set_option(H.OPT_DECODE_LAUNCH, 0)
+            assert np.array_equal(plain.view(np.uint32), whole.view(np.uint32))
     finally:
         st.close()
 
@@ -249,6 +254,11 @@ def test_spread_decode_matches_oracle_and_launch_path(orc, shape, kernel):
             launched = st.decode(xs[0], 0, nl, W.RMS_EPS)
             st.set_option(H.OPT_PERSISTENT_DECODE, 2)
             parity.assert_parity(whole, launched, "spread vs per-layer launches")
+            st.set_option(H.OPT_DECODE_LAUNCH, 1)
+            plain = st.decode(xs[0], 0, nl, W.RMS_EPS)
+            st.sync_check()
+            st.set_option(H.OPT_DECODE_LAUNCH, 0)
+            assert np.array_equal(plain.view(np.uint32), whole.view(np.uint32))
             if shape is W.QWEN3_30B:
                 st.set_option(H.OPT_DECODE_KERNEL, 1)
                 per_xcd = st.decode(xs[0], 0, nl, W.RMS_EPS)
