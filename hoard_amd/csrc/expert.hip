@@ -75,18 +75,18 @@ __device__ __forceinline__ float row_sum_dyn(int type, const float2 *t, int nb) 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------------------
-// gate/up + SwiGLU.  grid = (rows_max / 16, k + has_shared); block = 256.
+// gate/up + SwiGLU.  grid = (rows_max / R, k + has_shared); block = 256; R
+// rows of gate and of up per workgroup (fewer for wide rows, so they fit LDS).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void gateup_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kThreads) void gateup_kernel(GateUpArgs a, int R) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int j = blockIdx.y;
     const bool shared = j >= a.k;
     const MatDesc G = shared ? a.sh_gate : a.gate;
     const MatDesc U = shared ? a.sh_up : a.up;
     const int rows = G.rows;
-    const int r0 = blockIdx.x * kGateUpRows;
+    const int r0 = blockIdx.x * R;
     if (r0 >= rows) return;
-    const int R = kGateUpRows;
     const int nb = a.n_embd / QK;
     float *hout = a.h + (size_t)j * a.hstride + r0;
 
@@ -261,21 +261,24 @@ static size_t host_row_bytes(int type, int cols) { return (size_t)(cols / QK) * 
 
 hipError_t launch_gateup(const GateUpArgs &a, hipStream_t s) {
     const int nb = a.n_embd / QK;
-    size_t lds = 0;
     int rows_max = a.gate.rows;
-    size_t need = stage_region(kGateUpRows * host_row_bytes(a.gate.type, a.n_embd)) +
-                  stage_region(kGateUpRows * host_row_bytes(a.up.type, a.n_embd));
-    if (a.sh_gate.base) {
-        rows_max = rows_max > a.sh_gate.rows ? rows_max : a.sh_gate.rows;
-        const size_t ns = stage_region(kGateUpRows * host_row_bytes(a.sh_gate.type, a.n_embd)) +
-                          stage_region(kGateUpRows * host_row_bytes(a.sh_up.type, a.n_embd));
-        need = need > ns ? need : ns;
+    if (a.sh_gate.base) rows_max = rows_max > a.sh_gate.rows ? rows_max : a.sh_gate.rows;
+    // the most rows per workgroup (16 down to 1) whose staged tiles fit 64 KiB of LDS
+    for (int R = kGateUpRows; R >= 1; R >>= 1) {
+        size_t need = stage_region(R * host_row_bytes(a.gate.type, a.n_embd)) +
+                      stage_region(R * host_row_bytes(a.up.type, a.n_embd));
+        if (a.sh_gate.base) {
+            const size_t ns = stage_region(R * host_row_bytes(a.sh_gate.type, a.n_embd)) +
+                              stage_region(R * host_row_bytes(a.sh_up.type, a.n_embd));
+            need = need > ns ? need : ns;
+        }
+        const size_t lds = need + nb * sizeof(Q8Block) + 16 + 2 * (size_t)R * nb * sizeof(float2);
+        if (lds > 65536 || rows_max % R) continue;
+        dim3 grid((unsigned)(rows_max / R), (unsigned)(a.k + (a.sh_gate.base ? 1 : 0)));
+        hipLaunchKernelGGL(gateup_kernel, grid, dim3(kThreads), lds, s, a, R);
+        return hipGetLastError();
     }
-    lds = need + nb * sizeof(Q8Block) + 16 + 2 * kGateUpRows * nb * sizeof(float2);
-    if (lds > 65536) return hipErrorInvalidConfiguration;
-    dim3 grid((unsigned)(rows_max / kGateUpRows), (unsigned)(a.k + (a.sh_gate.base ? 1 : 0)));
-    hipLaunchKernelGGL(gateup_kernel, grid, dim3(kThreads), lds, s, a);
-    return hipGetLastError();
+    return hipErrorInvalidConfiguration;
 }
 
 hipError_t launch_down_combine(const DownArgs &a, hipStream_t s) {
