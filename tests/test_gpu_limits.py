@@ -20,6 +20,11 @@ CASES = [
     W.Shape("d1024_e8_k2_norenorm", 7, 1024, 8, 2, 512, 0, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q4_K, 1),
     W.Shape("d4096_e32_k4_shared", 8, 4096, 32, 4, 256, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1,
             n_ff_shexp=512),
+    # an odd expert count (router workgroups partly filled), and 60 experts top-4 with a
+    # shared expert, the routing of Qwen1.5-MoE
+    W.Shape("e61_k7", 9, 2048, 61, 7, 768, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1),
+    W.Shape("e60_k4_shared", 10, 2048, 60, 4, 1536, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1,
+            n_ff_shexp=1024),
 ]
 
 
