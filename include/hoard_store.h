@@ -69,23 +69,28 @@ typedef struct hoard_store_stats {
 } hoard_store_stats;
 
 /* Opens `path` for expert reads and sets up the RAM tier (its memory is
-   allocated as entries are first used).  layers[n_layer] as above. */
+   allocated as entries are first used): DirectIO::init and the RamTier set-up
+   (src/run_qwen35.cpp:113-121, :390-393).  layers[n_layer] as above. */
 int hoard_store_open(const char *path, int n_layer, int n_expert, const hoard_store_layer *layers,
                      const hoard_store_cfg *cfg, hoard_store **out);
 void hoard_store_close(hoard_store *s);
 
 /* Makes experts ids[0..n) of `layer` resident in the RAM tier, reading the
-   missing ones from the file, and returns the address of each one's gate, up
+   missing ones from the file (phases A and B of the fetch,
+   src/run_qwen35.cpp:600-627), and returns the address of each one's gate, up
    and down bytes in parts[3*j + 0..2] (hit[j] = 1 when it was already held,
    optional).  n <= the RAM tier's capacity.  The addresses stay valid until a
    later call evicts the entry. */
 int hoard_store_fetch(hoard_store *s, int layer, int n, const int32_t *ids, const void **parts, uint8_t *hit);
 
+/* The counters since opening or the last reset: the reference's ram_hit,
+   nvme_fall, disk_bytes and disk_ns (src/run_qwen35.cpp:398-399, :606, :624-632). */
 int hoard_store_get_stats(const hoard_store *s, hoard_store_stats *out);
 int hoard_store_reset_stats(hoard_store *s);
 
 /* Serves the slot misses of a pool handle (pool_k > 0) from the store
-   instead of the pinned copy of every expert.  Call before the first
+   instead of the pinned copy of every expert: the reference's three tiers,
+   VRAM slot, RAM tier, file (src/run_qwen35.cpp:596-638).  Call before the first
    hoard_moe_set_layer_weights; afterwards that call takes expert tensors
    from the store (w->gate / up / down may be NULL; their types must give the
    store's strides).  The store must stay open while the handle uses it. */
