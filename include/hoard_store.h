@@ -70,7 +70,7 @@ typedef struct hoard_store_stats {
 
 /* Opens `path` for expert reads and sets up the RAM tier (its memory is
    allocated as entries are first used): DirectIO::init and the RamTier set-up
-   (src/run_qwen35.cpp:113-121, :390-393).  layers[n_layer] as above. */
+   (src/run_qwen35.cpp:105-113, :390-393).  layers[n_layer] as above. */
 int hoard_store_open(const char *path, int n_layer, int n_expert, const hoard_store_layer *layers,
                      const hoard_store_cfg *cfg, hoard_store **out);
 void hoard_store_close(hoard_store *s);
