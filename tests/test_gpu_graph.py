@@ -1,0 +1,120 @@
+"""The per-layer path under HIP graph capture: hoard_moe_layer and the
+per-layer decode (route, gate/up, down launches; no copies, memsets or
+allocations once the handle is set up) captured into one graph, replayed
+several times with the program's own eager work and synchronisations between
+replays, each replay bit-identical to the eager launches, and the eager result
+at the parity bar against the oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import hoard_amd as H
+import parity
+from hoard_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+N_LAYER = 2
+REPLAYS = 4
+
+
+@pytest.fixture(scope="module")
+def stage():
+    from hoard_amd.runtime import MoEStage
+    shape = W.QWEN3_30B
+    layers = {l: W.make_layer(shape, 11, l) for l in range(N_LAYER)}
+    st = MoEStage(shape, n_layer=N_LAYER, layers=layers)
+    st.set_option(H.OPT_PERSISTENT_DECODE, 0)
+    yield shape, layers, st
+    st.close()
+
+
+def _replays_match(g, reset, outputs, eager, what):
+    for r in range(REPLAYS):
+        reset()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outputs, eager):
+            assert torch.equal(o.view(torch.int32), e.view(torch.int32)), (what, r)
+        # eager work of the program's own between replays
+        torch.empty(1 << 16, device="cuda").normal_().sum().item()
+
+
+def test_layer_chain_captured(orc, stage):
+    shape, layers, st = stage
+    D, k = shape.n_embd, shape.n_used
+    fx, res = W.make_hidden(shape, 11, 0, 0)
+    fx_d, res_d = st.dev(fx), st.dev(res)
+    out = [torch.empty(D, device="cuda") for _ in range(N_LAYER)]
+    sel = [torch.empty(k, dtype=torch.int32, device="cuda") for _ in range(N_LAYER)]
+    w = [torch.empty(k, device="cuda") for _ in range(N_LAYER)]
+    s = torch.cuda.Stream()
+
+    def chain():  # layer l takes layer l-1's output as its normed input and residual
+        sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for l in range(N_LAYER):
+            a = fx_d if l == 0 else out[l - 1]
+            r = res_d if l == 0 else out[l - 1]
+            H.check(st.lib.hoard_moe_layer(st.h, l, st.ptr(a), st.ptr(r), st.ptr(out[l]), st.ptr(sel[l]),
+                                           st.ptr(w[l]), sp))
+
+    print("graph: eager layer chain", flush=True)
+    with torch.cuda.stream(s):
+        chain()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in out + sel + w]
+    # the eager result against the oracle
+    x_h, r_h = fx, res
+    for l in range(N_LAYER):
+        ref, sel_o, _ = orc.moe_layer(layers[l], x_h, r_h)
+        assert np.array_equal(sel[l].cpu().numpy(), sel_o), l
+        parity.assert_parity(out[l].cpu().numpy(), ref, f"layer chain {l}")
+        x_h = r_h = out[l].cpu().numpy()
+    print("graph: capture and replay", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        chain()
+    torch.cuda.synchronize()
+
+    def reset():
+        for t in out + w:
+            t.fill_(float("nan"))
+        for t in sel:
+            t.fill_(-1)
+
+    _replays_match(g, reset, out + sel + w, eager, "layer chain")
+
+
+def test_decode_captured(orc, stage):
+    shape, layers, st = stage
+    _, x = W.make_hidden(shape, 11, 0, 1)
+    x0 = st.dev(x)
+    xd = x0.clone()
+    s = torch.cuda.Stream()
+
+    def step():
+        H.check(st.lib.hoard_moe_decode(st.h, 0, N_LAYER, st.ptr(xd), ctypes.c_float(W.RMS_EPS),
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+
+    print("graph: eager per-layer decode", flush=True)
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    st.sync_check()
+    eager = xd.clone()
+    ref = x
+    for l in range(N_LAYER):
+        ref, _, _ = orc.moe_layer(layers[l], orc.rms_norm(ref, W.RMS_EPS), ref)
+    parity.assert_parity(eager.cpu().numpy(), ref, "per-layer decode")
+    print("graph: capture and replay decode", flush=True)
+    xd.copy_(x0)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    torch.cuda.synchronize()
+    _replays_match(g, lambda: xd.copy_(x0), [xd], [eager], "decode")
+    st.sync_check()
