@@ -1,6 +1,7 @@
-"""The per-layer path under HIP graph capture: hoard_moe_layer and the
-per-layer decode (route, gate/up, down launches; no copies, memsets or
-allocations once the handle is set up) captured into one graph, replayed
+"""The resident paths under HIP graph capture: hoard_moe_layer, the
+per-layer decode and the batched forward (kernel launches only: no copies,
+memsets or allocations once the handle is set up and each entry point has run
+once) captured into a graph, replayed
 several times with the program's own eager work and synchronisations between
 replays, each replay bit-identical to the eager launches, and the eager result
 at the parity bar against the oracle."""
@@ -19,6 +20,7 @@ torch = pytest.importorskip("torch")
 
 N_LAYER = 2
 REPLAYS = 4
+M = 16
 
 
 @pytest.fixture(scope="module")
@@ -26,7 +28,7 @@ def stage():
     from hoard_amd.runtime import MoEStage
     shape = W.QWEN3_30B
     layers = {l: W.make_layer(shape, 11, l) for l in range(N_LAYER)}
-    st = MoEStage(shape, n_layer=N_LAYER, layers=layers)
+    st = MoEStage(shape, n_layer=N_LAYER, layers=layers, max_tokens=M)
     st.set_option(H.OPT_PERSISTENT_DECODE, 0)
     yield shape, layers, st
     st.close()
@@ -118,3 +120,41 @@ def test_decode_captured(orc, stage):
     torch.cuda.synchronize()
     _replays_match(g, lambda: xd.copy_(x0), [xd], [eager], "decode")
     st.sync_check()
+
+
+def test_batched_forward_captured(orc, stage):
+    shape, layers, st = stage
+    D, k = shape.n_embd, shape.n_used
+    toks = [W.make_hidden(shape, 11, 1, 20 + t) for t in range(M)]
+    fx_d = st.dev(np.stack([f for f, _ in toks]))
+    res_d = st.dev(np.stack([r for _, r in toks]))
+    out = torch.empty(M, D, device="cuda")
+    sel = torch.empty(M, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(M, k, device="cuda")
+    s = torch.cuda.Stream()
+
+    def step():
+        H.check(st.lib.hoard_moe_forward_batched(st.h, 1, M, st.ptr(fx_d), st.ptr(res_d), st.ptr(out), st.ptr(sel),
+                                                 st.ptr(w), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+
+    print(f"graph: eager batched forward, M={M}", flush=True)
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    eager = [out.clone(), sel.clone(), w.clone()]
+    for t, (fx, res) in enumerate(toks):
+        ref, sel_o, _ = orc.moe_layer(layers[1], fx, res)
+        assert np.array_equal(sel[t].cpu().numpy(), sel_o), t
+        parity.assert_parity(out[t].cpu().numpy(), ref, f"batched token {t}")
+    print("graph: capture and replay batched forward", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    torch.cuda.synchronize()
+
+    def reset():
+        out.fill_(float("nan"))
+        w.fill_(float("nan"))
+        sel.fill_(-1)
+
+    _replays_match(g, reset, [out, sel, w], eager, "batched forward")
