@@ -237,9 +237,10 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value);
    resident, as the fetch step at :379-420 does: hits are classified first
    and move to the front of the layer's LRU list (:385-387), then each miss
    takes the least recently used slot, evicts its expert and is uploaded with
-   hipMemcpyAsync on copy_stream (:416-419; to_vram, :279-284).  copy_stream
-   first waits for the last FFN that read this layer's slots, and `stream` is
-   made to wait for the uploads, so an FFN launched on `stream` afterwards reads
+   hipMemcpyAsync (:416-419; to_vram, :279-284), the misses dealt round-robin
+   to copy_stream and two upload streams of the handle's own.  Each upload
+   stream first waits for the last FFN that read this layer's slots, and
+   `stream` is made to wait for the uploads, so an FFN launched on `stream` afterwards reads
    them; with copy_stream distinct from `stream` the uploads of layer l+1 overlap
    the FFN of layer l.  The slots go to slot_host and/or slot_dev (int32[n_used]),
    to be passed as ids to hoard_moe_ffn_combine.  hoard_moe_layer and
