@@ -8,9 +8,12 @@ activation chain never leaving the device.  Inputs are resident before the
 timed region starts.
 
 Prints ONE JSON line (rank 0).  `value` is microseconds per MoE layer per token
-(lower is better); `roofline` covers the dominant kernel, timed with HIP event
-pairs on its own stream; `cpu_baseline` is the C restatement of ggml-CPU's
-algorithm for the same stage on this host's cores.
+(lower is better); `drop_in_layer_us` is the same layer through hoard_moe_layer
+(three launches per layer, the entry point an engine calls when attention runs
+between MoE layers); `roofline` covers the dominant kernel, timed with a HIP
+event pair around each of its launches on the stream it runs on;
+`cpu_baseline` is the C restatement of ggml-CPU's algorithm for the same stage
+on this host's cores.
 """
 from __future__ import annotations
 
@@ -18,6 +21,7 @@ import argparse
 import ctypes
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -29,6 +33,15 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
 TYPE_NAMES = {11: "Q3_K", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}
+MODEL_NAMES = {"qwen3_30b": "Qwen3-30B-A3B", "qwen3_next": "Qwen3-Next-80B-A3B", "olmoe": "OLMoE-1B-7B",
+               "qwen35": "Qwen3.5-35B-A3B", "olmoe_q3": "OLMoE-1B-7B (Q3_K_M)"}
+CPU_THREADS_MAX = 16  # the host-core share of one GPU on the measurement boxes
+
+
+def metric_label(shape) -> str:
+    """The headline metric's wording for the shape measured."""
+    gu = TYPE_NAMES[shape.gate_type]
+    return f"MoE-layer us/token + HBM GB/s (% of peak), {MODEL_NAMES[shape.name]}-shape {gu} decode"
 
 
 def parse():
@@ -50,6 +63,11 @@ def parse():
     ap.add_argument("--pool", type=int, default=0, metavar="K",
                     help="slot-pool workload: K HBM slots per layer, all experts in pinned host memory, "
                          "routing from the seeded 512-token Zipf(0.8)+reuse trace")
+    ap.add_argument("--pool-mode", default="both", choices=["both", "demand", "trace"],
+                    help="demand: each layer's uploads are issued after its router has run and its selection "
+                         "was read back (the engine's situation); trace: every layer's uploads are enqueued "
+                         "ahead from the known trace, overlapping the previous layer's FFN; both: the two in "
+                         "turn, `value` being the on-demand rate")
     ap.add_argument("--store", action="store_true",
                     help="with --pool: experts streamed from a GGUF file on local disk through the storage tier "
                          "(RAM tier of --ram experts, --readers parallel O_DIRECT reads) instead of pinned masters")
@@ -157,10 +175,16 @@ def h2d_probe_gbps(nbytes: int = 1 << 30) -> float:
 
 def run_pool(args, shape, n_layer):
     """Slot-pool workload: one token = every layer's pool step (LRU bookkeeping,
-    uploads of the misses on a side stream) and expert FFN + combine, with the
-    routing taken from the seeded synthetic trace.  The uploads of layer l+1
-    overlap the FFN of layer l: the host enqueues every layer's pool step ahead
-    of the device, and each FFN waits only for its own layer's uploads."""
+    uploads of the misses on side streams) and expert FFN + combine, with the
+    selection taken from the seeded synthetic trace.  Two ways to fetch:
+    * on demand, as in the engine, where layer l's experts are known only once
+      its router has run (notes/MEMORY-FLOW.md:58-64 of the reference): the
+      router runs, its selection is read back (a synchronisation), then the
+      misses are uploaded and the FFN waits for them;
+    * trace-known prefetch: the host enqueues every layer's pool step ahead of
+      the device, so the uploads of layer l+1 overlap the FFN of layer l, and
+      each FFN waits only for its own layer's uploads.
+    Both start from an empty pool and see the same hits and misses."""
     import torch
 
     import hoard_amd as H
@@ -220,70 +244,104 @@ def run_pool(args, shape, n_layer):
     slots_d = torch.empty((n_layer, shape.n_used), dtype=torch.int32, device=dev)
     sel_h = np.ascontiguousarray(trace.sel)
 
-    def token(t):
+    sel_scratch = torch.empty(shape.n_used, dtype=torch.int32, device=dev)
+    w_scratch = torch.empty(shape.n_used, dtype=torch.float32, device=dev)
+
+    def token(t, on_demand):
         x = x_d[t % n_tok]
+        fx = ctypes.c_void_p(fx_d[t % n_tok].data_ptr())
         for l in range(n_layer):
+            if on_demand:
+                # the layer's router runs and its selection is read back before the
+                # fetch can start (the reference's D2H of sel, src/run_moe_stream.cpp:367);
+                # the selection used is the trace's
+                H.check(lib.hoard_moe_route(h, l, fx, ctypes.c_void_p(sel_scratch.data_ptr()),
+                                            ctypes.c_void_p(w_scratch.data_ptr()), sp))
+                stream.synchronize()
             H.check(lib.hoard_moe_pool_ensure(h, l, ctypes.c_void_p(sel_h[t, l].ctypes.data), None,
                                               ctypes.c_void_p(slots_d[l].data_ptr()), sp, cp))
-            H.check(lib.hoard_moe_ffn_combine(h, l, ctypes.c_void_p(fx_d[t % n_tok].data_ptr()),
-                                              ctypes.c_void_p(slots_d[l].data_ptr()),
+            H.check(lib.hoard_moe_ffn_combine(h, l, fx, ctypes.c_void_p(slots_d[l].data_ptr()),
                                               ctypes.c_void_p(w_d[t, l].data_ptr()), ctypes.c_void_p(x.data_ptr()),
                                               ctypes.c_void_p(x.data_ptr()), sp))
 
-    for t in range(warm):
-        token(t)
-    torch.cuda.synchronize()
-    H.check(lib.hoard_moe_reset_stats(h))
-    if store is not None:
-        store.reset_stats()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for t in range(warm, warm + steps):
-        token(t)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    st = H.MoeStats()
-    H.check(lib.hoard_moe_get_stats(h, ctypes.byref(st)))
+    def timed(on_demand):
+        """Warm-up tokens, then the timed ones, from an empty pool; (ms per token, stats)."""
+        H.check(lib.hoard_moe_set_option(h, H.OPT_POOL_NAIVE, 1))  # toggling naive mode empties every layer's slots
+        H.check(lib.hoard_moe_set_option(h, H.OPT_POOL_NAIVE, 0))
+        for t in range(warm):
+            token(t, on_demand)
+        torch.cuda.synchronize()
+        H.check(lib.hoard_moe_reset_stats(h))
+        if store is not None:
+            store.reset_stats()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for t in range(warm, warm + steps):
+            token(t, on_demand)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        st = H.MoeStats()
+        H.check(lib.hoard_moe_get_stats(h, ctypes.byref(st)))
+        # the events span the device's whole timeline, the idle gaps of the on-demand
+        # read-backs included
+        return e0.elapsed_time(e1) / steps, st
+
+    modes = {"both": [False, True], "trace": [False], "demand": [True]}[args.pool_mode]
+    runs = {}
+    for on_demand in modes:
+        runs[on_demand] = timed(on_demand)
+        sst_mode = store.stats() if store is not None else None
+        runs[on_demand] += (sst_mode,)
     lib.hoard_moe_destroy(h)
-    sst = None
     if store is not None:
-        sst = store.stats()
         store.close()
         import shutil
         shutil.rmtree(path.parent, ignore_errors=True)
     probe = h2d_probe_gbps()
-    bytes_tok = st.bytes_h2d / steps
+
+    def summary(ms, st, sst):
+        bytes_tok = st.bytes_h2d / steps
+        out = {"tokens_per_s": round(1000.0 / ms, 3), "ms_per_token": round(ms, 4),
+               "hit_rate": round(st.hits / max(1, st.reqs), 4), "requests": int(st.reqs), "misses": int(st.misses),
+               "h2d_bytes_per_token": int(bytes_tok), "h2d_gbps": round(bytes_tok / (ms * 1e-3) / 1e9, 2),
+               "link_frac": round(bytes_tok / (ms * 1e-3) / 1e9 / probe, 4)}
+        if sst is not None:
+            out["store"] = {
+                "requests": int(sst.requests), "ram_hits": int(sst.ram_hits), "file_reads": int(sst.file_reads),
+                "ram_hit_rate": round(sst.ram_hits / max(1, sst.requests), 4),
+                "read_gbps": round(sst.bytes_read / max(1, sst.read_ns), 3),
+                "read_ms_per_token": round(sst.read_ns / 1e6 / steps, 3),
+                "direct": int(sst.direct),
+            }
+        return out
+
+    main_mode = True if True in runs else False
+    ms, st, sst = runs[main_mode]
+    head = summary(ms, st, sst)
     result = {
         "metric": "slot-pool decode tokens/s, Qwen3-30B-A3B-shape Q4_K, K-slot HBM LRU over pinned host experts",
-        "value": round(1000.0 / ms, 3), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": head["ms_per_token"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_K/q6_K weights x q8_K activations (int8 dot), f32 router/accumulate",
         "data": "synthetic weights; routing from a seeded 512-token trace: Zipf(0.8) popularity per layer, "
                 "40% reuse of the previous 4 tokens' experts",
         "config": {"workload": f"{shape.name}: {n_layer} layers, K={K} slots per layer, "
                                f"all {shape.n_expert} experts per layer in pinned host memory",
-                   "pool_k": K, "layers": n_layer},
-        "hit_rate": round(st.hits / max(1, st.reqs), 4),
-        "requests": int(st.reqs), "misses": int(st.misses),
-        "h2d_bytes_per_token": int(bytes_tok),
-        "h2d_gbps": round(bytes_tok / (ms * 1e-3) / 1e9, 2),
+                   "pool_k": K, "layers": n_layer,
+                   "fetch": "on demand: each layer's uploads issued after its router ran and the selection was "
+                            "read back" if main_mode else
+                            "trace-known prefetch: every layer's uploads enqueued ahead from the trace"},
         "h2d_probe_gbps": round(probe, 2),
-        "link_frac": round(bytes_tok / (ms * 1e-3) / 1e9 / probe, 4),
     }
-    if sst is not None:
+    result.update({k: v for k, v in head.items() if k not in ("tokens_per_s", "ms_per_token")})
+    if main_mode and False in runs:
+        result["trace_known_prefetch"] = summary(*runs[False])
+    if store is not None:
         result["metric"] = ("slot-pool decode tokens/s, Qwen3-30B-A3B-shape Q4_K, K-slot HBM LRU over a RAM tier "
                             "streamed from the model file")
         result["config"]["workload"] = (f"{shape.name}: {n_layer} layers, K={K} slots per layer, RAM tier of "
                                         f"{sst.ram_experts} experts, the rest read from a GGUF on local disk")
         result["config"].update(ram_experts=int(sst.ram_experts), readers=args.readers)
-        result["store"] = {
-            "requests": int(sst.requests), "ram_hits": int(sst.ram_hits), "file_reads": int(sst.file_reads),
-            "ram_hit_rate": round(sst.ram_hits / max(1, sst.requests), 4),
-            "read_gbps": round(sst.bytes_read / max(1, sst.read_ns), 3),
-            "read_ms_per_token": round(sst.read_ns / 1e6 / steps, 3),
-            "direct": int(sst.direct),
-        }
     print(json.dumps(result), flush=True)
 
 
@@ -405,30 +463,65 @@ def measured_traffic(shape, kernel: str, n_layer: int):
     return int(t["hbm_bytes_per_launch"])
 
 
-def cpu_baseline(shape, seed: int, budget_s: float):
-    """The oracle (C restatement of ggml-CPU's algorithm) on host cores."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(shape, seed: int, budget_s: float, n_layer: int):
+    """The oracle (C restatement of ggml-CPU's algorithm: f32 router, Q8_K of the
+    activations, integer super-block dots, OpenMP over rows) on host cores.  The
+    sample cycles through every layer of the stack, each with its own weights and
+    4 hiddens, so the weights stream from DRAM (only the experts those hiddens
+    select are generated: several GB, far above the last-level cache)."""
     import oracle
     from hoard_amd import workloads as W
-    threads = min(16, os.cpu_count() or 1)
-    oracle.lib().orc_set_num_threads(threads)
-    n_host_layers = 4
-    layers = [W.make_layer(shape, seed, l) for l in range(n_host_layers)]
-    toks = [W.make_hidden(shape, seed, 1000 + t % 16, t) for t in range(16)]
-    oracle.moe_layer(layers[0], *toks[0])  # warm
-    done, t0 = 0, time.perf_counter()
-    while True:
-        fx, res = toks[done % len(toks)]
-        oracle.moe_layer(layers[done % n_host_layers], fx, res)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and done >= 8:
-            break
-    us = el / done * 1e6
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(avail, CPU_THREADS_MAX))
+    n_hid = 4
+    layers, toks, touched = [], [], 0
+    for l in range(n_layer):
+        hid = [W.make_hidden(shape, seed, 1000 + l, t) for t in range(n_hid)]
+        router = W.make_router(shape, seed, l)
+        need = set()
+        for fx, _ in hid:
+            need |= set(oracle.route(router, fx, shape.n_expert, shape.n_used, shape.renorm)[0].tolist())
+        layers.append(W.make_layer(shape, seed, l, experts=sorted(need)))
+        toks.append(hid)
+        touched += len(need) * shape.expert_bytes() + router.nbytes
+    lib = oracle.lib()
+
+    def run(nthreads, budget):
+        lib.orc_set_num_threads(nthreads)
+        oracle.moe_layer(layers[0], *toks[0][0])  # warm
+        done, t0 = 0, time.perf_counter()
+        while True:
+            l = done % n_layer
+            oracle.moe_layer(layers[l], *toks[l][(done // n_layer) % n_hid])
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= budget and done >= n_layer:
+                return el / done * 1e6, done, el
+
+    us, done, el = run(threads, budget_s)
+    us1, done1, el1 = run(1, budget_s / 3)
+    lb = shape.bytes_per_token_layer()
     return {
         "value": round(us, 2), "unit": "us/layer", "cores": threads, "kind": "port",
-        "sample": f"{done} token-layers of the same shape cycling {n_host_layers} distinct layers "
-                  f"({shape.name}, fresh hidden per token), OpenMP over rows, {el:.1f} s",
-        "tokens_per_s_48_layers": round(1e6 / (us * 48), 3),
+        "sample": f"{done} token-layers cycling the {n_layer} layers of {shape.name} (4 hiddens each, "
+                  f"{touched / 1e9:.1f} GB of weights touched), OpenMP over rows, {el:.1f} s",
+        "cpu_model": cpu_model(), "cores_available": avail,
+        "tokens_per_s": round(1e6 / (us * n_layer), 3),
+        "dram_gbps": round(lb / us / 1e3, 2),
+        "one_thread": {"value": round(us1, 2), "unit": "us/layer", "sample": f"{done1} token-layers, {el1:.1f} s",
+                       "tokens_per_s": round(1e6 / (us1 * n_layer), 3)},
+        "what": "ggml-algorithm restatement (ggml itself is not available offline)",
     }
 
 
@@ -508,7 +601,29 @@ def main():
     us_layer = ms_per_step * 1000.0 / n_layer
     assert torch.isfinite(xs).all().item(), "non-finite decode output"
 
-    # ---- per-kernel durations: event pair around every launch ------------------
+    # ---- the drop-in path: hoard_moe_layer per layer (fx given, residual chained) --
+    fxs = torch.stack([torch.from_numpy(W.make_hidden(shape, args.seed, 0, t)[0]) for t in range(8)]).to(dev)
+    xl = xs[:8].clone()
+
+    def layer_step(i):
+        x = xl[i % 8]
+        fx = ctypes.c_void_p(fxs[i % 8].data_ptr())
+        for l in range(n_layer):
+            H.check(lib.hoard_moe_layer(h, l, fx, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                        None, None, sp))
+
+    for i in range(warm):
+        layer_step(i)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(steps):
+        layer_step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    drop_in_us = ev0.elapsed_time(ev1) * 1000.0 / (steps * n_layer)
+    assert torch.isfinite(xl).all().item(), "non-finite hoard_moe_layer output"
+
+    # ---- per-kernel durations: a HIP event pair around every launch, on its stream --
     H.check(lib.hoard_moe_profile(h, 1))
     for i in range(warm, warm + steps):
         step(i)
@@ -530,7 +645,7 @@ def main():
     layer_gbps = layer_bytes / (us_layer * 1e3)
     wtypes = "/".join(dict.fromkeys(TYPE_NAMES[t] for t in (shape.gate_type, shape.up_type, shape.down_type)))
     result = {
-        "metric": "MoE-layer us/token + HBM GB/s (% of peak), Qwen3-30B-A3B-shape Q4_K decode",
+        "metric": metric_label(shape),
         "value": round(us_layer, 3),
         "unit": "us/layer",
         "n_gpus": 1,
@@ -550,11 +665,15 @@ def main():
         "layer_hbm_gbps": round(layer_gbps, 1),
         "layer_hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "layer_bytes": layer_bytes,
+        "drop_in_layer_us": round(drop_in_us, 3),
+        "drop_in_layer_hbm_frac": round(layer_bytes / (drop_in_us * 1e3) / HBM_PEAK_GBPS, 4),
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbps"], "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(dk["gbps"] / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(shape, dom, n_layer),
-                     "algorithmic_bytes": dk["bytes"]},
+                     "algorithmic_bytes": dk["bytes"],
+                     "basis": "algorithmic bytes per launch / mean duration of a hipEvent pair recorded around "
+                              "each launch on its stream (launch gaps included)"},
     }
     persistent = ctypes.c_int()
     H.check(lib.hoard_moe_get_option(h, H.OPT_PERSISTENT_AVAILABLE, ctypes.byref(persistent)))
@@ -571,9 +690,13 @@ def main():
             result["phases_us"] = ph
             for k_, v_ in ph.items():
                 log(f"[phase] {k_:40s} {v_:8.3f} us")
+    # release every device object before the CPU leg: the handle, then torch's tensors
     lib.hoard_moe_destroy(h)
+    del xs, xl, fxs
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds, n_layer)
     print(json.dumps(result), flush=True)
 
 

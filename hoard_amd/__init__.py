@@ -71,6 +71,8 @@ OPT_DECODE_KERNEL = 4
 OPT_DECODE_KERNELS_AVAILABLE = 5
 OPT_LAYER_KERNELS = 6
 OPT_DECODE_LAUNCH = 7
+OPT_WAIT_LIMIT_US = 8
+OPT_FAIL_UPLOAD = 9
 DECODE_AUTO, DECODE_XCD, DECODE_SPREAD = 0, 1, 2
 
 

@@ -328,9 +328,9 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
         acc = acc + __shfl_xor(acc, 2);
         if (l == 0 && row < E)
             __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // Q8_K of fx: the first nb workgroups of a token group quantise block
-        // blockIdx.x of their tokens
-        if ((int)blockIdx.x < nb) wave_quantize_q8l(x + blockIdx.x * QK, q8(a.q8x) + (size_t)t * nb + blockIdx.x);
+        // Q8_K of fx: workgroup i of a token group quantises blocks i, i + gridDim.x, ...
+        // of its tokens, so every block is formed whatever the expert count (grid width)
+        for (int b = blockIdx.x; b < nb; b += gridDim.x) wave_quantize_q8l(x + b * QK, q8(a.q8x) + (size_t)t * nb + b);
     }
     // Completion protocol without cache-flushing fences: the logits and the
     // tails' sel / wsel are stored at device scope (through to memory, past

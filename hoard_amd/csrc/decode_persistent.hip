@@ -101,6 +101,7 @@ template <int TGU, int NB, int TD, int NBH>
 __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sh_rank, sh_fail;
+    __shared__ unsigned seq_s;
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
     __shared__ unsigned gu_done;   // gate/up row waves done, counted over layers
@@ -115,9 +116,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         sh_rank = (int)(t % kPerXcd);
         sh_fail = 0;
         gu_done = 0;
+        seq_s = seq_begin(a.seq);
     }
     __syncthreads();
     const int rank = sh_rank;
+    const unsigned seq0 = seq_s;
     const Smem S = smem_layout(a, nullptr);
     float *xs = reinterpret_cast<float *>(smem + S.xs);
     const float *wl = reinterpret_cast<const float *>(smem + S.w);
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     bool ok = true;
     for (int l = a.l0; l < a.l1; ++l) {
         const DecodeLayer &L = a.layers[l];
-        const unsigned seq = a.seq0 + 4u * (unsigned)(l - a.l0);
+        const unsigned seq = seq0 + 4u * (unsigned)(l - a.l0);
         const int cur = (l - a.l0) & 1;
         const bool last = l + 1 == a.l1;
         stamp(l, 0);
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                     for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 1u);
                     return r;
                 },
-                a.err);
+                a.err, a.wait_ticks);
             if (!got) sh_fail = 1;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                     const bool r = (lane >= E || tag_seq(w0) == seq) && (lane + 64 >= E || tag_seq(w1) == seq);
                     return (bool)__all(r);
                 },
-                a.err);
+                a.err, a.wait_ticks);
             if (!got && lane == 0) sh_fail = 1;
             float p0 = lane < E ? tag_val(w0) : -INFINITY;
             float p1 = lane + 64 < E ? tag_val(w1) : -INFINITY;
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                         [&]() {
                             return __hip_atomic_load(&gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target;
                         },
-                        a.err);
+                        a.err, a.wait_ticks);
                     if (!done) sh_fail = 1;
                     publish_h();
                 }
@@ -445,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                         }
                         return (bool)__all(r);
                     },
-                    a.err);
+                    a.err, a.wait_ticks);
                 if (!got && lane == 0) sh_fail = 1;
                 const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
                 wave_quantize_q8l_regs(v, &q8h[wave]);
@@ -507,7 +510,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                         for (int j = 0; j < 8; ++j) r = r & ((j >= k) | (tag_seq(w[j]) == seq + 2u));
                         return r;
                     },
-                    yw, a.err);
+                    yw, a.err, a.wait_ticks);
                 if (!got) sh_fail = 1;
                 float acc = 0.0f;
 #pragma unroll
@@ -529,6 +532,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
     if ((!ok || sh_fail) && xcc == 0) {  // poison this workgroup's output rows so the caller sees the failure
         for (int t = tid; t < RD; t += kThreads) a.x[rank * RD + t] = __builtin_nanf("");
     }
+    if (tid == 0) seq_end(a.seq, seq0, 4u * (unsigned)(a.l1 - a.l0) + 4u, gridDim.x);
 }
 
 }  // namespace

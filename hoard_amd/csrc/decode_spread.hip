@@ -170,6 +170,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     __shared__ float w_s[16];
     __shared__ float sg_s;
     __shared__ int fail_s, rank_s;
+    __shared__ unsigned seq_s;
     __shared__ unsigned gu_done;  // waves 0-5 done with their gate/up rows, counted over layers
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -180,10 +181,12 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                                                   __HIP_MEMORY_SCOPE_AGENT);
         rank_s = (int)(t % kPerXcd);
         fail_s = 0;
+        seq_s = seq_begin(a.seq);
         gu_done = 0;
     }
     __syncthreads();
     const int rank = rank_s;
+    const unsigned seq0 = seq_s;
     const int g = (int)xcc * kPerXcd + rank;
 
     float *xs = reinterpret_cast<float *>(smem + S::oXS);
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
 
     for (int l = a.l0; l < a.l1; ++l) {
         const DecodeLayer &L = a.layers[l];
-        const unsigned seq = a.seq0 + 4u * (unsigned)(l - a.l0);
+        const unsigned seq = seq0 + 4u * (unsigned)(l - a.l0);
         const bool last = l + 1 == a.l1;
         stamp(l, 0);
 
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                         for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 1u);
                         return r;
                     },
-                    a.err);
+                    a.err, a.wait_ticks);
                 if (!got) fail_s = 1;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
@@ -322,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                     for (int c = 0; c < kPer; ++c) r = r & (tag_seq(w[c]) == seq);
                     return (bool)__all(r);
                 },
-                a.err);
+                a.err, a.wait_ticks);
             if (!got) fail_s = 1;
             float m = -INFINITY;
 #pragma unroll
@@ -465,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             const unsigned target = (unsigned)S::kGuWaves * (unsigned)(l - a.l0 + 1);
             const bool done = poll(
                 [&]() { return __hip_atomic_load(&gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target; },
-                a.err);
+                a.err, a.wait_ticks);
             if (!done) fail_s = 1;
             if (lane < HR) {
                 const float gv = guv[lane], uv = guv[HR + lane];
@@ -490,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                     for (int c = 0; c < S::kGatherH; ++c) r = r & (tag_seq(w[c]) == seq + 1u);
                     return r;
                 },
-                a.err);
+                a.err, a.wait_ticks);
             if (!got) fail_s = 1;
 #pragma unroll
             for (int c = 0; c < S::kGatherH; ++c) {
@@ -556,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                     for (int u = 0; u < U; ++u) r = r & (tag_seq(yw[u]) == seq + 2u);
                     return r;
                 },
-                a.err);
+                a.err, a.wait_ticks);
             if (!got) fail_s = 1;
             float acc = 0.0f;
 #pragma unroll
@@ -577,6 +580,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (fail_s && xcc == 0 && tid < RC) a.x[rank * RC + tid] = __builtin_nanf("");  // the caller sees the failure
+    if (tid == 0) seq_end(a.seq, seq0, 4u * (unsigned)(a.l1 - a.l0) + 4u, gridDim.x);
 }
 
 }  // namespace

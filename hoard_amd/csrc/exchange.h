@@ -13,7 +13,7 @@
 
 namespace hoard {
 
-constexpr long long kTimeoutTicks = 20000000;  // 200 ms at the 100 MHz wall clock
+constexpr long long kTimeoutTicks = 20000000;  // default bound of a wait: 200 ms at the 100 MHz wall clock
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned v;
@@ -54,15 +54,31 @@ __device__ __forceinline__ uint64_t ld_dev64(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Bounded poll: true once ready() holds; false on timeout or a raised error.
+// Sequence base of a one-launch decode, kept in device memory so that a
+// launch needs no host-side state and a launch replayed from a captured
+// graph tags its words afresh: seq[0] holds the base of the next launch,
+// seq[1] counts finished workgroups.  Every workgroup reads the base when it
+// starts; the last of a launch's `groups` workgroups to finish moves it past
+// every tag the launch used.  The next launch on the stream starts after this
+// one has ended, so it reads the moved base.
+__device__ __forceinline__ unsigned seq_begin(const unsigned *seq) { return ld_dev_u32(seq); }
+__device__ __forceinline__ void seq_end(unsigned *seq, unsigned base, unsigned used, unsigned groups) {
+    const unsigned done = __hip_atomic_fetch_add(seq + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (done % groups == 0u) st_dev_u32(seq, base + used);
+}
+
+// Bounded poll: true once ready() holds; false on timeout (`limit` ticks of
+// the 100 MHz wall clock) or a raised error.  The flag and the clock are
+// checked every 32 probes; a limit of 0 gives up at the first probe that finds
+// the data missing (the host forces the failure path that way).
 template <class F>
-__device__ __forceinline__ bool poll(F ready, int *err) {
+__device__ __forceinline__ bool poll(F ready, int *err, long long limit) {
     const long long t0 = wall_clock64();
     for (int it = 0;; ++it) {
         if (ready()) return true;
-        if ((it & 31) == 31) {
+        if ((it & 31) == 31 || limit == 0) {
             if (ld_dev_u32((const unsigned *)err) != 0u) return false;
-            if (wall_clock64() - t0 > kTimeoutTicks) {
+            if (wall_clock64() - t0 >= limit) {
                 st_dev_u32((unsigned *)err, 1u);
                 return false;
             }
@@ -77,7 +93,7 @@ __device__ __forceinline__ bool poll(F ready, int *err) {
 // for it); the probe's loads must not sit behind branches, or the compiler
 // waits for both.  On success the landed probe is copied to out.
 template <int N, class P, class C>
-__device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int *err) {
+__device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int *err, long long limit) {
     uint64_t pa[N], pb[N];
     probe(pa);
     return poll(
@@ -96,7 +112,7 @@ __device__ __forceinline__ bool poll2(P probe, C landed, uint64_t (&out)[N], int
             }
             return false;
         },
-        err);
+        err, limit);
 }
 
 }  // namespace hoard

@@ -127,7 +127,8 @@ struct PersistentArgs {
     uint64_t *Y;                // [2][8][n_embd]  expert outputs by slot
     unsigned *tickets;          // [8] counters, 128 B apart
     int *err;
-    unsigned seq0;
+    unsigned *seq;              // [2] device-side sequence base and finished-workgroup count
+    long long wait_ticks;       // bound of every cross-workgroup wait (100 MHz ticks)
     unsigned long long *trace;  // optional [layer][256 workgroups][kTracePhases] wall-clock stamps
 };
 constexpr int kTracePhases = 12;
@@ -158,7 +159,8 @@ struct SpreadArgs {
     uint64_t *X;                // [8][n_embd]          x between layers, one copy per XCD
     unsigned *tickets;          // [8] counters, 128 B apart
     int *err;
-    unsigned seq0;
+    unsigned *seq;              // [2] device-side sequence base and finished-workgroup count
+    long long wait_ticks;       // bound of every cross-workgroup wait (100 MHz ticks)
     unsigned long long *trace;  // optional [layer][256 workgroups][kTracePhases] wall-clock stamps
 };
 bool spread_shape_compiled(const SpreadArgs &a);

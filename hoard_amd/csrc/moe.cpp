@@ -107,14 +107,15 @@ struct hoard_moe {
     int decode_kernel = 0;             // HOARD_OPT_DECODE_KERNEL value
     bool layer_kernels = true;         // HOARD_OPT_LAYER_KERNELS: instantiated per-layer kernels
     bool coop_launch = true;           // HOARD_OPT_DECODE_LAUNCH 0: cooperative one-launch decode
-    bool table_dirty = true;
-    hoard::DecodeLayer *d_table = nullptr;
+    long long wait_ticks = 20000000;   // HOARD_OPT_WAIT_LIMIT_US: bound of the decode's waits (100 MHz ticks)
+    hoard::DecodeLayer *d_table = nullptr;  // per-layer pointers of the one-launch decode, kept current
     uint64_t *pX = nullptr, *pLG = nullptr, *pH = nullptr, *pY = nullptr;
     uint64_t *sX = nullptr, *sLG = nullptr, *sH = nullptr, *sY = nullptr;  // spread kernel's exchange words
     unsigned *sflags = nullptr;                                             // its tickets
     unsigned *pflags = nullptr;        // tickets
     int *perr = nullptr;
-    unsigned seq = 1;
+    unsigned *seqw = nullptr;          // device: sequence base + finished count, [0..1] expert-per-XCD kernel,
+                                       // [32..33] rows-spread kernel
     unsigned long long *ptrace = nullptr;  // phase stamps of the last traced decode
     // expert slot pool (pool_k > 0)
     hoard::SlotLru lru;
@@ -123,6 +124,7 @@ struct hoard_moe {
     int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
     hipStream_t copy_x[kUpStreams - 1] = {};  // upload streams besides the caller's: copies in flight
                                               // together hide each one's set-up
+    int fail_upload = 0;            // HOARD_OPT_FAIL_UPLOAD: the n-th slot upload from now fails (test hook)
     hoard::Store *store = nullptr;  // storage tier serving slot misses (attached), else pinned masters
     bool weights_set = false;       // a layer's weights were set (a store attaches before that)
     // batched path (allocated on first use)
@@ -162,6 +164,7 @@ struct hoard_moe {
         hipFree(sflags);
         hipFree(pflags);
         hipFree(perr);
+        hipFree(seqw);
         hipFree(ptrace);
         hipHostFree(pin_sel);
         hipFree(slot_ids);
@@ -346,6 +349,22 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
 // the slot ids through a pinned staging copy on `stream`.
 constexpr int kMaxPoolIds = 16 * 16;  // ids one pool step takes: up to 16 tokens x 16 experts
 
+// One slot upload.  HOARD_OPT_FAIL_UPLOAD counts down to an upload that fails
+// as a refused hipMemcpyAsync would, before anything is issued.
+hipError_t slot_upload(hoard_moe *h, void *dst, const void *src, size_t n, hipStream_t s) {
+    if (h->fail_upload > 0 && --h->fail_upload == 0) return hipErrorOutOfMemory;
+    return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s);
+}
+
+// A pool step that failed part-way: wait for the uploads it issued, then
+// forget the layer's slot residency.
+void pool_abandon(hoard_moe *h, int layer, const hipStream_t *up) {
+    for (int i = 0; i < kUpStreams; ++i)
+        (void)hipStreamSynchronize(up[i]);
+    (void)hipGetLastError();
+    h->lru.reset_layer(layer);
+}
+
 int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequential, int32_t *slot_host,
                 int32_t *slot_dev, hipStream_t s, hipStream_t cs) {
     const hoard_moe_cfg &c = h->cfg;
@@ -360,6 +379,19 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
         h->lru.access(layer, sel, n, h->pool_naive, slots, miss);
     int n_miss = 0;
     for (int j = 0; j < n; ++j) n_miss += miss[j];
+    // From here on the LRU maps the missed slots to their new experts: a failure
+    // before their uploads are issued leaves the slots holding other bytes, so
+    // the layer's residency is forgotten (every slot is a miss next time), and
+    // the uploads already issued are waited for, so none lands after a later
+    // upload into the same slot.
+#define POOL_TRY(expr)                                                                           \
+    do {                                                                                         \
+        hipError_t e_ = (expr);                                                                  \
+        if (e_ != hipSuccess) {                                                                  \
+            pool_abandon(h, layer, up);                                                          \
+            return fail(HOARD_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));                  \
+        }                                                                                        \
+    } while (0)
     // misses are dealt round-robin to the caller's copy stream and the internal
     // ones; each first waits until the last FFN reading this layer's slots is done
     hipStream_t up[kUpStreams];
@@ -367,7 +399,7 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
     for (int i = 1; i < kUpStreams; ++i) up[i] = h->copy_x[i - 1];
     const int n_up = n_miss < kUpStreams ? (n_miss > 0 ? n_miss : 1) : kUpStreams;
     if (n_miss && L.used)
-        for (int i = 0; i < n_up; ++i) HIP_TRY(hipStreamWaitEvent(up[i], L.last_use, 0));
+        for (int i = 0; i < n_up; ++i) POOL_TRY(hipStreamWaitEvent(up[i], L.last_use, 0));
     int m = 0;
     if (h->store) {
         // storage tier: the RAM tier serves or reads the missed experts (reads in
@@ -391,10 +423,13 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
         for (int i = 0; i < nm; ++i) {
             uint8_t *dst = L.slots + (size_t)slots[mj[i]] * rec;
             hipStream_t us = up[m++ % n_up];
-            HIP_TRY(hipMemcpyAsync(dst, ent[i].part[0], L.gbytes, hipMemcpyHostToDevice, us));
-            HIP_TRY(hipMemcpyAsync(dst + L.gbytes, ent[i].part[1], L.ubytes, hipMemcpyHostToDevice, us));
-            HIP_TRY(hipMemcpyAsync(dst + L.gbytes + L.ubytes, ent[i].part[2], L.dbytes, hipMemcpyHostToDevice, us));
-            if (int rc = h->store->fence(ent[i].slot, us)) return rc;
+            POOL_TRY(slot_upload(h, dst, ent[i].part[0], L.gbytes, us));
+            POOL_TRY(slot_upload(h, dst + L.gbytes, ent[i].part[1], L.ubytes, us));
+            POOL_TRY(slot_upload(h, dst + L.gbytes + L.ubytes, ent[i].part[2], L.dbytes, us));
+            if (int rc = h->store->fence(ent[i].slot, us)) {
+                pool_abandon(h, layer, up);
+                return rc;
+            }
         }
         for (int j = 0; j < n; ++j) {
             h->stats.reqs += 1;
@@ -410,18 +445,18 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
                 continue;
             }
             const size_t e = (size_t)sel[j], sl = (size_t)slots[j], rec = L.gstride;  // one [g|u|d] record
-            HIP_TRY(hipMemcpyAsync(L.slots + sl * rec, L.host_experts + e * rec, rec, hipMemcpyHostToDevice,
-                                   up[m++ % n_up]));
+            POOL_TRY(slot_upload(h, L.slots + sl * rec, L.host_experts + e * rec, rec, up[m++ % n_up]));
             h->stats.misses += 1;
             h->stats.bytes_h2d += rec;
         }
     }
     if (n_miss) {
         for (int i = 0; i < n_up; ++i) {
-            HIP_TRY(hipEventRecord(L.copied[i], up[i]));
-            HIP_TRY(hipStreamWaitEvent(s, L.copied[i], 0));
+            POOL_TRY(hipEventRecord(L.copied[i], up[i]));
+            POOL_TRY(hipStreamWaitEvent(s, L.copied[i], 0));
         }
     }
+#undef POOL_TRY
     if (slot_host) std::memcpy(slot_host, slots, sizeof(int32_t) * n);
     if (slot_dev) {
         if (L.stage_pending) HIP_TRY(hipEventSynchronize(L.staged));  // previous ids consumed
@@ -484,10 +519,15 @@ int persistent_setup(hoard_moe *h) {
     if (h->persistent_shape_ok) {
         rc = dev_alloc((void **)&h->d_table, sizeof(hoard::DecodeLayer) * c.n_layer);
         rc = rc ? rc : dev_alloc((void **)&h->perr, sizeof(int));
+        rc = rc ? rc : dev_alloc((void **)&h->seqw, 64 * sizeof(unsigned));
         if (rc) return rc;
+        HIP_TRY(hipMemset(h->d_table, 0, sizeof(hoard::DecodeLayer) * c.n_layer));
         HIP_TRY(hipMemset(h->perr, 0, sizeof(int)));
+        // sequence tags start at 1, so zeroed exchange words never read as current
+        unsigned init[64] = {};
+        init[0] = init[32] = 1u;
+        HIP_TRY(hipMemcpy(h->seqw, init, sizeof init, hipMemcpyHostToDevice));
     }
-    // sequence tags start at 1, so zeroed words never read as current
     if (h->xcd_ok) {
         const size_t nX = (size_t)2 * 8 * c.n_embd, nLG = (size_t)8 * c.n_expert, nH = (size_t)8 * c.n_ff;
         rc = rc ? rc : dev_alloc((void **)&h->pX, sizeof(uint64_t) * nX);
@@ -575,7 +615,8 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
     a.X = h->sX;
     a.tickets = h->sflags;
     a.err = h->perr;
-    a.seq0 = h->seq;
+    a.seq = h->seqw + 32;
+    a.wait_ticks = h->wait_ticks;
     if (int rc = trace_buffer(h, l0, l1, &a.trace)) return rc;
     hipError_t e;
     {
@@ -587,7 +628,6 @@ int spread_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStream_t
         if (h->persistent_mode == 2) return fail(HOARD_ERR_HIP, "spread decode launch: %s", hipGetErrorString(e));
         return HOARD_OK;  // auto mode: fall back to the per-layer kernels
     }
-    h->seq += 4u * (unsigned)(l1 - l0) + 4u;
     *used = true;
     return HOARD_OK;
 }
@@ -634,6 +674,16 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     auto skip = [&](const char *why) {
         return h->persistent_mode == 2 ? fail(HOARD_ERR_UNSUPPORTED, "persistent decode: %s", why) : HOARD_OK;
     };
+    // Under stream capture only the plain launch is recorded (its sequence tags
+    // live in device memory, so every replay tags its words afresh); the
+    // cooperative launch is not captured, and auto mode records the per-layer
+    // kernels instead.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &capture));
+    if (capture != hipStreamCaptureStatusNone) {
+        if (h->coop_launch) return skip("a cooperative launch cannot be captured (HOARD_OPT_DECODE_LAUNCH 1 can)");
+        if (h->tracing) return skip("phase tracing is not captured");
+    }
     // one kernel instantiation serves the whole range: uniform types, gate = up
     const int gu_type = h->layers[l0].gate_type, d_type = h->layers[l0].down_type;
     for (int l = l0; l < l1; ++l) {
@@ -649,17 +699,6 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     // auto picks the expert-per-XCD kernel where it applies, else the rows-spread one
     const bool spread = h->decode_kernel == 2 || (h->decode_kernel == 0 && !h->xcd_ok);
     if (spread ? !h->spread_ok : !h->xcd_ok) return skip("the selected decode kernel does not take this shape");
-    if (h->table_dirty) {
-        std::vector<hoard::DecodeLayer> t(c.n_layer);
-        for (int l = 0; l < c.n_layer; ++l) {
-            const Layer &L = h->layers[l];
-            t[l] = hoard::DecodeLayer{L.router,   L.gate,      L.up,        L.down,        L.gstride,
-                                      L.ustride,  L.dstride,   L.gate_type, L.up_type,     L.down_type,
-                                      L.sh_gate,  L.sh_up,     L.sh_down,   L.sh_gate_inp};
-        }
-        HIP_TRY(hipMemcpy(h->d_table, t.data(), sizeof(hoard::DecodeLayer) * t.size(), hipMemcpyHostToDevice));
-        h->table_dirty = false;
-    }
     if (spread) return spread_decode(h, l0, l1, x, eps, s, used, skip);
     if (!hoard::persistent_shape_compiled(gu_type, c.n_embd, d_type, c.n_ff))
         return skip("no kernel instantiated for these types and sizes");
@@ -688,7 +727,8 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
     a.Y = h->pY;
     a.tickets = h->pflags;
     a.err = h->perr;
-    a.seq0 = h->seq;
+    a.seq = h->seqw;
+    a.wait_ticks = h->wait_ticks;
     if (int rc = trace_buffer(h, l0, l1, &a.trace)) return rc;
     hipError_t e;
     {
@@ -700,7 +740,6 @@ int persistent_decode(hoard_moe *h, int l0, int l1, float *x, float eps, hipStre
         if (h->persistent_mode == 2) return fail(HOARD_ERR_HIP, "persistent decode launch: %s", hipGetErrorString(e));
         return HOARD_OK;  // auto mode: fall back to the per-layer kernels
     }
-    h->seq += 4u * (unsigned)(l1 - l0) + 4u;
     *used = true;
     return HOARD_OK;
 }
@@ -763,6 +802,10 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
                 rc = fail(HOARD_ERR_HIP, "upload stream");
     }
     if (!rc) rc = persistent_setup(h);
+    // the zeroed counters and exchange words are in place before any launch, on
+    // whatever stream the caller uses (a non-blocking stream does not wait for
+    // the null stream's memsets)
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = fail(HOARD_ERR_HIP, "device synchronisation after set-up");
     if (rc) {
         delete h;
         return rc;
@@ -870,7 +913,13 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
         return rc;
     }
     L.loaded = true;
-    h->table_dirty = true;
+    if (h->d_table) {
+        // the one-launch decode reads each layer's pointers from this table
+        const hoard::DecodeLayer t{L.router,  L.gate,      L.up,      L.down,        L.gstride,
+                                   L.ustride, L.dstride,   L.gate_type, L.up_type,   L.down_type,
+                                   L.sh_gate, L.sh_up,     L.sh_down, L.sh_gate_inp};
+        HIP_TRY(hipMemcpy(h->d_table + layer, &t, sizeof t, hipMemcpyHostToDevice));
+    }
     return HOARD_OK;
 }
 
@@ -1013,6 +1062,9 @@ int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
         rc = rc ? rc : dev_alloc((void **)&h->b_counters, sizeof(unsigned) * hoard::kBatchedCounters);
         if (rc) return rc;
         HIP_TRY(hipMemset(h->b_counters, 0, sizeof(unsigned) * hoard::kBatchedCounters));
+        // the counters must read zero before the first launch, which may go to a
+        // non-blocking stream that does not wait for work on the null stream
+        HIP_TRY(hipDeviceSynchronize());
     }
     hoard::BatchedArgs a{};
     a.M = M;
@@ -1164,6 +1216,14 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "decode launch %d", value);
         h->coop_launch = value == 0;
         return HOARD_OK;
+    case HOARD_OPT_WAIT_LIMIT_US:
+        if (value < 0) return fail(HOARD_ERR_INVALID, "wait limit %d us", value);
+        h->wait_ticks = 100ll * value;  // the device wall clock runs at 100 MHz
+        return HOARD_OK;
+    case HOARD_OPT_FAIL_UPLOAD:
+        if (value < 0) return fail(HOARD_ERR_INVALID, "fail-upload countdown %d", value);
+        h->fail_upload = value;
+        return HOARD_OK;
     case HOARD_OPT_POOL_NAIVE:
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "pool naive flag %d", value);
         if (value && h->cfg.pool_k > 0) {
@@ -1200,6 +1260,12 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
         return HOARD_OK;
     case HOARD_OPT_DECODE_KERNELS_AVAILABLE:
         *value = (h->xcd_ok ? 1 : 0) | (h->spread_ok ? 2 : 0);
+        return HOARD_OK;
+    case HOARD_OPT_WAIT_LIMIT_US:
+        *value = (int)(h->wait_ticks / 100);
+        return HOARD_OK;
+    case HOARD_OPT_FAIL_UPLOAD:
+        *value = h->fail_upload;
         return HOARD_OK;
     default:
         return fail(HOARD_ERR_INVALID, "unknown option %d", option);

@@ -224,8 +224,22 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
    13.5 us per layer), for callers that own the device: it relies on no other
    work holding compute units while it runs.  Its cross-workgroup waits are
    bounded either way: a workgroup left waiting sets the error flag, the
-   output is NaN and hoard_moe_sync_check reports HOARD_ERR_HIP. */
+   output is NaN and hoard_moe_sync_check reports HOARD_ERR_HIP.
+   The plain launch can be captured into a HIP graph: its sequence tags live
+   in device memory and advance at the end of every launch, replays included.
+   Under capture with the cooperative launch, automatic mode records the
+   per-layer kernels instead and forced mode returns HOARD_ERR_UNSUPPORTED. */
 #define HOARD_OPT_DECODE_LAUNCH 7
+/* HOARD_OPT_WAIT_LIMIT_US: bound of every cross-workgroup wait of the
+   one-launch decode, in microseconds (default 200000).  A wait that runs past
+   it gives up as described above; 0 makes the first wait that is not met at
+   once give up, which forces that failure path from the host. */
+#define HOARD_OPT_WAIT_LIMIT_US 8
+/* HOARD_OPT_FAIL_UPLOAD: test hook of the slot pool.  n > 0 makes the n-th
+   slot upload from now fail before it is issued, as a refused hipMemcpyAsync
+   would: the pool call returns HOARD_ERR_HIP and the layer's slot residency is
+   forgotten (its next call uploads every selected expert again).  0 = off. */
+#define HOARD_OPT_FAIL_UPLOAD 9
 int hoard_moe_set_option(hoard_moe *h, int option, int value);
 int hoard_moe_get_option(hoard_moe *h, int option, int *value);
 

@@ -180,3 +180,26 @@ def test_verify_step_over_the_slot_pool(orc):
         lib.hoard_slot_lru_destroy(rp)
         st.close()
         ref.close()
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (2, 1)])
+def test_batched_few_experts(orc, E, k):
+    """Fewer experts than twice the 8 Q8_K blocks of a 2048-wide fx: the route
+    launch is narrower than the block count, and every block must still be
+    quantised (each token against the oracle and the single-token path)."""
+    from hoard_amd.runtime import MoEStage
+    shape = W.Shape(f"e{E}", 5, 2048, E, k, 768, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1)
+    hl = W.make_layer(shape, 6, 0)
+    st = MoEStage(shape, n_layer=1, layers={0: hl}, max_tokens=16)
+    try:
+        fx, res = _tokens(shape, 5, 40)
+        print(f"batched with {E} experts, top-{k}", flush=True)
+        out, sel, _ = st.forward_batched(0, fx, res)
+        ref, sel_o, _ = orc.moe_layer_batched(hl, fx, res)
+        assert np.array_equal(sel, sel_o)
+        for t in range(5):
+            o1, _, _ = st.layer(0, fx[t], res[t])
+            assert np.array_equal(o1.view(np.uint32), out[t].view(np.uint32)), f"token {t}"
+            parity.assert_parity(out[t], ref[t], f"E={E} token {t}")
+    finally:
+        st.close()

@@ -158,3 +158,78 @@ def test_batched_forward_captured(orc, stage):
         sel.fill_(-1)
 
     _replays_match(g, reset, [out, sel, w], eager, "batched forward")
+
+
+@pytest.mark.parametrize("kernel", [1, 2], ids=["xcd", "spread"])
+def test_one_launch_decode_plain_launch_captured(orc, kernel):
+    """The one-launch decode as a plain launch under capture: its sequence tags
+    live in device memory, so every replay (with eager decodes on the same handle
+    in between, which move the same tags) gives the eager bits.  Under capture
+    with the cooperative launch, automatic mode records the per-layer kernels and
+    forced mode refuses before launching anything."""
+    from hoard_amd.runtime import MoEStage
+    shape = W.QWEN3_30B
+    nl = 4
+    layers = {l: W.make_layer(shape, 12, l) for l in range(nl)}
+    st = MoEStage(shape, n_layer=nl, layers=layers)
+    try:
+        st.set_option(H.OPT_DECODE_KERNEL, kernel)
+        st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+        st.set_option(H.OPT_DECODE_LAUNCH, 1)
+        _, x = W.make_hidden(shape, 12, 0, 0)
+        x0 = st.dev(x)
+        xd = x0.clone()
+        other = st.dev(W.make_hidden(shape, 12, 0, 1)[1])
+        s = torch.cuda.Stream()
+
+        def decode(buf):
+            return st.lib.hoard_moe_decode(st.h, 0, nl, st.ptr(buf), ctypes.c_float(W.RMS_EPS),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+        print(f"graph: eager one-launch decode, kernel {kernel}", flush=True)
+        with torch.cuda.stream(s):
+            H.check(decode(xd))
+        torch.cuda.synchronize()
+        st.sync_check()
+        eager = xd.clone()
+        ref = x
+        for l in range(nl):
+            ref, _, _ = orc.moe_layer(layers[l], orc.rms_norm(ref, W.RMS_EPS), ref)
+        parity.assert_parity(eager.cpu().numpy(), ref, "one-launch decode")
+        print("graph: capture and replay the plain launch", flush=True)
+        xd.copy_(x0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            H.check(decode(xd))
+        torch.cuda.synchronize()
+
+        def reset():
+            xd.copy_(x0)
+            o = other.clone()
+            H.check(decode(o))  # an eager launch between replays moves the device tags too
+
+        _replays_match(g, reset, [xd], [eager], "plain one-launch decode")
+        st.sync_check()
+        # cooperative launch under capture: auto mode records the per-layer kernels
+        st.set_option(H.OPT_DECODE_LAUNCH, 0)
+        st.set_option(H.OPT_PERSISTENT_DECODE, 1)
+        print("graph: cooperative launch under capture, auto mode", flush=True)
+        xd.copy_(x0)
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2, stream=s):
+            H.check(decode(xd))
+        torch.cuda.synchronize()
+        xd.copy_(x0)
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        parity.assert_parity(xd.cpu().numpy(), ref, "per-layer kernels recorded in place of the cooperative launch")
+        st.set_option(H.OPT_PERSISTENT_DECODE, 2)
+        g3 = torch.cuda.CUDAGraph()
+        rc = None
+        with torch.cuda.graph(g3, stream=s):
+            rc = decode(xd)
+        torch.cuda.synchronize()
+        assert rc == H.ERR_UNSUPPORTED
+    finally:
+        st.close()
