@@ -75,8 +75,9 @@ def parse():
     ap.add_argument("--readers", type=int, default=8, help="storage tier: reads in flight")
     ap.add_argument("--store-dir", default="/tmp", help="storage tier: directory for the model file")
     ap.add_argument("--batch", type=int, default=0, metavar="M",
-                    help="batched workload: M tokens per step (4, 8 or 16), routed independently, "
-                         "grouped by expert on int8 MFMA")
+                    help="batched workload: M tokens per step (1..512), routed independently, grouped by expert; "
+                         "up to 16 the verify-sized kernels, above that the prefill-sized sorted-pair units, "
+                         "all on int8 MFMA")
     ap.add_argument("--batch-same", action="store_true",
                     help="with --batch: the M tokens of a step share one hidden, so every expert group holds "
                          "M tokens and runs on MFMA (the skewed end of the verify workload)")
@@ -415,7 +416,10 @@ def run_batched(args, shape, n_layer):
     gbps = bat_bytes / bat_us / 1e3
     macs_per_pair = 3 * shape.n_ff * shape.n_embd
     int8_ops = 2 * macs_per_pair * int(hist.sum())
-    mfma_ops = 2 * macs_per_pair * int(hist[hist >= MFMA_MIN_TOKENS].sum())
+    # verify-sized batches run groups of MFMA_MIN_TOKENS or more on MFMA; prefill-sized
+    # ones (more than 16 tokens) run every group on MFMA
+    mfma_groups = hist >= (MFMA_MIN_TOKENS if M <= 16 else 1)
+    mfma_ops = 2 * macs_per_pair * int(hist[mfma_groups].sum())
     result = {
         "metric": f"batched MoE-layer us per step of {M} tokens + HBM GB/s, Qwen3-30B-A3B-shape Q4_K",
         "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -423,7 +427,9 @@ def run_batched(args, shape, n_layer):
         "dtype": "q4_K/q6_K weights x q8_K activations (int8 dot / MFMA), f32 router/accumulate",
         "data": "synthetic weights and N(0,1) hiddens, every token routed independently",
         "config": {"workload": f"{shape.name}: {n_layer} layers, {M} tokens per step, all experts resident",
-                   "tokens_per_step": M, "layers": n_layer},
+                   "tokens_per_step": M, "layers": n_layer,
+                   "path": "verify-sized: expert groups of 16 token places" if M <= 16 else
+                           "prefill-sized: pairs sorted by expert, 64-pair units on MFMA"},
         "tokens_per_s": round(M * 1000.0 / ms, 2),
         "unique_experts_per_layer": round(float(uniq.mean()), 2),
         "tokens_per_expert_max": int(hist.max()),
@@ -435,8 +441,8 @@ def run_batched(args, shape, n_layer):
                      "traffic": None, "avg_us": round(bat_us, 3)},
         # expert groups of 12 or more tokens run on int8 MFMA, smaller ones on
         # the per-token int8 dot (MFMA_MIN_TOKENS in the batched kernels)
-        "expert_groups": {"per_token_dot": int(((hist > 0) & (hist < MFMA_MIN_TOKENS)).sum()),
-                          "mfma": int((hist >= MFMA_MIN_TOKENS).sum())},
+        "expert_groups": {"per_token_dot": int(((hist > 0) & ~mfma_groups).sum()),
+                          "mfma": int(((hist > 0) & mfma_groups).sum())},
         # int8 operations of the expert products (2 per multiply-add: gate, up and
         # down of every (token, expert) pair), the MFMA share of them, and that
         # share's rate against MI355X's dense int8 peak of 5.0 POP/s

@@ -6,19 +6,12 @@
 // (src/run_specloop.cpp:126-139; all-resident form src/run_m1.cpp:97-108)
 // followed by the weighted sum over the selected experts.
 //
-// Exactness: each v_mfma_i32_16x16x32_i8 covers one 32-element Q4_K
-// sub-block (or, with half of A zeroed, one 16-element Q6_K group) of 16 rows
-// against 16 tokens' Q8_K quants, so it yields exactly the integer sub-block
-// sums the per-token path forms with dot4.  The sub-block scales, the min
-// term and the fp32 block terms are then applied per (row, token) in the
-// per-token path's order, so each token's output is bit-identical to a
-// single-token call.
-//
-// MFMA lane layout (K = 32): lane l supplies A[l % 16][8 (l / 16) .. +7]
-// (8 int8 of row l % 16) and B[8 (l / 16) .. +7][l % 16] (8 int8 of token
-// column l % 16), and receives D[4 (l / 16) + i][l % 16], i = 0..3.
+// The MFMA tiles and why they give the per-token path's bits are in mfma.h.
+// Batches of more than 16 tokens take the sorted-pair path of prefill.hip after
+// the routing and grouping here.
 #include "kernels.h"
 #include "lds_dma.h"
+#include "mfma.h"
 #include "qblocks.h"
 #include "rowdot.h"
 #include "router_tail.h"
@@ -26,8 +19,6 @@
 namespace hoard {
 
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;                   // weight rows per MFMA tile
 constexpr int kMaxTok = kBatchedMaxTokens;  // token columns per MFMA tile
@@ -37,185 +28,6 @@ constexpr int kMaxExperts = 1024;
 static_assert(sizeof(Q8L) == kQ8LBytes, "Q8_K block size shared with the host");
 
 __device__ __forceinline__ Q8L *q8(uint8_t *p) { return reinterpret_cast<Q8L *>(p); }
-
-__device__ __forceinline__ v4i mfma_16x16x32(long a, long b) {
-    const v4i z = {0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
-}
-
-__device__ __forceinline__ long lo_nibbles(uint2 w) {
-    return (long)(((unsigned long)(w.y & 0x0f0f0f0fu) << 32) | (w.x & 0x0f0f0f0fu));
-}
-__device__ __forceinline__ long hi_nibbles(uint2 w) {
-    return (long)(((unsigned long)((w.y >> 4) & 0x0f0f0f0fu) << 32) | ((w.x >> 4) & 0x0f0f0f0fu));
-}
-
-// Operands of one super-block for one lane: its row's quants for the four
-// 64-element chunks, the headers of the four rows whose results it receives,
-// and its token's Q8_K quants, 16-element sums and scale.
-struct Q4Ops {
-    uint2 qa[4];
-    uint4 hd[4];
-    long xb[8];
-    uint4 b0, b1;
-    float xd;
-};
-
-// Rows of a tile of fewer than 16 rows repeat (row index & RM); the repeated
-// rows' results are not used.
-template <int RM>
-__device__ __forceinline__ void q4_load(const uint8_t *W, size_t rb, const Q8L *xq, int b, Q4Ops &o) {
-    const int lane = threadIdx.x & 63, r = lane & 15 & RM, q = lane >> 4;
-    const uint8_t *blk_r = W + (size_t)r * rb + (size_t)b * kQ4KBytes;
-#pragma unroll
-    for (int jc = 0; jc < 4; ++jc) o.qa[jc] = *reinterpret_cast<const uint2 *>(blk_r + 16 + 32 * jc + 8 * q);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        o.hd[i] = *reinterpret_cast<const uint4 *>(W + (size_t)((4 * q + i) & RM) * rb + (size_t)b * kQ4KBytes);
-    const Q8L &x = xq[b];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) o.xb[s] = *reinterpret_cast<const long *>(&x.qs[8 * s + 2 * q]);
-    o.b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
-    o.b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
-    o.xd = x.d;
-}
-
-// The 6-bit scales (sc) and mins (mn) of a Q4_K header, four per word: byte
-// s of sc[0] / mn[0] belongs to sub-block s, byte s of sc[1] / mn[1] to s + 4.
-__device__ __forceinline__ void q4k_scales_packed(const uint4 &hd, uint32_t sc[2], uint32_t mn[2]) {
-    sc[0] = hd.y & 0x3f3f3f3fu;
-    mn[0] = hd.z & 0x3f3f3f3fu;
-    sc[1] = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
-    mn[1] = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
-}
-
-__device__ __forceinline__ int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
-
-__device__ __forceinline__ void q4_compute(const Q4Ops &o, float acc[4], float accm[4]) {
-    const uint32_t bw[8] = {o.b0.x, o.b0.y, o.b0.z, o.b0.w, o.b1.x, o.b1.y, o.b1.z, o.b1.w};
-    int bs[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) bs[s] = (int)(int16_t)(bw[s] & 0xffffu) + (int)(int16_t)(bw[s] >> 16);
-    uint32_t sc[4][2], mn[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) q4k_scales_packed(o.hd[i], sc[i], mn[i]);
-    int isum[4] = {0, 0, 0, 0}, msum[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const long a = (s & 1) ? hi_nibbles(o.qa[s >> 1]) : lo_nibbles(o.qa[s >> 1]);
-        const v4i d = mfma_16x16x32(a, o.xb[s]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            isum[i] += byte_of(sc[i][s >> 2], s & 3) * d[i];
-            msum[i] += byte_of(mn[i][s >> 2], s & 3) * bs[s];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float dd = half_bits_to_float(o.hd[i].x & 0xffffu) * o.xd;
-        const float dm = half_bits_to_float(o.hd[i].x >> 16) * o.xd;
-        acc[i] = acc[i] + dd * (float)isum[i];
-        accm[i] = accm[i] + dm * (float)msum[i];
-    }
-}
-
-// One 16-row Q4_K tile (row r at W + r*rb, NBLK super-blocks; with RM = 7 an
-// 8-row tile, rows 8-15 repeating rows 0-7) against the lane's token column.
-// xq: the token's Q8_K blocks; a column without a token reads another
-// column's token and its results are not used (the MFMA's output columns are
-// independent), which keeps the loads free of divergent branches.  Returns,
-// for rows 4(l/16)+i, acc_i - accm_i as the per-token path forms them.
-template <int NBLK, int RM = 15>
-__device__ __forceinline__ void tile_q4k(const uint8_t *W, size_t rb, const Q8L *xq, float out[4]) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 1
-    for (int b = 0; b < NBLK; ++b) {
-        Q4Ops o;
-        q4_load<RM>(W, rb, xq, b, o);
-        q4_compute(o, acc, accm);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = acc[i] - accm[i];
-}
-
-// 8 bytes at a 2-byte aligned LDS address.
-__device__ __forceinline__ uint2 lds_u64_a2(const uint8_t *p) {
-    // aligned base by pointer arithmetic, so that the compiler still sees an
-    // LDS pointer and emits ds_read rather than flat loads
-    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-    return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
-}
-
-// A token's Q8_K operands of one super-block for one lane (see q4_load).
-struct Q6X {
-    long xb[8];
-    uint4 b0, b1;
-    float xd;
-};
-
-__device__ __forceinline__ void q6_load_x(const Q8L *xq, int b, Q6X &o) {
-    const int q = (threadIdx.x & 63) >> 4;
-    const Q8L &x = xq[b];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) o.xb[s] = *reinterpret_cast<const long *>(&x.qs[8 * s + 2 * q]);
-    o.b0 = *reinterpret_cast<const uint4 *>(&x.bsums[0]);
-    o.b1 = *reinterpret_cast<const uint4 *>(&x.bsums[8]);
-    o.xd = x.d;
-}
-
-// One 16-row Q6_K tile staged in LDS (row r at T + r*rb).  Element e of a
-// super-block: half n = e/128, quarter qd = (e/32)%4, l = e%32; its 6-bit
-// value is the (qd/2)-th nibble of ql[64n + 32(qd%2) + l] with bits
-// 2qd..2qd+1 of qh[32n + l] on top, minus 32.  The -32 is applied through the
-// token's 16-element sums (bsums), as the per-token path's zero-point term.
-template <int NBLK>
-__device__ __forceinline__ void tile_q6k(const uint8_t *T, size_t rb, const Q8L *xq, float out[4]) {
-    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
-    const bool first_half = q < 2;  // elements 0..15 of each 32-element range
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 1
-    for (int b = 0; b < NBLK; ++b) {
-        Q6X cur;
-        q6_load_x(xq, b, cur);
-        const uint8_t *blk_r = T + (size_t)r * rb + (size_t)b * kQ6KBytes;
-        const uint32_t w[8] = {cur.b0.x, cur.b0.y, cur.b0.z, cur.b0.w, cur.b1.x, cur.b1.y, cur.b1.z, cur.b1.w};
-        int bs[16];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            bs[2 * g] = (int)(int16_t)(w[g] & 0xffffu);
-            bs[2 * g + 1] = (int)(int16_t)(w[g] >> 16);
-        }
-        int isum[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {  // 32-element range s: groups 2s and 2s+1
-            const int n = s >> 2, qd = s & 3;
-            const uint2 ql = lds_u64_a2(blk_r + 64 * n + 32 * (qd & 1) + 8 * q);
-            const uint2 qh = lds_u64_a2(blk_r + 128 + 32 * n + 8 * q);
-            const int nsh = 4 * (qd >> 1), hsh = 2 * qd;
-            const uint32_t v0 = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
-            const uint32_t v1 = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
-            const long a = (long)(((unsigned long)v1 << 32) | v0);
-            const v4i d0 = mfma_16x16x32(first_half ? a : 0, cur.xb[s]);
-            const v4i d1 = mfma_16x16x32(first_half ? 0 : a, cur.xb[s]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint8_t *blk_i = T + (size_t)(4 * q + i) * rb + (size_t)b * kQ6KBytes;
-                const int sc0 = (int)(int8_t)blk_i[192 + 2 * s], sc1 = (int)(int8_t)blk_i[193 + 2 * s];
-                isum[i] += sc0 * (d0[i] - 32 * bs[2 * s]) + sc1 * (d1[i] - 32 * bs[2 * s + 1]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint8_t *blk_i = T + (size_t)(4 * q + i) * rb + (size_t)b * kQ6KBytes;
-            const uint32_t dbits = (uint32_t)blk_i[208] | ((uint32_t)blk_i[209] << 8);
-            acc[i] = acc[i] + (half_bits_to_float(dbits) * cur.xd) * (float)isum[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = acc[i];
-}
 
 // -- route: router logits, softmax / top-k, Q8_K of fx, grouping by expert ----
 // One launch replaces the router kernels and the grouping pass.  A workgroup
@@ -241,10 +53,21 @@ __device__ __forceinline__ bool pair_computed(const BatchedArgs &a, const int *y
     return !ysrc || (ysrc[p] == p % a.k && !bad[p / a.k]);
 }
 
-__device__ void group_by_expert(const BatchedArgs &a, const int *ysrc = nullptr, const int *bad = nullptr) {
-    __shared__ unsigned mask[kMaxExperts];
-    __shared__ int uidx[kMaxExperts];
-    __shared__ int wave_total;
+// LDS of the grouping passes; the route kernel lays it over its staging
+// buffers, which are free by then.
+struct GroupLds {
+    unsigned mask[kMaxExperts];  // tokens (of a chunk) selecting each expert
+    int uidx[kMaxExperts];       // group of each expert
+    unsigned cnt[kMaxExperts];   // pairs per expert
+    int base[kMaxExperts];       // next sorted position of each expert
+    int total;
+};
+
+__device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ysrc = nullptr,
+                                const int *bad = nullptr) {
+    unsigned *mask = g.mask;
+    int *uidx = g.uidx;
+    int &wave_total = g.total;
     const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k;
     for (int e = tid; e < E; e += nt) mask[e] = 0u;
     __syncthreads();
@@ -290,6 +113,87 @@ __device__ void group_by_expert(const BatchedArgs &a, const int *ysrc = nullptr,
         a.uslot[g * kMaxTok + c] = j;
     }
     if (tid == 0) a.n_unique[0] = wave_total;
+}
+
+// Grouping of a prefill-sized batch (all threads of one workgroup): the
+// computed (token, slot) pairs sorted by (expert, token) into ptok / pslot, the
+// groups (used experts in ascending order: uexp, ucount, goff) and the work
+// units (at most kUnitTokens pairs of one group each).  pe[p] (in LDS) is the
+// expert of pair p, or -1 for a pair that joins no group.  The order within an
+// expert comes from chunks of at most 32 tokens taken in token order: a pair's
+// place is its expert's running base plus the tokens of its chunk before it
+// that select the same expert (a token joins a group at most once).
+__device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
+    for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
+    __syncthreads();
+    for (int p = tid; p < P; p += nt)
+        if (pe[p] >= 0) atomicAdd(&g.cnt[pe[p]], 1u);
+    __syncthreads();
+    if (tid < 64) {
+        // groups and units in ascending expert order: lane owns a contiguous run of experts
+        const int lane = tid, per = (E + 63) / 64, e0 = lane * per;
+        int cg = 0, cu = 0, cp = 0;
+        for (int e = e0; e < e0 + per && e < E; ++e) {
+            const int c = (int)g.cnt[e];
+            cg += c ? 1 : 0;
+            cu += (c + kUnitTokens - 1) / kUnitTokens;
+            cp += c;
+        }
+        int ig = cg, iu = cu, ip = cp;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int og = __shfl_up(ig, off), ou = __shfl_up(iu, off), op = __shfl_up(ip, off);
+            if (lane >= off) {
+                ig += og;
+                iu += ou;
+                ip += op;
+            }
+        }
+        int gi = ig - cg, ui = iu - cu, pi = ip - cp;
+        for (int e = e0; e < e0 + per && e < E; ++e) {
+            const int c = (int)g.cnt[e];
+            a.hist[e] = (unsigned)c;
+            g.base[e] = pi;
+            if (c) {
+                a.uexp[gi] = e;
+                a.ucount[gi] = c;
+                a.goff[gi] = pi;
+                for (int s0 = 0; s0 < c; s0 += kUnitTokens, ++ui) {
+                    a.units[3 * ui] = gi;
+                    a.units[3 * ui + 1] = s0;
+                    a.units[3 * ui + 2] = min(kUnitTokens, c - s0);
+                }
+                ++gi;
+            }
+            pi += c;
+        }
+        if (lane == 63) {
+            a.n_unique[0] = ig;
+            a.n_units[0] = iu;
+        }
+    }
+    __syncthreads();
+    const int tpc = min(32, max(1, nt / k));  // tokens per chunk: one mask bit each
+    for (int t0 = 0; t0 < a.M; t0 += tpc) {
+        for (int e = tid; e < E; e += nt) g.mask[e] = 0u;
+        __syncthreads();
+        const int pend = min(P, (t0 + tpc) * k);
+        for (int p = t0 * k + tid; p < pend; p += nt)
+            if (pe[p] >= 0) atomicOr(&g.mask[pe[p]], 1u << (p / k - t0));
+        __syncthreads();
+        for (int p = t0 * k + tid; p < pend; p += nt) {
+            const int e = pe[p];
+            if (e < 0) continue;
+            const int t = p / k;
+            const int pos = g.base[e] + __popc(g.mask[e] & ((1u << (t - t0)) - 1u));
+            a.ptok[pos] = t;
+            a.pslot[pos] = p - t * k;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += nt) g.base[e] += __popc(g.mask[e]);
+        __syncthreads();
+    }
 }
 
 __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
@@ -357,9 +261,143 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     }
     __syncthreads();
     if (!last) return;
-    group_by_expert(a);
+    // the staging buffers are free: the grouping's LDS goes over them
+    static_assert(sizeof(GroupLds) <= sizeof(xl), "grouping LDS fits the token staging");
+    GroupLds &g = *reinterpret_cast<GroupLds *>(&xl[0][0]);
+    group_by_expert(a, g);
     if (threadIdx.x == 0)
         __hip_atomic_store(&a.counters[kBatchedCounters - 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// -- prefill-sized routing: tiled router GEMM, then tails, then the grouping -----
+// Logits of 16 experts x 16 tokens per workgroup of 256 threads.  Thread
+// (group q = tid / 32, lane l = tid % 32) holds accumulator l of ggml's x86 f32
+// dot (elements 32 i + l, i ascending) for 4 experts x 8 tokens: the rows and
+// tokens pass through LDS 256 elements at a time, every element read once per
+// 32 dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
+// which fold them in ggml's order, so every logit is the single-token router's.
+constexpr int kTileE = 16, kTileT = 16, kTileK = 256;
+
+__global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
+    __shared__ __align__(16) float wl[kTileE][kTileK];
+    __shared__ __align__(16) float xl[kTileT][kTileK];
+    constexpr int n = kRouteN;
+    const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = tid >> 6, lane = tid & 63;
+    const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
+    const int re = (q & 3) * 4, rt = (q >> 2) * 8;  // this group's 4 experts and 8 tokens within the tile
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+#pragma unroll 1
+    for (int k0 = 0; k0 < n; k0 += kTileK) {
+        // 32 rows of 1 KB: expert rows then token rows, one wave per 8 rows;
+        // rows past the end repeat the last one (their results are not stored)
+        for (int r = wave; r < kTileE + kTileT; r += 4) {
+            const float *src = r < kTileE ? a.router + (size_t)min(e0 + r, a.E - 1) * n
+                                          : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
+            float *dst = r < kTileE ? wl[r] : xl[r - kTileE];
+            dma_chunk(reinterpret_cast<uint8_t *>(dst), reinterpret_cast<const uint8_t *>(src + k0));
+        }
+        lds_dma_wait();
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kTileK / 32; ++i) {
+            float wv[4], xv[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wv[r] = wl[re + r][32 * i + l];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xv[t] = xl[rt + t][32 * i + l];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            float v = acc[r][t];
+            v = v + __shfl_xor(v, 16);  // accumulators l and l + 16
+            v = row16_ggml_fold(v);
+            const int e = e0 + re + r, tok = t0 + rt + t;
+            if (l == 0 && e < a.E && tok < a.M) a.logits[(size_t)tok * a.E + e] = v;
+        }
+    (void)lane;
+}
+
+// One token per workgroup of 512 threads: wave 0 runs the router tail
+// (softmax, top-k, renorm) on the token's logits, and wave b forms Q8_K of
+// block b of its fx.
+// The pair's expert for the grouping: its id clamped into range (an id out of
+// range counts as expert 0), or -1 where an earlier slot of the token holds the
+// same clamped id, so that a token joins a group once.  ids: the token's k ids
+// in lanes 0..k-1 of the calling wave.
+__device__ __forceinline__ int pair_expert(int id, int j, int k, int n_ids) {
+    const int e = (id < 0 || id >= n_ids) ? 0 : id;
+    bool first = true;
+    for (int i = 0; i < k; ++i) {
+        const int o = __shfl(e, i);
+        first = first && !(i < j && o == e);
+    }
+    return first ? e : -1;
+}
+
+// One token per workgroup of 512 threads: wave 0 runs the router tail
+// (softmax, top-k, renorm) on the token's logits and writes the pairs' experts
+// for the grouping; wave b forms Q8_K of block b of its fx.
+__global__ __launch_bounds__(512) void route_tails_kernel(BatchedArgs a) {
+    constexpr int nb = kRouteN / QK;
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 0) {
+        router_tail<false>(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, t);
+        __builtin_amdgcn_s_waitcnt(0);  // the selection is stored: read it back past L1
+        const int id = lane < a.k ? __hip_atomic_load(a.sel + (size_t)t * a.k + lane, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0;
+        const int e = pair_expert(id, lane, a.k, a.n_ids);
+        if (lane < a.k) a.pexp[(size_t)t * a.k + lane] = e;
+    }
+    if (wave < nb) wave_quantize_q8l(a.fx + (size_t)t * kRouteN + wave * QK, q8(a.q8x) + (size_t)t * nb + wave);
+}
+
+// Caller ids of a prefill-sized batch, one token per workgroup of 512 threads:
+// wave b forms Q8_K of block b; wave 0 finds each slot's first occurrence of its
+// id within the token (ysrc) and whether the token has an id out of range
+// (bad), and writes the pairs' experts for the grouping (none for a bad token
+// or a repeated id).
+__global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
+    constexpr int nb = kRouteN / QK;
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, k = a.k;
+    if (wave == 0) {
+        const int id = lane < k ? a.sel[(size_t)t * k + lane] : 0;
+        const bool bad = __any(lane < k && (id < 0 || id >= a.n_ids));
+        int first = lane;
+        for (int i = k - 1; i >= 0; --i) {
+            const int o = __shfl(id, i);
+            if (i < lane && o == id) first = i;
+        }
+        if (lane < k) {
+            a.ysrc[(size_t)t * k + lane] = first;
+            a.pexp[(size_t)t * k + lane] = (bad || first != lane) ? -1 : id;
+        }
+        if (lane == 0) a.bad[t] = bad ? 1 : 0;
+    }
+    if (wave < nb) wave_quantize_q8l(a.fx + (size_t)t * kRouteN + wave * QK, q8(a.q8x) + (size_t)t * nb + wave);
+}
+
+// The grouping of a prefill-sized batch, in one workgroup: the pairs' experts
+// are copied into LDS first, so every pass reads them from there.
+__global__ __launch_bounds__(1024) void group_kernel(BatchedArgs a) {
+    __shared__ GroupLds g;
+    __shared__ int pe[kBatchedMaxTokensLarge * kMaxK];
+    const int P = a.M * a.k;
+    for (int p = threadIdx.x; p < P; p += blockDim.x) pe[p] = a.pexp[p];
+    __syncthreads();
+    group_large(a, g, pe);
 }
 
 // -- caller ids: Q8_K of fx (workgroups 0..M-1, a wave per block) and the
@@ -379,8 +417,9 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
     }
     __shared__ int bad_s[kMaxTok];
     __shared__ int ysrc_s[kMaxTok * kMaxK];
+    __shared__ GroupLds g;
     const int tid = threadIdx.x, P = a.M * a.k;
-    if (tid < kMaxTok) bad_s[tid] = 0;
+    for (int t = tid; t < a.M; t += blockDim.x) bad_s[t] = 0;
     __syncthreads();
     for (int p = tid; p < P; p += blockDim.x) {
         const int t = p / a.k, j = p % a.k;
@@ -393,8 +432,8 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
         a.ysrc[p] = first;  // for the combine launch
     }
     __syncthreads();
-    if (tid < a.M) a.bad[tid] = bad_s[tid];
-    group_by_expert(a, ysrc_s, bad_s);
+    for (int t = tid; t < a.M; t += blockDim.x) a.bad[t] = bad_s[t];
+    group_by_expert(a, g, ysrc_s, bad_s);
 }
 
 // Expert groups are computed two ways.  A group of fewer than kMfmaMinTokens
@@ -613,15 +652,25 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
 }
 
 bool args_ok(const BatchedArgs &a) {
-    return a.M >= 1 && a.M <= kMaxTok && a.n_embd == kRouteN && a.gu_type == kTypeQ4K && a.k <= kMaxK &&
-           a.n_ids >= 1 && a.n_ids <= kMaxExperts && a.E <= kMaxExperts;
+    return a.M >= 1 && a.M <= kBatchedMaxTokensLarge && a.n_embd == kRouteN && a.gu_type == kTypeQ4K &&
+           a.k <= kMaxK && a.n_ids >= 1 && a.n_ids <= kMaxExperts && a.E <= kMaxExperts &&
+           (a.M <= kMaxTok || (a.goff && a.ptok && a.pslot && a.pexp && a.units && a.n_units && a.max_units >= 1));
 }
 
 }  // namespace
 
+// Batches of up to 16 tokens group by expert with 16 token places per group;
+// larger ones sort the pairs and run the prefill units (prefill.hip).
 hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
         return hipErrorInvalidValue;
+    if (a.M > kMaxTok) {
+        hipLaunchKernelGGL(route_gemm_kernel, dim3((a.E + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT),
+                           dim3(256), 0, s, a);
+        hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(512), 0, s, a);
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
+        return launch_prefill_groups(a, s);
+    }
     hipLaunchKernelGGL(route_kernel, dim3((a.E + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
                        dim3(256), 0, s, a);
     return launch_groups(a, s);
@@ -629,6 +678,11 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
 
 hipError_t launch_batched_ids(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || !a.ysrc || !a.bad) return hipErrorInvalidValue;
+    if (a.M > kMaxTok) {
+        hipLaunchKernelGGL(prep_ids_large_kernel, dim3(a.M), dim3(512), 0, s, a);
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
+        return launch_prefill_groups(a, s);
+    }
     hipLaunchKernelGGL(prep_ids_kernel, dim3((unsigned)a.M + 1), dim3(512), 0, s, a);
     return launch_groups(a, s);
 }

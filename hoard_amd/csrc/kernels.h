@@ -92,14 +92,32 @@ struct BatchedArgs {
     int *ysrc;              // [M][k] caller ids only: the slot j' <= j whose output pair (t, j) takes
                             // (its first occurrence of the same id), else null
     int *bad;               // [M] caller ids only: 1 for a token with an id outside [0, n_ids), else null
+    // prefill-sized batches (M > kBatchedMaxTokens): the pairs sorted by (expert, token)
+    // and cut into work units of at most kUnitTokens pairs of one expert
+    int *goff;              // [umax] first sorted position of each group
+    int *ptok, *pslot;      // [M*k] token and slot of each sorted pair
+    int *pexp;              // [M*k] expert of each pair for the grouping, -1 for one that joins none
+    int *units;             // [max_units][3] group, first pair within the group, pairs
+    int *n_units;           // [1]
+    int max_units;
 };
-constexpr int kBatchedMaxTokens = 16;
-constexpr int kBatchedCounters = 8;
+constexpr int kBatchedMaxTokens = 16;         // the verify-sized path: per-token dots or MFMA per group
+constexpr int kBatchedMaxTokensLarge = 512;   // the prefill-sized path: sorted pairs, MFMA units
+constexpr int kUnitTokens = 64;               // pairs of one expert per prefill work unit
+constexpr int kBatchedCounters = 160;         // route completion counters: one per 4 tokens, and the tails'
 constexpr size_t kQ8LBytes = 304;
 hipError_t launch_batched(const BatchedArgs &a, hipStream_t s);
 // The same expert products and combine for the caller's ids (a.sel) and weights (a.wsel).
 hipError_t launch_batched_ids(const BatchedArgs &a, hipStream_t s);
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
+// The expert products and combine of a prefill-sized batch after its grouping
+// (prefill.hip): gate/up + SwiGLU, Q8_K(h), down, ordered combine.
+hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s);
+// Upper bound of the prefill work units for M*k pairs over n_ids groups.
+inline int prefill_max_units(int M, int k, int n_ids) {
+    const int P = M * k, umax = n_ids < P ? n_ids : P;
+    return umax + (P + kUnitTokens - 1) / kUnitTokens;
+}
 
 // Persistent stacked decode (one cooperative launch per token).
 struct DecodeLayer {

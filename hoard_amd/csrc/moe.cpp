@@ -130,9 +130,10 @@ struct hoard_moe {
     // batched path (allocated on first use)
     uint8_t *b_q8x = nullptr, *b_q8h = nullptr;
     float *b_h = nullptr, *b_y = nullptr;
-    int *b_ints = nullptr;          // n_unique, slot_of[E], uexp, ucount, utok, uslot
+    int *b_ints = nullptr;          // group count, then the arrays of batched_layout
     unsigned *b_hist = nullptr;     // [E]
     unsigned *b_counters = nullptr; // route kernel's completion counters
+    int *b_layout_ysrc = nullptr, *b_layout_bad = nullptr;  // caller-id arrays within b_ints
     bool hist_pending = false;      // a batched call ran since the histogram was last read
     size_t trace_layers = 0;
     bool tracing = false;
@@ -1023,18 +1024,92 @@ int hoard_moe_attach_store(hoard_moe *h, hoard_store *st) {
 
 namespace {
 
-// Checks and buffers common to the batched entry points, and their arguments
-// but the selection: the shapes and types the kernels are built for, 16-byte
-// aligned fx and weights, and the scratch allocated on first use.
-int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev, float *out_dev,
-                  bool pooled_ok, hoard::BatchedArgs *out) {
+// Scratch of the batched entry points for batches of up to T tokens: the
+// byte size of every buffer and the layout of the int arrays.  The verify-sized
+// path (M <= 16) keeps 16 token places per expert group; the prefill-sized one
+// keeps the pairs sorted by expert.
+struct BatchedLayout {
+    int T, Ts, umax, umax_s, max_units;
+    size_t q8x, q8h, hbuf, ybuf, n_ints, hist, counters;  // bytes (n_ints: ints)
+    size_t o_slot_of, o_uexp, o_ucount, o_utok, o_uslot, o_ysrc, o_bad, o_goff, o_ptok, o_pslot, o_pexp, o_units,
+        o_nunits;
+};
+
+BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
+    BatchedLayout L{};
+    const int k = c.n_used, E = c.n_expert;  // the slots of a pool never outnumber the experts
+    const int nb = c.n_embd / 256, nbh = c.n_ff / 256;
+    L.T = T;
+    L.Ts = std::min(T, hoard::kBatchedMaxTokens);
+    L.umax_s = std::min(E, L.Ts * k);
+    L.umax = std::min(E, T * k);
+    L.max_units = hoard::prefill_max_units(T, k, E);
+    const size_t pairs_s = (size_t)L.umax_s * hoard::kBatchedMaxTokens, pairs = (size_t)T * k;
+    L.q8x = (size_t)T * nb * hoard::kQ8LBytes;
+    L.q8h = std::max(pairs_s, pairs) * nbh * hoard::kQ8LBytes;
+    L.hbuf = std::max(pairs_s, pairs) * c.n_ff * sizeof(float);
+    L.ybuf = pairs * c.n_embd * sizeof(float);
+    size_t o = 1;  // [0]: the group count
+    auto take = [&](size_t n) {
+        const size_t r = o;
+        o += n;
+        return r;
+    };
+    L.o_slot_of = take(E);
+    L.o_uexp = take(L.umax);
+    L.o_ucount = take(L.umax);
+    L.o_utok = take(pairs_s);
+    L.o_uslot = take(pairs_s);
+    L.o_ysrc = take(pairs);
+    L.o_bad = take(T);
+    L.o_goff = take(L.umax);
+    L.o_ptok = take(pairs);
+    L.o_pslot = take(pairs);
+    L.o_pexp = take(pairs);
+    L.o_units = take((size_t)3 * L.max_units);
+    L.o_nunits = take(1);
+    L.n_ints = o;
+    L.hist = sizeof(unsigned) * E;
+    L.counters = sizeof(unsigned) * hoard::kBatchedCounters;
+    return L;
+}
+
+// Points the args' scratch at buffers laid out by L: q8x, q8h, hbuf, ybuf and
+// the int arrays, histogram and counters.
+void bind_batched(hoard::BatchedArgs &a, const BatchedLayout &L, uint8_t *q8x, uint8_t *q8h, float *hbuf, float *ybuf,
+                  int *ints, unsigned *hist, unsigned *counters) {
+    a.q8x = q8x;
+    a.q8h = q8h;
+    a.hbuf = hbuf;
+    a.ybuf = ybuf;
+    a.n_unique = ints;
+    a.slot_of = ints + L.o_slot_of;
+    a.uexp = ints + L.o_uexp;
+    a.ucount = ints + L.o_ucount;
+    a.utok = ints + L.o_utok;
+    a.uslot = ints + L.o_uslot;
+    a.goff = ints + L.o_goff;
+    a.ptok = ints + L.o_ptok;
+    a.pslot = ints + L.o_pslot;
+    a.pexp = ints + L.o_pexp;
+    a.units = ints + L.o_units;
+    a.n_units = ints + L.o_nunits;
+    a.max_units = hoard::prefill_max_units(a.M, a.k, a.n_ids);
+    a.hist = hist;
+    a.counters = counters;
+}
+
+// Checks common to the batched entry points, and their arguments but the
+// selection and the scratch: the shapes and types the kernels are built for,
+// 16-byte aligned fx and weights.
+int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev, float *out_dev,
+                  bool pooled_ok, int max_m, hoard::BatchedArgs *out) {
     int rc = check_layer(h, layer);
     if (rc) return rc;
     const hoard_moe_cfg &c = h->cfg;
     if (!fx_dev || !res_dev || !out_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
-    if (M < 1 || M > c.max_tokens || M > hoard::kBatchedMaxTokens)
-        return fail(HOARD_ERR_INVALID, "M %d outside 1..min(max_tokens %d, %d)", M, c.max_tokens,
-                    hoard::kBatchedMaxTokens);
+    if (M < 1 || M > c.max_tokens || M > max_m)
+        return fail(HOARD_ERR_INVALID, "M %d outside 1..min(max_tokens %d, %d)", M, c.max_tokens, max_m);
     if (c.pool_k > 0 && !pooled_ok)
         return fail(HOARD_ERR_UNSUPPORTED, "batched routing needs every expert resident (pool_k 0)");
     if (c.n_ff_shexp > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path has no shared expert");
@@ -1047,25 +1122,6 @@ int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     if (((uintptr_t)L.gate | (uintptr_t)L.up | (uintptr_t)L.down | (uintptr_t)L.gstride | (uintptr_t)L.ustride |
          (uintptr_t)L.dstride) & 15)
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: expert matrices must be 16-byte aligned");
-    const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
-    const int umax = std::min(c.n_expert, T * c.n_used);  // pool_k <= n_expert: slots never exceed it
-    const int nb = c.n_embd / 256, nbh = c.n_ff / 256;
-    if (!h->b_q8x) {
-        rc = rc ? rc : dev_alloc((void **)&h->b_q8x, (size_t)T * nb * hoard::kQ8LBytes);
-        rc = rc ? rc : dev_alloc((void **)&h->b_q8h, (size_t)umax * hoard::kBatchedMaxTokens * nbh * hoard::kQ8LBytes);
-        rc = rc ? rc : dev_alloc((void **)&h->b_h, (size_t)umax * hoard::kBatchedMaxTokens * c.n_ff * sizeof(float));
-        rc = rc ? rc : dev_alloc((void **)&h->b_y, (size_t)T * c.n_used * c.n_embd * sizeof(float));
-        rc = rc ? rc : dev_alloc((void **)&h->b_ints,
-                                 sizeof(int) * (1 + c.n_expert + 2 * umax + 2 * umax * hoard::kBatchedMaxTokens +
-                                                T * c.n_used + T));
-        rc = rc ? rc : dev_alloc((void **)&h->b_hist, sizeof(unsigned) * c.n_expert);
-        rc = rc ? rc : dev_alloc((void **)&h->b_counters, sizeof(unsigned) * hoard::kBatchedCounters);
-        if (rc) return rc;
-        HIP_TRY(hipMemset(h->b_counters, 0, sizeof(unsigned) * hoard::kBatchedCounters));
-        // the counters must read zero before the first launch, which may go to a
-        // non-blocking stream that does not wait for work on the null stream
-        HIP_TRY(hipDeviceSynchronize());
-    }
     hoard::BatchedArgs a{};
     a.M = M;
     a.n_embd = c.n_embd;
@@ -1081,26 +1137,43 @@ int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     a.router = L.router;
     a.renorm = c.renorm;
     a.logits = h->logits;
-    a.counters = h->b_counters;
     a.gate = L.gate;
     a.up = L.up;
     a.down = L.down;
     a.gstride = L.gstride;
     a.ustride = L.ustride;
     a.dstride = L.dstride;
-    a.q8x = h->b_q8x;
-    a.q8h = h->b_q8h;
-    a.hbuf = h->b_h;
-    a.ybuf = h->b_y;
-    int *ip = h->b_ints;
-    a.n_unique = ip;
-    a.slot_of = ip + 1;
-    a.uexp = a.slot_of + c.n_expert;
-    a.ucount = a.uexp + umax;
-    a.utok = a.ucount + umax;
-    a.uslot = a.utok + umax * hoard::kBatchedMaxTokens;
-    a.hist = h->b_hist;
     *out = a;
+    return HOARD_OK;
+}
+
+// batched_check, and the handle's scratch, allocated on first use for
+// max_tokens (at most kBatchedMaxTokensLarge) tokens.
+int batched_setup(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev, float *out_dev,
+                  bool pooled_ok, hoard::BatchedArgs *out) {
+    if (int rc = batched_check(h, layer, M, fx_dev, res_dev, out_dev, pooled_ok, hoard::kBatchedMaxTokensLarge, out))
+        return rc;
+    const hoard_moe_cfg &c = h->cfg;
+    const BatchedLayout L = batched_layout(c, std::min(c.max_tokens, hoard::kBatchedMaxTokensLarge));
+    if (!h->b_q8x) {
+        int rc = 0;
+        rc = rc ? rc : dev_alloc((void **)&h->b_q8x, L.q8x);
+        rc = rc ? rc : dev_alloc((void **)&h->b_q8h, L.q8h);
+        rc = rc ? rc : dev_alloc((void **)&h->b_h, L.hbuf);
+        rc = rc ? rc : dev_alloc((void **)&h->b_y, L.ybuf);
+        rc = rc ? rc : dev_alloc((void **)&h->b_ints, sizeof(int) * L.n_ints);
+        rc = rc ? rc : dev_alloc((void **)&h->b_hist, L.hist);
+        rc = rc ? rc : dev_alloc((void **)&h->b_counters, L.counters);
+        if (rc) return rc;
+        HIP_TRY(hipMemset(h->b_counters, 0, L.counters));
+        // the counters must read zero before the first launch, which may go to a
+        // non-blocking stream that does not wait for work on the null stream
+        HIP_TRY(hipDeviceSynchronize());
+    }
+    bind_batched(*out, L, h->b_q8x, h->b_q8h, h->b_h, h->b_y, h->b_ints, h->b_hist, h->b_counters);
+    out->ysrc = out->bad = nullptr;
+    h->b_layout_ysrc = h->b_ints + L.o_ysrc;
+    h->b_layout_bad = h->b_ints + L.o_bad;
     return HOARD_OK;
 }
 
@@ -1131,13 +1204,11 @@ int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *f
     if (!ids_dev || !w_dev) return fail(HOARD_ERR_INVALID, "null device pointer");
     hoard::BatchedArgs a;
     if (int rc = batched_setup(h, layer, M, fx_dev, res_dev, out_dev, true, &a)) return rc;
-    const hoard_moe_cfg &c = h->cfg;
-    const int T = std::min(c.max_tokens, hoard::kBatchedMaxTokens);
     hipStream_t s = (hipStream_t)stream;
     a.sel = const_cast<int32_t *>(ids_dev);
     a.wsel = const_cast<float *>(w_dev);
-    a.ysrc = a.uslot + std::min(c.n_expert, T * c.n_used) * hoard::kBatchedMaxTokens;
-    a.bad = a.ysrc + T * c.n_used;
+    a.ysrc = h->b_layout_ysrc;
+    a.bad = h->b_layout_bad;
     hipError_t e;
     {
         KernelMark mark(h, HOARD_KERNEL_BATCHED, s);

@@ -1,0 +1,341 @@
+// Expert products of a prefill-sized batch (more than 16 tokens): the
+// counterpart of ggml_mul_mat_id over all T prompt tokens
+// (src/run_m1.cpp:93-108) and of the verify step's mul_mat_id with per-token
+// ids (src/run_specloop.cpp:126-139), followed by the weighted sum over the
+// selected experts.
+//
+// batched.hip routes the tokens (or takes the caller's ids), forms Q8_K(fx)
+// and sorts the (token, slot) pairs by (expert, token) into work units of at
+// most kUnitTokens pairs of one expert.  Here, per unit:
+//   gate/up  32 rows of gate and of up per workgroup (16 rows of one matrix per
+//            wave) against the unit's tokens on v_mfma_i32_16x16x64_i8, 16
+//            token columns per MFMA, the sub-block scales folded into the
+//            weight operand; each weight super-block is loaded and folded once
+//            and used for every token chunk of the unit; SwiGLU fused;
+//   Q8_K(h)  per pair;
+//   down     64 rows per workgroup, the tile staged in LDS in one burst;
+//            y goes to its (token, slot) place;
+//   combine  per token, slots in order, plus the residual.
+// Every expert's weights are read once per unit (once per call for a group of
+// at most kUnitTokens tokens); each (row, token) value is formed from the
+// per-token path's integer sub-block sums in its fp32 order (mfma.h), so every
+// token's result is the single-token path's bit for bit.
+#include "kernels.h"
+#include "lds_dma.h"
+#include "mfma.h"
+#include "qblocks.h"
+#include "rowdot.h"
+
+namespace hoard {
+
+namespace {
+
+constexpr int kWaveRows = 16;  // rows per wave: one MFMA tile
+constexpr int kGuRows = 32;    // gate (and up) rows per workgroup: two 16-row tiles
+constexpr int kDnRows = 64;    // down rows per workgroup
+constexpr int kChunks = kUnitTokens / 16;  // 16-token MFMA chunks per unit
+static_assert(kChunks == 4, "four token chunks per unit");
+
+__device__ __forceinline__ const Q8L *q8c(const uint8_t *p) { return reinterpret_cast<const Q8L *>(p); }
+
+// A work unit: group u (expert uexp[u]), its pairs [p0, p0 + n) in sorted order.
+struct Unit {
+    int e, p0, n;
+};
+__device__ __forceinline__ bool load_unit(const BatchedArgs &a, int unit, Unit &w) {
+    if (unit >= a.n_units[0]) return false;
+    const int u = a.units[3 * unit];
+    w.e = a.uexp[u];
+    w.p0 = a.goff[u] + a.units[3 * unit + 1];
+    w.n = a.units[3 * unit + 2];
+    return w.n > 0;
+}
+
+__device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// One Q4_K super-block of a 16-row tile, folded for v_mfma_i32_16x16x64_i8.
+// Lane l supplies A[l % 16][16 g .. 16 g + 15] (g = l / 16) of each 64-element
+// chunk jc (the lane layout checked by a probe: B[16 g ..][l % 16] alike,
+// D[4 g + i][l % 16]).  Chunk jc holds sub-block 2 jc in the low nibbles of its
+// 32 quant bytes and sub-block 2 jc + 1 in the high ones, so lane group g takes
+// the low (g < 2) or high (g >= 2) nibbles of bytes 16 (g & 1) .. + 15:
+// sub-block s = 2 jc + g / 2.  The sub-block scale sc (6 bits) is folded into A
+// in two parts that keep every product an int8: hi = q * (sc >> 3) and
+// lo = q * (sc & 7), each <= 105, with sc * q = 8 hi + lo; a nibble times a
+// factor below 8 never carries into the next byte, so a whole word multiplies
+// at once.  The min term sum_s m_s * (sum of sub-block s's activation quants)
+// is a third MFMA with m_s broadcast over its sub-block.  The three chains give
+// exactly the per-token path's integer sums isum = 8 D_hi + D_lo and
+// msum = D_min.
+struct Q4Fold {
+    v4i hi[4], lo[4];
+    uint32_t mn;          // byte jc: the min of the lane's sub-block in chunk jc
+    float d[4], dmin[4];  // factors of the four rows whose results the lane receives
+};
+
+__device__ __forceinline__ uint32_t splat_byte(uint32_t v) { return v * 0x01010101u; }
+
+// The lane's raw bytes of one super-block of a 16-row tile: its row's header
+// and quants (16 bytes of each 64-element chunk) and the fp16 factors of the
+// four rows whose results it receives; loaded one super-block ahead.
+struct Q4Raw {
+    uint4 hd;
+    uint4 qv[4];
+    uint32_t dm[4];
+};
+
+__device__ __forceinline__ void q4_raw_load(const uint8_t *W, size_t rb, int b, Q4Raw &o) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const uint8_t *blk = W + (size_t)r * rb + (size_t)b * kQ4KBytes;
+    o.hd = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) o.qv[jc] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * jc + 16 * (g & 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o.dm[i] = *reinterpret_cast<const uint32_t *>(W + (size_t)(4 * g + i) * rb + (size_t)b * kQ4KBytes);
+}
+
+__device__ __forceinline__ void q4_fold(const Q4Raw &raw, Q4Fold &o) {
+    const int g = (threadIdx.x & 63) >> 4;
+    uint32_t sc[2], mn[2];
+    q4k_scales_packed(raw.hd, sc, mn);
+    const uint32_t nsh = 4u * (uint32_t)(g >> 1);
+    o.mn = 0u;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        const int s = 2 * jc + (g >> 1);
+        const uint32_t scs = (uint32_t)byte_of(sc[s >> 2], s & 3), mns = (uint32_t)byte_of(mn[s >> 2], s & 3);
+        const uint4 qv = raw.qv[jc];
+        const uint32_t w[4] = {(qv.x >> nsh) & 0x0f0f0f0fu, (qv.y >> nsh) & 0x0f0f0f0fu, (qv.z >> nsh) & 0x0f0f0f0fu,
+                               (qv.w >> nsh) & 0x0f0f0f0fu};
+        const uint32_t h = scs >> 3, lw = scs & 7u;
+        o.hi[jc] = v4i{(int)(w[0] * h), (int)(w[1] * h), (int)(w[2] * h), (int)(w[3] * h)};
+        o.lo[jc] = v4i{(int)(w[0] * lw), (int)(w[1] * lw), (int)(w[2] * lw), (int)(w[3] * lw)};
+        o.mn |= mns << (8 * jc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o.d[i] = half_bits_to_float(raw.dm[i] & 0xffffu);
+        o.dmin[i] = half_bits_to_float(raw.dm[i] >> 16);
+    }
+}
+
+// One super-block of the folded tile against the lane's token column (its Q8_K
+// block x): the integer sums from the three MFMA chains, then the per-token
+// path's fp32 block terms added in order.
+__device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const Q8L &x, float acc[4], float accm[4]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0}, dn = {0, 0, 0, 0};
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        const v4i xv = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
+        dh = mfma_16x16x64(w.hi[jc], xv, dh);
+        dl = mfma_16x16x64(w.lo[jc], xv, dl);
+        const int m4 = (int)splat_byte((w.mn >> (8 * jc)) & 0xffu);
+        dn = mfma_16x16x64(v4i{m4, m4, m4, m4}, xv, dn);
+    }
+    const float xd = x.d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int isum = 8 * dh[i] + dl[i];
+        const float dd = w.d[i] * xd;
+        const float dm = w.dmin[i] * xd;
+        acc[i] = acc[i] + dd * (float)isum;
+        accm[i] = accm[i] + dm * (float)dn[i];
+    }
+}
+
+// -- gate/up + SwiGLU ------------------------------------------------------------
+// grid (n_ff / 32, max units), block 256: wave w takes rows [32 x + 16 (w % 2), +16)
+// of gate (w < 2) or up (w >= 2) of the unit's expert against every token of the
+// unit.  Per super-block the workgroup copies the Q8_K blocks of the unit's
+// token chunks into LDS (one buffer ahead) while each wave holds the next
+// super-block of its rows in registers; the gate waves hand their values to the
+// up waves through LDS, which form h and store it to hbuf[sorted pair][row].
+// Three workgroups share a CU.
+constexpr int kXGran = (int)sizeof(Q8L) / 16;                          // 16-byte granules per Q8_K block
+constexpr int kXChunksPerBlock = (kUnitTokens * kXGran + 63) / 64;     // 1 KB copies per unit block
+
+template <int NB>
+__global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
+    __shared__ __align__(16) Q8L xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
+    __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
+    Unit w;
+    if (!load_unit(a, blockIdx.y, w)) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int m = wave >> 1, rt = wave & 1;
+    const int row0 = blockIdx.x * kGuRows + rt * kWaveRows;
+    constexpr size_t rb = (size_t)NB * kQ4KBytes;
+    const uint8_t *W = (m ? a.up + (size_t)w.e * a.ustride : a.gate + (size_t)w.e * a.gstride) + (size_t)row0 * rb;
+    const int nch = (w.n + 15) >> 4;
+    // this lane's granules of the x copy: chunks wave, wave + 4, ...; only the
+    // unit's token chunks are copied, token places past its end copy its last token
+    constexpr int kXJ = (kXChunksPerBlock + 3) / 4;
+    const int ngran = nch * 16 * kXGran;
+    const uint8_t *xsrc[kXJ];
+#pragma unroll
+    for (int j = 0; j < kXJ; ++j) {
+        const int p = 64 * (wave + 4 * j) + lane, tt = min(p / kXGran, kUnitTokens - 1), o = p % kXGran;
+        xsrc[j] = a.q8x + (size_t)a.ptok[w.p0 + min(tt, w.n - 1)] * NB * sizeof(Q8L) + 16 * o;
+    }
+    auto stage_x = [&](int b, int buf) {
+#pragma unroll
+        for (int j = 0; j < kXJ; ++j) {
+            const int ck = wave + 4 * j;
+            if (64 * ck < ngran && 64 * ck + lane < ngran)
+                dma_lanes(reinterpret_cast<uint8_t *>(&xs[buf][0]) + 1024 * ck, xsrc[j] + (size_t)b * sizeof(Q8L));
+        }
+    };
+    float acc[kChunks][4], accm[kChunks][4];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ch][i] = accm[ch][i] = 0.0f;
+    Q4Raw raw;
+    q4_raw_load(W, rb, 0, raw);
+    stage_x(0, 0);
+#pragma unroll 1
+    for (int b = 0; b < NB; ++b) {
+        __syncthreads();  // every wave's copies of x(b) landed, and x(b - 1) is read
+        Q4Fold t;
+        q4_fold(raw, t);
+        if (b + 1 < NB) {
+            q4_raw_load(W, rb, b + 1, raw);
+            stage_x(b + 1, (b + 1) & 1);
+        }
+        const Q8L *xb = xs[b & 1];
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch)
+            if (ch < nch) q4_fold_step(t, xb[ch * 16 + c], acc[ch], accm[ch]);
+    }
+    if (m == 0) {
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gx[rt][ch][i][lane] = acc[ch][i] - accm[ch][i];
+    }
+    __syncthreads();
+    if (m == 0) return;
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+        const int idx = ch * 16 + c;
+        if (ch < nch && idx < w.n) {
+            float hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float g = gx[rt][ch][i][lane], uu = acc[ch][i] - accm[ch][i];
+                hv[i] = g / (1.0f + expf(-g)) * uu;
+            }
+            *reinterpret_cast<float4 *>(a.hbuf + (size_t)(w.p0 + idx) * a.n_ff + row0 + 4 * q) =
+                make_float4(hv[0], hv[1], hv[2], hv[3]);
+        }
+    }
+}
+
+// -- Q8_K of h per sorted pair --------------------------------------------------
+// grid (pairs), block 64 * NBH: wave b quantises block b of the pair's h.
+__global__ __launch_bounds__(256) void pf_quant_h_kernel(BatchedArgs a) {
+    const int pos = blockIdx.x, b = threadIdx.x >> 6;
+    const int nbh = a.n_ff / QK;
+    if (b >= nbh) return;
+    wave_quantize_q8l(a.hbuf + (size_t)pos * a.n_ff + (size_t)b * QK,
+                      reinterpret_cast<Q8L *>(a.q8h) + (size_t)pos * nbh + b);
+}
+
+// -- down: 64 rows of the unit's expert, y to its (token, slot) place -----------
+// grid (n_embd / 64, max units), block 256.  The 64-row tile is copied into LDS
+// in one burst; wave w takes rows [16 w, +16) of it.
+template <int TD, int NBH>
+__global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
+    constexpr int kRowBytes = NBH * QType<TD>::bytes;
+    constexpr int kTileBytes = kDnRows * kRowBytes;
+    static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
+    __shared__ __align__(16) uint8_t tile[kTileBytes];
+    Unit w;
+    if (!load_unit(a, blockIdx.y, w)) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int rt0 = blockIdx.x * kDnRows;
+    {
+        // the burst split over the four waves, 1 KB chunks each
+        const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
+        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
+        for (int ck = wave; ck < kChunksTotal; ck += 4)
+            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk(tile + ck * 1024, src + (size_t)ck * 1024);
+        lds_dma_wait();
+    }
+    __syncthreads();
+    const uint8_t *T = tile + wave * kWaveRows * kRowBytes;
+    const int nch = (w.n + 15) >> 4;
+    const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
+    // (chunk, block) steps with the next step's activation operands loaded
+    // while the current one computes
+    auto xq_of = [&](int ch) { return q8h + (size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH; };
+    Q6X cur, nxt;
+    q6_load_x(xq_of(0), 0, cur);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = nch * NBH;
+#pragma unroll 1
+    for (int st = 0; st < steps; ++st) {
+        const int ch = st / NBH, b = st - ch * NBH;
+        if (st + 1 < steps) q6_load_x(xq_of((st + 1) / NBH), (st + 1) % NBH, nxt);
+        if constexpr (TD == kTypeQ4K)
+            q4_tile_block(T, kRowBytes, b, cur, acc, accm);
+        else
+            q6_tile_block(T, kRowBytes, b, cur, acc);
+        if (b == NBH - 1) {
+            const int idx = ch * 16 + c;
+            if (idx < w.n) {
+                const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = TD == kTypeQ4K ? acc[i] - accm[i] : acc[i];
+                *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * a.k + j) * a.n_embd + rt0 + wave * kWaveRows +
+                                            4 * q) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = accm[i] = 0.0f;
+        }
+        cur = nxt;
+    }
+}
+
+// -- combine: out[t][d] = (sum_j w[t][j] * y[t][j][d]) + res[t][d], j ascending --
+__global__ __launch_bounds__(256) void pf_combine_kernel(BatchedArgs a) {
+    const int t = blockIdx.y;
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= a.n_embd) return;
+    if (a.bad && a.bad[t]) {  // an id outside the pool or expert set: the token's row is poisoned
+        a.out[(size_t)t * a.n_embd + d] = __builtin_nanf("");
+        return;
+    }
+    float acc = 0.0f;
+    for (int j = 0; j < a.k; ++j) {
+        const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
+        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * a.k + js) * a.n_embd + d];
+    }
+    a.out[(size_t)t * a.n_embd + d] = acc + a.res[(size_t)t * a.n_embd + d];
+}
+
+}  // namespace
+
+hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s) {
+    const int nbh = a.n_ff / QK;
+    if (a.n_embd != 2048 || a.n_ff % kGuRows || a.n_embd % kDnRows || nbh > 4 || a.max_units < 1)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_gateup_kernel<8>, dim3(a.n_ff / kGuRows, a.max_units), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(pf_quant_h_kernel, dim3(a.M * a.k), dim3(64 * nbh), 0, s, a);
+    const dim3 dg(a.n_embd / kDnRows, a.max_units);
+#define HOARD_DOWN(T, N)                                                         \
+    if (a.d_type == T && nbh == N) {                                             \
+        hipLaunchKernelGGL((pf_down_kernel<T, N>), dg, dim3(256), 0, s, a);     \
+    } else
+    HOARD_DOWN(kTypeQ6K, 3) HOARD_DOWN(kTypeQ6K, 2) HOARD_DOWN(kTypeQ6K, 4) HOARD_DOWN(kTypeQ4K, 4)
+    HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
+#undef HOARD_DOWN
+    hipLaunchKernelGGL(pf_combine_kernel, dim3((a.n_embd + 255) / 256, a.M), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace hoard
