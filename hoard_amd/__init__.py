@@ -114,6 +114,7 @@ ABI = {
     "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
     "hoard_moe_pool_ensure": (_I, [_P, _I, _P, _P, _P, _P, _P]),
     "hoard_moe_forward_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "hoard_moe_forward_batched_noalloc": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "hoard_moe_ffn_combine_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "hoard_moe_pool_ensure_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "hoard_moe_get_stats": (_I, [_P, ctypes.POINTER(MoeStats)]),

@@ -110,6 +110,13 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s);
 // The same expert products and combine for the caller's ids (a.sel) and weights (a.wsel).
 hipError_t launch_batched_ids(const BatchedArgs &a, hipStream_t s);
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff);
+// The allocation-free batched entry point's fixed scratch (noalloc.hip): the
+// route counters lead it, zeroed at set-up; the rest is laid out per call.
+constexpr int kNoAllocMaxTokens = 16;
+constexpr size_t kNoAllocCounterBytes = 1024;
+hipError_t noalloc_setup(int device);
+uint8_t *noalloc_scratch(int device);
+size_t noalloc_scratch_bytes();
 // The expert products and combine of a prefill-sized batch after its grouping
 // (prefill.hip): gate/up + SwiGLU, Q8_K(h), down, ordered combine.
 hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s);

@@ -135,6 +135,8 @@ struct hoard_moe {
     unsigned *b_counters = nullptr; // route kernel's completion counters
     int *b_layout_ysrc = nullptr, *b_layout_bad = nullptr;  // caller-id arrays within b_ints
     bool hist_pending = false;      // a batched call ran since the histogram was last read
+    const unsigned *hist_src = nullptr;  // the last batched call's histogram and group count
+    const int *nu_src = nullptr;
     size_t trace_layers = 0;
     bool tracing = false;
     int trace_last = 0;  // layers covered by the last traced decode
@@ -803,6 +805,11 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
                 rc = fail(HOARD_ERR_HIP, "upload stream");
     }
     if (!rc) rc = persistent_setup(h);
+    if (!rc) {
+        // this device's copy of the allocation-free entry point's fixed scratch
+        const hipError_t e = hoard::noalloc_setup(h->device);
+        if (e != hipSuccess) rc = fail(HOARD_ERR_HIP, "fixed scratch set-up: %s", hipGetErrorString(e));
+    }
     // the zeroed counters and exchange words are in place before any launch, on
     // whatever stream the caller uses (a non-blocking stream does not wait for
     // the null stream's memsets)
@@ -1196,6 +1203,53 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
     if (e != hipSuccess) return fail(HOARD_ERR_HIP, "batched launch: %s", hipGetErrorString(e));
     h->stats.tokens += (uint64_t)M;
     h->hist_pending = true;
+    h->hist_src = a.hist;
+    h->nu_src = a.n_unique;
+    return HOARD_OK;
+}
+
+// The batched forward with its per-call scratch in the library's fixed device
+// array (noalloc.hip) instead of buffers allocated on first use: the call
+// allocates nothing.  Layout: the route counters (zeroed at set-up, left zero
+// by every launch), then the logits, Q8_K(fx), Q8_K(h), h, y, the int arrays
+// and the histogram, each 256-byte aligned.
+int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
+                                      float *out_dev, int32_t *sel_dev, float *w_dev, void *stream) {
+    hoard::BatchedArgs a;
+    if (int rc = batched_check(h, layer, M, fx_dev, res_dev, out_dev, false, hoard::kNoAllocMaxTokens, &a)) return rc;
+    uint8_t *base = hoard::noalloc_scratch(h->device);
+    if (!base) return fail(HOARD_ERR_STATE, "no fixed scratch set up for device %d", h->device);
+    const hoard_moe_cfg &c = h->cfg;
+    const BatchedLayout L = batched_layout(c, M);
+    size_t o = hoard::kNoAllocCounterBytes;
+    auto take = [&](size_t n) {
+        const size_t r = o;
+        o += (n + 255) & ~(size_t)255;
+        return r;
+    };
+    const size_t o_log = take(sizeof(float) * M * c.n_expert), o_q8x = take(L.q8x), o_q8h = take(L.q8h);
+    const size_t o_h = take(L.hbuf), o_y = take(L.ybuf), o_ints = take(sizeof(int) * L.n_ints), o_hist = take(L.hist);
+    if (o > hoard::noalloc_scratch_bytes())
+        return fail(HOARD_ERR_INVALID, "M %d of this shape needs %zu bytes of scratch; the fixed array holds %zu", M, o,
+                    hoard::noalloc_scratch_bytes());
+    a.logits = reinterpret_cast<float *>(base + o_log);
+    bind_batched(a, L, base + o_q8x, base + o_q8h, reinterpret_cast<float *>(base + o_h),
+                 reinterpret_cast<float *>(base + o_y), reinterpret_cast<int *>(base + o_ints),
+                 reinterpret_cast<unsigned *>(base + o_hist), reinterpret_cast<unsigned *>(base));
+    a.ysrc = a.bad = nullptr;
+    a.sel = sel_dev ? sel_dev : h->sel;
+    a.wsel = w_dev ? w_dev : h->wsel;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    {
+        KernelMark mark(h, HOARD_KERNEL_BATCHED, s);
+        e = hoard::launch_batched(a, s);
+    }
+    if (e != hipSuccess) return fail(HOARD_ERR_HIP, "batched launch: %s", hipGetErrorString(e));
+    h->stats.tokens += (uint64_t)M;
+    h->hist_pending = true;
+    h->hist_src = a.hist;
+    h->nu_src = a.n_unique;
     return HOARD_OK;
 }
 
@@ -1248,8 +1302,8 @@ int hoard_moe_get_stats(hoard_moe *h, hoard_moe_stats *out) {
         int nu = 0;
         HIP_TRY(hipSetDevice(h->device));
         HIP_TRY(hipDeviceSynchronize());
-        HIP_TRY(hipMemcpy(hist.data(), h->b_hist, sizeof(unsigned) * E, hipMemcpyDeviceToHost));
-        HIP_TRY(hipMemcpy(&nu, h->b_ints, sizeof(int), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hist.data(), h->hist_src, sizeof(unsigned) * E, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(&nu, h->nu_src, sizeof(int), hipMemcpyDeviceToHost));
         for (int e = 0; e < E && e < 1024; ++e) h->stats.expert_hist[e] = hist[e];
         h->stats.last_unique = nu;
         h->hist_pending = false;

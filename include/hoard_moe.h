@@ -145,6 +145,19 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
 int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
                               float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 
+/* hoard_moe_forward_batched with nothing allocated by the call, for callers
+   that cannot allocate device memory (code under HIP graph capture, tight
+   serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+   reference.  The per-call scratch lives in one fixed device array per GPU,
+   16 MiB, looked up when a handle is created and held until the process ends;
+   1 <= M <= min(max_tokens, 16), and a shape whose scratch for M tokens exceeds
+   the array is refused with HOARD_ERR_INVALID (the Qwen3-30B shape needs about
+   9 MiB at M = 16).  Results are hoard_moe_forward_batched's bit for bit.  Every
+   call on a GPU shares that GPU's array: calls that overlap on one GPU (any
+   handle, any stream) race. */
+int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
+                                      float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
+
 /* The batched expert products and combine for the caller's selection, the
    counterpart of the verify step's mul_mat_id over the slot pool with the host's
    ids and weights and the sum over views (src/run_specloop.cpp:116-139):
