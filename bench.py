@@ -92,11 +92,13 @@ def log(*a):
 
 def kernel_bytes(shape, kind: int, n_layer: int) -> int:
     """Algorithmic HBM bytes of one launch of each kernel for one token."""
-    from hoard_amd import KERNEL_DECODE, KERNEL_DOWN, KERNEL_GATEUP, KERNEL_ROUTER, expert_bytes
+    from hoard_amd import KERNEL_DECODE, KERNEL_DOWN, KERNEL_GATEUP, KERNEL_LAYER, KERNEL_ROUTER, expert_bytes
     s = shape
     n = s.n_embd
     if kind == KERNEL_DECODE:  # one launch runs every layer of the token
         return n_layer * s.bytes_per_token_layer()
+    if kind == KERNEL_LAYER:  # one launch runs one layer
+        return s.bytes_per_token_layer()
     if kind == KERNEL_ROUTER:
         return 4 * s.n_expert * n + 4 * n + 4 * n  # W, x in, fx out
     sh = bool(s.n_ff_shexp)

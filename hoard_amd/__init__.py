@@ -60,9 +60,9 @@ class MoeStats(ctypes.Structure):
     ]
 
 
-KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN, KERNEL_DECODE, KERNEL_BATCHED = 0, 1, 2, 3, 4
+KERNEL_ROUTER, KERNEL_GATEUP, KERNEL_DOWN, KERNEL_DECODE, KERNEL_BATCHED, KERNEL_LAYER = 0, 1, 2, 3, 4, 5
 KERNEL_NAMES = {KERNEL_ROUTER: "router", KERNEL_GATEUP: "gateup", KERNEL_DOWN: "down_combine",
-                KERNEL_DECODE: "decode_persistent", KERNEL_BATCHED: "batched_experts"}
+                KERNEL_DECODE: "decode_persistent", KERNEL_BATCHED: "batched_experts", KERNEL_LAYER: "layer_fused"}
 TRACE_PHASES = 12
 OPT_PERSISTENT_DECODE = 1
 OPT_PERSISTENT_AVAILABLE = 2
@@ -73,6 +73,7 @@ OPT_LAYER_KERNELS = 6
 OPT_DECODE_LAUNCH = 7
 OPT_WAIT_LIMIT_US = 8
 OPT_FAIL_UPLOAD = 9
+OPT_LAYER_FUSED = 10
 DECODE_AUTO, DECODE_XCD, DECODE_SPREAD = 0, 1, 2
 
 
@@ -112,6 +113,7 @@ ABI = {
     "hoard_moe_sync_check": (_I, [_P]),
     "hoard_moe_phase_trace": (_I, [_P, _I]),
     "hoard_moe_phase_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
+    "hoard_moe_fused_trace_read": (_I, [_P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
     "hoard_moe_pool_ensure": (_I, [_P, _I, _P, _P, _P, _P, _P]),
     "hoard_moe_forward_batched": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "hoard_moe_forward_batched_noalloc": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),

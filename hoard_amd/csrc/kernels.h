@@ -191,6 +191,33 @@ struct SpreadArgs {
 bool spread_shape_compiled(const SpreadArgs &a);
 hipError_t launch_spread_decode(const SpreadArgs &a, hipStream_t s, bool cooperative = true);
 
+// One launch for a whole layer of one token (layer.hip): router, gate/up and
+// down workgroups in the order they start, each waiting only on workgroups
+// that started before it, so no workgroup needs another to become resident.
+struct FusedLayerArgs {
+    const float *xin;          // [n_embd]: fx, or (rms) x whose rms_norm is fx
+    int rms;
+    float eps;
+    const float *res;          // [n_embd] residual (may alias out)
+    float *out;                // [n_embd]
+    int32_t *sel;              // [k] selected experts (written)
+    float *wsel;               // [k] their weights (written)
+    const float *router;       // [E][n_embd]
+    MatDesc gate, up, down;    // routed experts (stride per expert)
+    int n_embd, E, k, renorm;
+    float *logits;             // [E] scratch
+    float *h;                  // [k][n_ff] scratch
+    unsigned long long *ctr;   // kFusedCounterWords zeroed words: tickets, completion counts and flags
+    int *err;                  // raised by a wait that runs out
+    long long wait_ticks;
+    unsigned long long *trace; // optional [workgroup][kFusedStamps] wall-clock stamps, by ticket order per XCD
+};
+constexpr int kFusedStamps = 6;  // xcd * 65536 + role slot, start, 3 role events, end
+constexpr int kFusedCounterWords = 16 * (8 + 1 + 16 + 8 + 8);
+bool fused_layer_ok(const FusedLayerArgs &a);
+int fused_layer_groups(const FusedLayerArgs &a);  // workgroups of one launch
+hipError_t launch_fused_layer(const FusedLayerArgs &a, hipStream_t s);
+
 // Per-layer launches for the instantiated shapes (layer.hip); the *_ok tests
 // say whether they take the arguments, else the kernels above run.
 bool layer_route_ok(const RouterArgs &a);

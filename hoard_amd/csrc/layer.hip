@@ -17,6 +17,7 @@
 // the logits are stored and read at device scope (past the per-XCD L2) and
 // each workgroup counts itself done after its stores are acknowledged, with
 // no cache-flushing fence.
+#include "exchange.h"
 #include "kernels.h"
 #include "lds_dma.h"
 #include "qblocks.h"
@@ -272,6 +273,276 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
     }
 }
 
+// -- one launch per layer ---------------------------------------------------------
+// Workgroups take a ticket when they start, from a counter of their XCD; each
+// XCD's tickets give its share of the roles in order: router workgroups, then
+// gate/up ones, then down ones (the launch deals the workgroups round-robin to
+// the 8 XCDs, so every XCD holds an eighth of each role).  A workgroup waits
+// only for roles with lower tickets on its own XCD, which started before it,
+// or for roles that come first on every XCD, which need nothing from later
+// ones; so every wait ends whatever the number of workgroups resident at once.
+// The counters grow across launches: launch e (ticket / workgroups per XCD)
+// waits for the counts of launch e.  Every value crosses workgroups through
+// device-scope stores and loads (past the per-XCD L2), each counted only after
+// its stores are acknowledged.  What many workgroups wait for (the selection,
+// each slot's h) is published once per XCD, so the waiting spreads over eight
+// lines, and waiters sleep between probes.
+constexpr int kFRouteRows = 4;  // router rows per router workgroup
+constexpr int kFGuRows = 16;    // gate rows (and up rows) per gate/up workgroup
+constexpr int kFDownRows = 8;   // output rows per down workgroup
+constexpr int kFXcds = 8;
+// counter words (16 to a 128-byte line)
+constexpr int kFCtrTicket = 0;               // line x: tickets of XCD x
+constexpr int kFCtrRoute = 16 * 8;           // router workgroups done
+constexpr int kFCtrH = 16 * 9;               // line 9 + j: gate/up workgroups of slot j done
+constexpr int kFCtrSel = 16 * 25;            // line 25 + x: the selection published, copy for XCD x
+constexpr int kFCtrHDone = 16 * 33;          // line 33 + x, word j: slot j's h complete, copy for XCD x
+static_assert(kFCtrHDone + 16 * kFXcds == kFusedCounterWords, "counter lines");
+
+__device__ __forceinline__ unsigned long long ctr_load(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ctr_add(unsigned long long *p) {
+    return __hip_atomic_fetch_add(p, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ctr_store(unsigned long long *p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool reached(unsigned long long v, unsigned long long target) {
+    return (long long)(v - target) >= 0;
+}
+// Bounded wait of one thread for *p to reach `target`, sleeping ~0.2 us between probes.
+__device__ __forceinline__ bool wait_count(const unsigned long long *p, unsigned long long target, int *err,
+                                           long long limit) {
+    return poll(
+        [&]() {
+            if (reached(ctr_load(p), target)) return true;
+            __builtin_amdgcn_s_sleep(8);
+            return false;
+        },
+        err, limit);
+}
+
+// rms_norm scale of x (every thread takes part): mean of x*x in double,
+// 1/sqrtf(mean + eps), as the route kernel forms it.
+__device__ __forceinline__ float rms_scale(const float *x, int n, float eps, double *red) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        ss += (double)(v * v);
+    }
+    ss = wave_sum_d(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
+    const float mean = (float)(tot * (1.0 / (double)n));
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// Workgroups of each role per XCD.
+struct FusedRoles {
+    int route, gu, down;
+};
+__host__ __device__ __forceinline__ FusedRoles fused_roles(int E, int k, int n_ff, int n_embd) {
+    const int r = (E + kFRouteRows - 1) / kFRouteRows, g = k * (n_ff / kFGuRows), d = n_embd / kFDownRows;
+    return {(r + kFXcds - 1) / kFXcds, (g + kFXcds - 1) / kFXcds, (d + kFXcds - 1) / kFXcds};
+}
+
+template <int TD, int NBH>
+__global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
+    constexpr int N = 2048, NB = N / QK;
+    constexpr int kGuRowBytes = NB * kQ4KBytes;
+    constexpr int kDnRowBytes = NBH * QType<TD>::bytes;
+    constexpr int kSegBytes = kFDownRows * kDnRowBytes;  // 8 rows of one expert
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ unsigned long long tk_s;
+    __shared__ int flag_s;
+    __shared__ double red[8];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E = a.E, k = a.k, nff = a.gate.rows;
+    const unsigned xcc = xcc_id();
+    const FusedRoles R = fused_roles(E, k, nff, N);
+    const unsigned long long Gx = (unsigned long long)(R.route + R.gu + R.down);
+    if (tid == 0) {
+        tk_s = ctr_add(a.ctr + kFCtrTicket + 16 * xcc);
+        flag_s = 0;
+    }
+    __syncthreads();
+    const unsigned long long ep = tk_s / Gx;
+    const int lt = (int)(tk_s - ep * Gx);  // role slot within this XCD's share
+    const int n_route = R.route * kFXcds, gu_per = nff / kFGuRows, n_gu = k * gu_per;
+    // phase stamps: [xcc * Gx + lt][id, start, e1, e2, e3, end]
+    unsigned long long *st = a.trace ? a.trace + ((size_t)xcc * Gx + lt) * kFusedStamps : nullptr;
+    auto stamp = [&](int i) {
+        if (st && tid == 0) st[i] = wall_clock64();
+    };
+    if (st && tid == 0) st[0] = (unsigned long long)xcc * 65536ull + (unsigned long long)lt;
+    stamp(1);
+
+    if (lt < R.route) {
+        // -- router rows [4 i, +4): a half-wave per row in ggml's x86 f32 order --
+        const int i = (int)xcc * R.route + lt;
+        const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
+        const int row = i * kFRouteRows + (tid >> 5), l = tid & 31;
+        if (tid < 32 * kFRouteRows && row < E) {
+            const float *wr = a.router + (size_t)row * N + l;
+            const float *xr = a.xin + l;
+            float acc = 0.0f;
+#pragma unroll 16
+            for (int c = 0; c < N; c += 32) acc = fmaf(wr[c], xr[c] * scale, acc);
+            acc = acc + __shfl_xor(acc, 16);
+            acc = row16_ggml_fold(acc);
+            if (l == 0) __hip_atomic_store(a.logits + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logits are acknowledged
+        __syncthreads();
+        stamp(2);
+        if (tid == 0) flag_s = ctr_add(a.ctr + kFCtrRoute) + 1ull == (ep + 1ull) * (unsigned long long)n_route;
+        __syncthreads();
+        stamp(3);
+        if (!flag_s) {
+            stamp(5);
+            return;
+        }
+        // the last router workgroup: softmax, top-k, renorm; then the selection is
+        // published to every XCD
+        if (wave == 0) {
+            router_tail<true>(a.logits, E, k, a.renorm, a.sel, a.wsel, 0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (lane < kFXcds) ctr_store(a.ctr + kFCtrSel + 16 * lane, ep + 1ull);
+        }
+        stamp(4);
+        stamp(5);
+        return;
+    }
+
+    if (lt < R.route + R.gu) {
+        // -- gate/up rows [16 r, +16) of slot j, SwiGLU --
+        const int i = (int)xcc * R.gu + (lt - R.route);
+        if (i >= n_gu) return;  // padding of the XCD shares
+        const int j = i / gu_per, r0 = (i - j * gu_per) * kFGuRows;
+        uint8_t *wt = smem;  // [2][16 rows]
+        Q8L *q8 = reinterpret_cast<Q8L *>(smem + 2 * kFGuRows * kGuRowBytes);
+        float *gu = reinterpret_cast<float *>(q8 + NB);
+        const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
+        if (wave >= 4) {
+            // Q8_K of fx while the selection is awaited and the rows are copied
+            for (int b = wave - 4; b < NB; b += 4) {
+                const float4 x4 = *reinterpret_cast<const float4 *>(a.xin + b * QK + 4 * lane);
+                const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
+                wave_quantize_q8l_regs(v, &q8[b]);
+            }
+        } else if (tid == 0) {
+            if (!wait_count(a.ctr + kFCtrSel + 16 * xcc, ep + 1ull, a.err, a.wait_ticks)) flag_s = 1;
+            stamp(2);
+        }
+        __syncthreads();
+        const int id = __hip_atomic_load(a.sel + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool bad = flag_s || id < 0 || id >= a.gate.n_ids;
+        if (!bad && wave < 4) {
+            // gate rows on waves 0-1, up rows on waves 2-3
+            constexpr int half = (kFGuRows * kGuRowBytes / 2 + 1023) & ~1023;
+            const int m = wave >> 1, off = (wave & 1) * half;
+            const int len = min(half, kFGuRows * kGuRowBytes - off);
+            const uint8_t *src = (m ? a.up.base + (size_t)id * a.up.stride : a.gate.base + (size_t)id * a.gate.stride) +
+                                 (size_t)r0 * kGuRowBytes;
+            wave_copy(wt + m * kFGuRows * kGuRowBytes + off, src + off, len);
+            lds_dma_wait();
+        }
+        __syncthreads();
+        stamp(3);
+        if (!bad && (tid >> 3) < 2 * kFGuRows) {
+            const int grp = tid >> 3, t8 = tid & 7;
+            const int m = grp >= kFGuRows, row = grp - m * kFGuRows;
+            const float v = lpb_row_q4k_mem<NB>(wt + (m * kFGuRows + row) * kGuRowBytes, q8[t8], t8);
+            if (t8 == NB - 1) gu[grp] = v;
+        }
+        __syncthreads();
+        if (tid < kFGuRows) {
+            const float g = gu[tid], u = gu[kFGuRows + tid];
+            const float hv = bad ? __builtin_nanf("") : g / (1.0f + expf(-g)) * u;
+            __hip_atomic_store(a.h + (size_t)j * nff + r0 + tid, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // h is acknowledged before it is counted
+        __syncthreads();
+        stamp(4);
+        if (tid == 0) {
+            // the slot's last gate/up workgroup publishes the slot's h to every XCD
+            const unsigned long long c = ctr_add(a.ctr + kFCtrH + 16 * j) + 1ull;
+            if (c == (ep + 1ull) * (unsigned long long)gu_per)
+                for (int x = 0; x < kFXcds; ++x) ctr_store(a.ctr + kFCtrHDone + 16 * x + j, ep + 1ull);
+        }
+        stamp(5);
+        return;
+    }
+
+    // -- down rows [8 i, +8) of every selected expert, then the combine --
+    const int i = (int)xcc * R.down + (lt - R.route - R.gu);
+    if (i * kFDownRows >= N) return;  // padding of the XCD shares
+    const int d0 = i * kFDownRows;
+    uint8_t *wd = smem;  // [k][8 rows]
+    Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes);
+    float *ys = reinterpret_cast<float *>(q8h + k * NBH);
+    if (tid == 0 && !wait_count(a.ctr + kFCtrSel + 16 * xcc, ep + 1ull, a.err, a.wait_ticks)) flag_s = 1;
+    __syncthreads();
+    stamp(2);
+    int bad = flag_s;
+    for (int u = wave; u < k; u += 8) {
+        // expert u's 8 rows from wave u: copies in different pages do not wait on each other
+        const int id = __hip_atomic_load(a.sel + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (id < 0 || id >= a.down.n_ids) {
+            bad = 1;
+            continue;
+        }
+        if (!flag_s) wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kDnRowBytes,
+                               kSegBytes);
+    }
+    if (wave == 0 && !flag_s) {
+        // every slot's h complete: lane j watches slot j's word of this XCD's line
+        const unsigned long long *hd = a.ctr + kFCtrHDone + 16 * xcc;
+        const bool ok = poll(
+            [&]() {
+                const bool r = lane >= k || reached(ctr_load(hd + lane), ep + 1ull);
+                if (__all(r)) return true;
+                __builtin_amdgcn_s_sleep(8);
+                return false;
+            },
+            a.err, a.wait_ticks);
+        if (!ok && lane == 0) flag_s = 1;
+    }
+    __syncthreads();
+    stamp(3);
+    // Q8_K of every unit's h, read past the L2 (it was written on other XCDs)
+    for (int q = wave; q < k * NBH; q += 8) {
+        const int u = q / NBH, b = q - u * NBH;
+        const float *hp = a.h + (size_t)u * nff + b * QK + 4 * lane;
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __hip_atomic_load(hp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wave_quantize_q8l_regs(v, &q8h[q]);
+    }
+    lds_dma_wait();
+    if (bad) atomicOr(&flag_s, 1);
+    __syncthreads();
+    if (flag_s) {
+        if (tid < kFDownRows) a.out[d0 + tid] = __builtin_nanf("");
+        return;
+    }
+    stamp(4);
+    down_rows<TD, NBH>(wd, k * kFDownRows, 0, q8h, ys);
+    __syncthreads();
+    if (tid < kFDownRows) {
+        const int r = tid, d = d0 + r;
+        float acc = 0.0f;
+        for (int j = 0; j < k; ++j)
+            acc = acc + __hip_atomic_load(a.wsel + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * ys[j * kFDownRows + r];
+        a.out[d] = acc + a.res[d];
+    }
+    stamp(5);
+}
+
 }  // namespace
 
 // Instantiated shapes: router n_embd 2048; gate/up Q4_K or Q3_K with 8
@@ -344,6 +615,66 @@ hipError_t launch_layer_down(const DownArgs &d, hipStream_t s) {
     HOARD_DOWN(kTypeQ5K, 4, kTypeQ5K)
     HOARD_DOWN(kTypeQ5K, 2, kTypeQ6K)
 #undef HOARD_DOWN
+    return hipErrorInvalidConfiguration;
+}
+
+}  // namespace hoard
+
+namespace hoard {
+
+namespace {
+
+size_t fused_lds_bytes(const FusedLayerArgs &a) {
+    const int nbh = a.down.cols / QK;
+    const size_t gu = 2 * kFGuRows * (size_t)(8 * kQ4KBytes) + 8 * sizeof(Q8L) + 2 * kFGuRows * sizeof(float);
+    const size_t dn = (size_t)a.k * kFDownRows * nbh * block_bytes(a.down.type) + (size_t)a.k * nbh * sizeof(Q8L) +
+                      (size_t)a.k * kFDownRows * sizeof(float);
+    return gu > dn ? gu : dn;
+}
+
+}  // namespace
+
+// The shapes of the fused launch: n_embd 2048, Q4_K gate/up with n_ff a
+// multiple of 16, down Q6_K with 2-4 super-blocks, Q5_K with 2 or 4, or Q4_K
+// with 4 per row; no shared expert; 16-byte aligned tensors and activations.
+bool fused_layer_ok(const FusedLayerArgs &a) {
+    if (a.n_embd != 2048 || a.gate.type != kTypeQ4K || a.up.type != kTypeQ4K || a.gate.rows % kFGuRows ||
+        a.gate.rows != a.up.rows || a.k > 16 || a.k < 1)
+        return false;
+    const int nbh = a.down.cols / QK;
+    const bool q6 = a.down.type == kTypeQ6K && nbh >= 2 && nbh <= 4;
+    const bool q4 = a.down.type == kTypeQ4K && nbh == 4;
+    const bool q5 = a.down.type == kTypeQ5K && (nbh == 2 || nbh == 4);
+    if (!q6 && !q4 && !q5) return false;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.gate.base) | reinterpret_cast<uintptr_t>(a.up.base) |
+                         reinterpret_cast<uintptr_t>(a.down.base) | a.gate.stride | a.up.stride | a.down.stride |
+                         reinterpret_cast<uintptr_t>(a.xin) | reinterpret_cast<uintptr_t>(a.h);
+    return (al & 15) == 0 && fused_lds_bytes(a) <= 65536;
+}
+
+int fused_layer_groups(const FusedLayerArgs &a) {
+    const FusedRoles R = fused_roles(a.E, a.k, a.gate.rows, a.n_embd);
+    return kFXcds * (R.route + R.gu + R.down);
+}
+
+hipError_t launch_fused_layer(const FusedLayerArgs &a, hipStream_t s) {
+    if (!fused_layer_ok(a)) return hipErrorInvalidConfiguration;
+    const int nbh = a.down.cols / QK;
+    const FusedRoles R = fused_roles(a.E, a.k, a.gate.rows, a.n_embd);
+    const unsigned G = (unsigned)(kFXcds * (R.route + R.gu + R.down));
+    const size_t lds = fused_lds_bytes(a);
+#define HOARD_FUSED(TD, NBH)                                                                  \
+    if (a.down.type == TD && nbh == NBH) {                                                    \
+        hipLaunchKernelGGL((fused_layer_kernel<TD, NBH>), dim3(G), dim3(512), lds, s, a);    \
+        return hipGetLastError();                                                             \
+    }
+    HOARD_FUSED(kTypeQ6K, 2)
+    HOARD_FUSED(kTypeQ6K, 3)
+    HOARD_FUSED(kTypeQ6K, 4)
+    HOARD_FUSED(kTypeQ4K, 4)
+    HOARD_FUSED(kTypeQ5K, 2)
+    HOARD_FUSED(kTypeQ5K, 4)
+#undef HOARD_FUSED
     return hipErrorInvalidConfiguration;
 }
 

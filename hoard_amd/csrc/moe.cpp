@@ -106,6 +106,11 @@ struct hoard_moe {
     int persistent_mode = 1;           // HOARD_OPT_PERSISTENT_DECODE value
     int decode_kernel = 0;             // HOARD_OPT_DECODE_KERNEL value
     bool layer_kernels = true;         // HOARD_OPT_LAYER_KERNELS: instantiated per-layer kernels
+    bool layer_fused = true;           // HOARD_OPT_LAYER_FUSED: one launch per layer where it applies
+    bool chip_ok = false;              // gfx950 with 8 XCDs of 32 CUs, every expert resident
+    unsigned long long *fctr = nullptr;  // the one-launch layer's counters, then its error word
+    unsigned long long *ftrace = nullptr;  // its phase stamps while tracing
+    size_t ftrace_words = 0, ftrace_last = 0;
     bool coop_launch = true;           // HOARD_OPT_DECODE_LAUNCH 0: cooperative one-launch decode
     long long wait_ticks = 20000000;   // HOARD_OPT_WAIT_LIMIT_US: bound of the decode's waits (100 MHz ticks)
     hoard::DecodeLayer *d_table = nullptr;  // per-layer pointers of the one-launch decode, kept current
@@ -168,6 +173,8 @@ struct hoard_moe {
         hipFree(pflags);
         hipFree(perr);
         hipFree(seqw);
+        hipFree(fctr);
+        hipFree(ftrace);
         hipFree(ptrace);
         hipHostFree(pin_sel);
         hipFree(slot_ids);
@@ -346,6 +353,57 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
     return HOARD_OK;
 }
 
+// The whole layer in one launch (router, gate/up and down workgroups in the
+// order they start, layer.hip) where the shape and handle admit it: every
+// expert resident, no shared expert.  *done reports whether it ran.  xin is fx,
+// or with rms the residual x whose rms_norm is fx.
+int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, float eps, const float *res, float *out,
+                    int32_t *sel, float *w, hipStream_t s, bool *done) {
+    *done = false;
+    const hoard_moe_cfg &c = h->cfg;
+    if (!h->layer_fused || !h->layer_kernels || !h->chip_ok || c.pool_k > 0 || c.n_ff_shexp > 0) return HOARD_OK;
+    hoard::FusedLayerArgs a{};
+    a.xin = xin;
+    a.rms = rms;
+    a.eps = eps;
+    a.res = res;
+    a.out = out;
+    a.sel = sel;
+    a.wsel = w;
+    a.router = L.router;
+    a.gate = mat(L.gate, L.gstride, L.gate_type, c.n_ff, c.n_embd, c.n_expert);
+    a.up = mat(L.up, L.ustride, L.up_type, c.n_ff, c.n_embd, c.n_expert);
+    a.down = mat(L.down, L.dstride, L.down_type, c.n_embd, c.n_ff, c.n_expert);
+    a.n_embd = c.n_embd;
+    a.E = c.n_expert;
+    a.k = c.n_used;
+    a.renorm = c.renorm;
+    a.logits = h->logits;
+    a.h = h->hbuf;
+    a.ctr = h->fctr;
+    a.err = reinterpret_cast<int *>(h->fctr + hoard::kFusedCounterWords);
+    a.wait_ticks = h->wait_ticks;
+    if (!hoard::fused_layer_ok(a)) return HOARD_OK;
+    if (h->tracing) {
+        // phase stamps of this launch: [workgroup][kFusedStamps] (read with hoard_moe_fused_trace_read)
+        const size_t words = (size_t)hoard::fused_layer_groups(a) * hoard::kFusedStamps;
+        if (h->ftrace_words < words) {
+            hipFree(h->ftrace);
+            h->ftrace = nullptr;
+            if (int rc = dev_alloc((void **)&h->ftrace, words * sizeof(unsigned long long))) return rc;
+            h->ftrace_words = words;
+        }
+        a.trace = h->ftrace;
+        h->ftrace_last = words;
+    }
+    {
+        KernelMark mark(h, HOARD_KERNEL_LAYER, s);
+        HIP_TRY(hoard::launch_fused_layer(a, s));
+    }
+    *done = true;
+    return HOARD_OK;
+}
+
 // Slot pool step for one layer: LRU bookkeeping on the host, uploads of the
 // missed experts on copy_stream (after the previous FFN that read this layer's
 // slots), and `stream` made to wait for them.  slot_dev (optional) receives
@@ -513,6 +571,7 @@ int persistent_setup(hoard_moe *h) {
     if (hipGetDeviceProperties(&prop, h->device) != hipSuccess) return fail(HOARD_ERR_HIP, "device properties");
     cus = prop.multiProcessorCount;
     const bool arch_ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 && cus == kPersistentCus && c.pool_k == 0;
+    h->chip_ok = arch_ok;
     h->xcd_ok = arch_ok && c.n_embd == 2048 && c.n_used == 8 && c.n_expert % 32 == 0 && c.n_expert <= 128 &&
                 c.n_ff % 256 == 0 && c.n_ff <= 1024 && c.n_ff_shexp == 0;
     h->spread_ok = arch_ok && (c.n_ff_shexp == 0 || c.n_ff_shexp == c.n_ff) &&
@@ -640,6 +699,10 @@ int decode_layers(hoard_moe *h, int l0, int l1, float *x_dev, float eps, hipStre
     for (int l = l0; l < l1; ++l) {
         int rc = 0;
         const Layer &L = h->layers[l];
+        bool fused = false;
+        rc = run_layer_fused(h, L, x_dev, 1, eps, x_dev, x_dev, h->sel, h->wsel, s, &fused);
+        if (rc) return rc;
+        if (fused) continue;
         rc = run_route(h, L, x_dev, 1, eps, h->sel, h->wsel, s);
         if (rc) return rc;
         const int32_t *ids = h->sel;
@@ -793,6 +856,9 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     rc = rc ? rc : dev_alloc((void **)&h->wsel, T * c.n_used * sizeof(float));
     rc = rc ? rc : dev_alloc((void **)&h->sgate, T * sizeof(float));
     rc = rc ? rc : dev_alloc((void **)&h->hbuf, (size_t)(c.n_used + 1) * h->hstride * sizeof(float));
+    rc = rc ? rc : dev_alloc((void **)&h->fctr, sizeof(unsigned long long) * (hoard::kFusedCounterWords + 1));
+    if (!rc && hipMemset(h->fctr, 0, sizeof(unsigned long long) * (hoard::kFusedCounterWords + 1)) != hipSuccess)
+        rc = fail(HOARD_ERR_HIP, "hipMemset fused counters");
     if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
     if (!rc && c.pool_k > 0) {
@@ -958,6 +1024,9 @@ int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *r
     float *w = w_dev ? w_dev : h->wsel;
     const Layer &L = h->layers[layer];
     hipStream_t s = (hipStream_t)stream;
+    bool fused = false;
+    rc = run_layer_fused(h, L, fx_dev, 0, 0.0f, res_dev, out_dev, sel, w, s, &fused);
+    if (rc || fused) return rc;
     rc = run_route(h, L, fx_dev, 0, 0.0f, sel, w, s);
     if (rc) return rc;
     const int32_t *ids = sel;
@@ -1341,6 +1410,10 @@ int hoard_moe_set_option(hoard_moe *h, int option, int value) {
         if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "decode launch %d", value);
         h->coop_launch = value == 0;
         return HOARD_OK;
+    case HOARD_OPT_LAYER_FUSED:
+        if (value < 0 || value > 1) return fail(HOARD_ERR_INVALID, "fused layer flag %d", value);
+        h->layer_fused = value != 0;
+        return HOARD_OK;
     case HOARD_OPT_WAIT_LIMIT_US:
         if (value < 0) return fail(HOARD_ERR_INVALID, "wait limit %d us", value);
         h->wait_ticks = 100ll * value;  // the device wall clock runs at 100 MHz
@@ -1389,6 +1462,9 @@ int hoard_moe_get_option(hoard_moe *h, int option, int *value) {
     case HOARD_OPT_WAIT_LIMIT_US:
         *value = (int)(h->wait_ticks / 100);
         return HOARD_OK;
+    case HOARD_OPT_LAYER_FUSED:
+        *value = h->layer_fused ? 1 : 0;
+        return HOARD_OK;
     case HOARD_OPT_FAIL_UPLOAD:
         *value = h->fail_upload;
         return HOARD_OK;
@@ -1401,6 +1477,15 @@ int hoard_moe_sync_check(hoard_moe *h) {
     if (!h) return fail(HOARD_ERR_INVALID, "null handle");
     HIP_TRY(hipSetDevice(h->device));
     HIP_TRY(hipDeviceSynchronize());
+    if (h->fctr) {
+        int err = 0;
+        int *ep = reinterpret_cast<int *>(h->fctr + hoard::kFusedCounterWords);
+        HIP_TRY(hipMemcpy(&err, ep, sizeof(int), hipMemcpyDeviceToHost));
+        if (err) {
+            HIP_TRY(hipMemset(ep, 0, sizeof(int)));
+            return fail(HOARD_ERR_HIP, "one-launch layer: a cross-workgroup wait timed out (output poisoned)");
+        }
+    }
     if (h->perr) {
         int err = 0;
         HIP_TRY(hipMemcpy(&err, h->perr, sizeof(int), hipMemcpyDeviceToHost));
@@ -1428,6 +1513,18 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
     HIP_TRY(hipDeviceSynchronize());
     HIP_TRY(hipMemcpy(out, h->ptrace, words * sizeof(uint64_t), hipMemcpyDeviceToHost));
     *n_layers = h->trace_last;
+    return HOARD_OK;
+}
+
+int hoard_moe_fused_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, size_t *n_words) {
+    if (!h || !out || !n_words) return fail(HOARD_ERR_INVALID, "null argument");
+    *n_words = 0;
+    if (!h->ftrace || !h->ftrace_last) return HOARD_OK;
+    if (max_words < h->ftrace_last) return fail(HOARD_ERR_INVALID, "trace needs %zu words", h->ftrace_last);
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, h->ftrace, h->ftrace_last * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    *n_words = h->ftrace_last;
     return HOARD_OK;
 }
 

@@ -188,6 +188,7 @@ int hoard_moe_pool_ensure_batched(hoard_moe *h, int layer, int n, const int32_t 
 #define HOARD_KERNEL_DOWN 2
 #define HOARD_KERNEL_DECODE 3
 #define HOARD_KERNEL_BATCHED 4 /* the batched path's grouping, MFMA and combine launches together */
+#define HOARD_KERNEL_LAYER 5   /* the one-launch layer (router, gate/up, down and combine) */
 #define HOARD_KERNEL_KINDS 8
 typedef struct hoard_moe_kernel_times {
     uint64_t launches[HOARD_KERNEL_KINDS];
@@ -203,6 +204,14 @@ int hoard_moe_profile(hoard_moe *h, int enable);
    last traced call as [layer][256 workgroups (xcd*32 + rank)][12]. */
 int hoard_moe_phase_trace(hoard_moe *h, int enable);
 int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, int *n_layers);
+/* The same tracing for the one-launch layer (HOARD_OPT_LAYER_FUSED): the stamps
+   of the last traced launch, 6 words per workgroup in XCD-major ticket order:
+   xcd * 65536 + role slot, then the 100 MHz wall clock at its start, three
+   role events and its end.  Role slots count router, gate/up and down
+   workgroups in that order; the events are logits stored / counted / selection
+   published (router), selection seen / rows landed / h stored (gate/up), and
+   selection seen / every h seen / Q8_K(h) formed (down). */
+int hoard_moe_fused_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, size_t *n_words);
 
 /* Options.  HOARD_OPT_PERSISTENT_DECODE selects how hoard_moe_decode runs:
    0 = one launch per kernel per layer, 1 = one cooperative launch per run of
@@ -253,6 +262,16 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
    would: the pool call returns HOARD_ERR_HIP and the layer's slot residency is
    forgotten (its next call uploads every selected expert again).  0 = off. */
 #define HOARD_OPT_FAIL_UPLOAD 9
+/* HOARD_OPT_LAYER_FUSED: 1 (default) = hoard_moe_layer, and hoard_moe_decode
+   when it runs layer by layer, take one launch per layer where the shape
+   admits it (every expert resident, no shared expert, the shapes of
+   HOARD_OPT_LAYER_KERNELS with Q4_K gate/up): router, gate/up and down
+   workgroups run in the order they start, each waiting only on workgroups that
+   started before it, so the launch needs no co-residency and can be captured.
+   Its waits are bounded as HOARD_OPT_WAIT_LIMIT_US says, reported by
+   hoard_moe_sync_check.  0 = the three launches per layer.  Both give the same
+   bits. */
+#define HOARD_OPT_LAYER_FUSED 10
 int hoard_moe_set_option(hoard_moe *h, int option, int value);
 int hoard_moe_get_option(hoard_moe *h, int option, int *value);
 

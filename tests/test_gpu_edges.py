@@ -440,3 +440,34 @@ def test_failed_slot_upload_leaves_pool_consistent():
     finally:
         pool.close()
         res_st.close()
+
+
+def test_fused_layer_wait_limit_zero_gives_up_cleanly(orc):
+    """The one-launch layer's waits with a limit of 0: its gate/up and down
+    workgroups give up at the first missing count, the output is NaN and
+    hoard_moe_sync_check reports HOARD_ERR_HIP; restored, the next calls are exact
+    (the counters stayed in step through the failed launch)."""
+    shape = W.QWEN3_30B
+    layers = {l: W.make_layer(shape, 30, l) for l in range(2)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_LAYER_FUSED) == 1
+        fx, res = W.make_hidden(shape, 30, 0, 0)
+        good, _, _ = st.layer(0, fx, res)
+        st.sync_check()
+        st.set_option(H.OPT_WAIT_LIMIT_US, 0)
+        print("fused layer, wait limit 0", flush=True)
+        out, _, _ = st.layer(0, fx, res)
+        with pytest.raises(H.HoardError) as ei:
+            st.sync_check()
+        assert ei.value.code == H.ERR_HIP
+        assert np.isnan(out).any()
+        st.set_option(H.OPT_WAIT_LIMIT_US, 200000)
+        for _ in range(2):
+            out, _, _ = st.layer(0, fx, res)
+            st.sync_check()
+            assert np.array_equal(out.view(np.uint32), good.view(np.uint32))
+        ref, _, _ = orc.moe_layer(layers[0], fx, res)
+        parity.assert_parity(out, ref, "fused layer after the forced failure")
+    finally:
+        st.close()

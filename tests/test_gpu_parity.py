@@ -324,3 +324,42 @@ def test_decode_splits_the_range_where_layer_types_change(orc):
         assert ei.value.code == H.ERR_UNSUPPORTED
     finally:
         st.close()
+
+
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE], ids=lambda s: s.name)
+def test_fused_layer_matches_three_launches(orc, shape):
+    """hoard_moe_layer in one launch (router, gate/up and down workgroups in the
+    order they start) against the three launches per layer: the same output,
+    selection and weights bit for bit, for several tokens and layers in a row
+    (the launches' counters carry over), and the per-layer decode the same way."""
+    import hoard_amd as H
+    nl = 3
+    layers = {l: W.make_layer(shape, 14, l) for l in range(nl)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_LAYER_FUSED) == 1
+        for t in range(4):
+            for l in range(nl):
+                fx, res = W.make_hidden(shape, 14, l, t)
+                print(f"fused layer {shape.name} token {t} layer {l}", flush=True)
+                st.set_option(H.OPT_LAYER_FUSED, 1)
+                o1, s1, w1 = st.layer(l, fx, res)
+                st.set_option(H.OPT_LAYER_FUSED, 0)
+                o0, s0, w0 = st.layer(l, fx, res)
+                assert np.array_equal(s1, s0) and np.array_equal(w1.view(np.uint32), w0.view(np.uint32))
+                assert np.array_equal(o1.view(np.uint32), o0.view(np.uint32))
+                if t == 0:
+                    ref, sel_o, _ = orc.moe_layer(layers[l], fx, res)
+                    assert np.array_equal(s1, sel_o)
+                    parity.assert_parity(o1, ref, f"fused {shape.name} layer {l}")
+        st.set_option(H.OPT_PERSISTENT_DECODE, 0)
+        _, x = W.make_hidden(shape, 14, 0, 9)
+        st.set_option(H.OPT_LAYER_FUSED, 1)
+        y1 = st.decode(x, 0, nl, W.RMS_EPS)
+        st.sync_check()
+        st.set_option(H.OPT_LAYER_FUSED, 0)
+        y0 = st.decode(x, 0, nl, W.RMS_EPS)
+        assert np.array_equal(y1.view(np.uint32), y0.view(np.uint32))
+    finally:
+        st.set_option(H.OPT_LAYER_FUSED, 1)
+        st.close()
