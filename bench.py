@@ -57,8 +57,10 @@ def parse():
     ap.add_argument("--decode-kernel", default="auto", choices=["auto", "xcd", "spread", "launches"],
                     help="one-launch decode kernel: expert-per-XCD, rows spread over all CUs, or auto; "
                          "'launches' runs the per-layer kernels (hoard_moe_layer's path) instead")
-    ap.add_argument("--decode-launch", default="cooperative", choices=["cooperative", "plain"],
-                    help="how the one-launch decode is launched (plain: for a device holding no other work)")
+    ap.add_argument("--decode-launch", default="plain", choices=["cooperative", "plain"],
+                    help="how the one-launch decode is launched: plain (HOARD_OPT_DECODE_LAUNCH 1) for a "
+                         "caller that owns the device, as this benchmark does; cooperative (the library's "
+                         "default) has the runtime guarantee co-residency and costs about 18 us more a launch")
     ap.add_argument("--phases", action="store_true", help="trace one-launch decode phases of one token")
     ap.add_argument("--pool", type=int, default=0, metavar="K",
                     help="slot-pool workload: K HBM slots per layer, all experts in pinned host memory, "
