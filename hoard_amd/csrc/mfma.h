@@ -101,8 +101,8 @@ __device__ __forceinline__ void q4_compute(const Q4Ops &o, float acc[4], float a
         const v4i d = mfma_16x16x32(a, o.xb[s]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            isum[i] += imul24(byte_of(sc[i][s >> 2], s & 3), d[i]);
-            msum[i] += imul24(byte_of(mn[i][s >> 2], s & 3), bs[s]);
+            isum[i] += byte_of(sc[i][s >> 2], s & 3) * d[i];
+            msum[i] += byte_of(mn[i][s >> 2], s & 3) * bs[s];
         }
     }
 #pragma unroll
@@ -185,7 +185,7 @@ __device__ __forceinline__ void q6_tile_block(const uint8_t *T, size_t rb, int b
         for (int i = 0; i < 4; ++i) {
             const uint8_t *blk_i = T + (size_t)(4 * q + i) * rb + (size_t)b * kQ6KBytes;
             const int sc0 = (int)(int8_t)blk_i[192 + 2 * s], sc1 = (int)(int8_t)blk_i[193 + 2 * s];
-            isum[i] += imul24(sc0, d0[i] - 32 * bs[2 * s]) + imul24(sc1, d1[i] - 32 * bs[2 * s + 1]);
+            isum[i] += sc0 * (d0[i] - 32 * bs[2 * s]) + sc1 * (d1[i] - 32 * bs[2 * s + 1]);
         }
     }
 #pragma unroll

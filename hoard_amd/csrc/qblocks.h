@@ -67,12 +67,6 @@ struct Q8Block {
 };
 static_assert(sizeof(Q8Block) == 292, "block_q8_K is 292 bytes");
 
-// Product of two integers whose magnitudes are below 2^23 (scales times
-// sub-block sums): v_mul_i32_i24, a full-rate instruction, where a plain int
-// multiply becomes the quarter-rate v_mul_lo_u32.  Exact while the product
-// fits 32 bits, as every scale product of the K-quant dots does.
-__device__ __forceinline__ int imul24(int a, int b) { return __mul24(a, b); }
-
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }

@@ -59,10 +59,10 @@ __device__ __forceinline__ float g8_row_q4k(const uint8_t *row, const Q8L *x, in
         int sc0, m0, sc1, m1;
         q4k_scale_min(2 * c, hd.y, hd.z, hd.w, sc0, m0);
         q4k_scale_min(2 * c + 1, hd.y, hd.z, hd.w, sc1, m1);
-        int isum = imul24(sc0, lo) + imul24(sc1, hi);
+        int isum = sc0 * lo + sc1 * hi;
         int msum = h ? 0
-                     : imul24(m0, (int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
-                           imul24(m1, (int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
+                     : m0 * ((int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
+                           m1 * ((int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
         isum = group8_sum(isum);
         msum = group8_sum(msum);
         const float d = half_bits_to_float(hd.x & 0xffffu) * xb.d;
@@ -100,10 +100,10 @@ __device__ __forceinline__ float g8_row_q5k(const uint8_t *row, const Q8L *x, in
         int sc0, m0, sc1, m1;
         q4k_scale_min(2 * c, hd.y, hd.z, hd.w, sc0, m0);
         q4k_scale_min(2 * c + 1, hd.y, hd.z, hd.w, sc1, m1);
-        int isum = imul24(sc0, lo) + imul24(sc1, hi);
+        int isum = sc0 * lo + sc1 * hi;
         int msum = h ? 0
-                     : imul24(m0, (int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
-                           imul24(m1, (int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
+                     : m0 * ((int)xb.bsums[4 * c] + (int)xb.bsums[4 * c + 1]) +
+                           m1 * ((int)xb.bsums[4 * c + 2] + (int)xb.bsums[4 * c + 3]);
         isum = group8_sum(isum);
         msum = group8_sum(msum);
         const float d = half_bits_to_float(hd.x & 0xffffu) * xb.d;
@@ -147,7 +147,7 @@ __device__ __forceinline__ float g8_row_q6k(const uint8_t *row, const Q8L *x, in
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int g = 8 * n + 2 * i + (lh >> 1);
-            isum += imul24((int)(int8_t)blk[192 + g], s[i] - 32 * z[i]);
+            isum += (int)(int8_t)blk[192 + g] * (s[i] - 32 * z[i]);
         }
         isum = group8_sum(isum);
         const uint32_t dbits = (uint32_t)blk[208] | ((uint32_t)blk[209] << 8);
@@ -198,7 +198,7 @@ __device__ __forceinline__ int q6k_block_isum_g8(const uint8_t *blk, const Q8L &
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int g = 8 * n + 2 * i + (lh >> 1);
-        isum += imul24((int)(int8_t)blk[192 + g], s[i] - 32 * z[i]);
+        isum += (int)(int8_t)blk[192 + g] * (s[i] - 32 * z[i]);
     }
     return isum;
 }
@@ -315,8 +315,8 @@ __device__ __forceinline__ void q4k_block_sums(const uint8_t *blk, const Q8Reg &
                 sc = (byte(s + 4) & 0x0f) | ((byte(s - 4) >> 6) << 4);
                 mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
             }
-            isum += imul24(sc, h ? hi : lo);
-            msum += imul24(mn, x.bs[s]);
+            isum += sc * (h ? hi : lo);
+            msum += mn * x.bs[s];
         }
     }
 }
