@@ -693,7 +693,9 @@ def main():
     result["config"]["decode_path"] = (
         (f"one {args.decode_launch} launch per token, " + ("expert rows spread over all CUs" if spread
                                                            else "one expert per XCD"))
-        if "decode_persistent" in kernels else "router, gate/up and down+combine launches per layer")
+        if "decode_persistent" in kernels else
+        "one launch per layer (router, gate/up and down workgroups in ticket order)" if "layer_fused" in kernels else
+        "router, gate/up and down+combine launches per layer")
     if args.phases:
         ph = phase_breakdown(lib, h, lambda: step(warm), H, PHASES_SPREAD if spread else PHASES)
         if ph:

@@ -131,13 +131,15 @@ int hoard_moe_layer(hoard_moe *h, int layer, const float *fx_dev, const float *r
 int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev, float eps,
                      void *stream);
 
-/* Batched expert stage for M tokens (1 <= M <= min(max_tokens, 16)), every
+/* Batched expert stage for M tokens (1 <= M <= min(max_tokens, 512)), every
    token routed independently: the counterpart of ggml_mul_mat_id over the
    experts with per-token ids and the weighted sum over them
    (src/run_specloop.cpp:126-139, src/run_m1.cpp:97-108).  The (token, slot)
    pairs are grouped by expert so each selected expert's weights are read once
-   per call, and the expert products run on int8 MFMA; each token's result is
-   the single-token hoard_moe_layer's bit for bit.  fx_dev, res_dev, out_dev:
+   per call (per 64 pairs above 16 tokens, where the pairs are sorted by
+   expert into 64-pair units), and the expert products run on per-token int8
+   dots or int8 MFMA; each token's result is the single-token
+   hoard_moe_layer's bit for bit.  M > 512 returns HOARD_ERR_INVALID.  fx_dev, res_dev, out_dev:
    [M][n_embd] (out may alias res); sel_dev / w_dev ([M][n_used]) receive the
    routing when non-NULL.  The call's per-expert token histogram and unique
    expert count are reported by hoard_moe_get_stats.  Needs pool_k == 0 and no
@@ -166,7 +168,8 @@ int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const floa
    given (no renormalisation).  out[t] = res[t] + sum_j w[t][j] y(ids[t][j]), j
    ascending.  A token may repeat an id (the verify loop pads with a repeated id
    of weight 0); a token with an id outside the pool or expert set gets a NaN
-   row.  Each token's result equals hoard_moe_ffn_combine's for that token. */
+   row.  1 <= M <= min(max_tokens, 512).  Each token's result equals
+   hoard_moe_ffn_combine's for that token. */
 int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const int32_t *ids_dev,
                                   const float *w_dev, const float *res_dev, float *out_dev, void *stream);
 
