@@ -281,6 +281,10 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 // only for roles with lower tickets on its own XCD, which started before it,
 // or for roles that come first on every XCD, which need nothing from later
 // ones; so every wait ends whatever the number of workgroups resident at once.
+// The last router workgroup to finish publishes "logits complete"; every
+// gate/up and down workgroup then forms the top-k itself from the logits (the
+// same code on the same words, so the same experts and weights), and the last
+// router workgroup forms it once more for the caller's sel / wsel.
 // The counters grow across launches: launch e (ticket / workgroups per XCD)
 // waits for the counts of launch e.  Every value crosses workgroups through
 // device-scope stores and loads (past the per-XCD L2), each counted only after
@@ -295,7 +299,7 @@ constexpr int kFXcds = 8;
 constexpr int kFCtrTicket = 0;               // line x: tickets of XCD x
 constexpr int kFCtrRoute = 16 * 8;           // router workgroups done
 constexpr int kFCtrH = 16 * 9;               // line 9 + j: gate/up workgroups of slot j done
-constexpr int kFCtrSel = 16 * 25;            // line 25 + x: the selection published, copy for XCD x
+constexpr int kFCtrSel = 16 * 25;            // line 25 + x: the logits complete, copy for XCD x
 constexpr int kFCtrHDone = 16 * 33;          // line 33 + x, word j: slot j's h complete, copy for XCD x
 static_assert(kFCtrHDone + 16 * kFXcds == kFusedCounterWords, "counter lines");
 
@@ -360,8 +364,87 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __shared__ unsigned long long tk_s;
     __shared__ int flag_s;
     __shared__ double red[8];
+    __shared__ int sel_s[16];
+    __shared__ float w_s[16];
+    __shared__ float ps[128];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, k = a.k, nff = a.gate.rows;
+    // The selection in the gate/up and down roles.  select_a (wave 0) waits
+    // until every logit of this launch is stored; with E <= 128 it forms the
+    // softmax into ps, as router_tail does (the same loads, reductions and
+    // scale), and select_b (every thread) ranks it: expert e's rank is the
+    // number of experts of larger probability or of equal probability and a
+    // lower index, the order of router_tail's repeated maxima, and ranks below
+    // k fill sel_s / w_s.  With E > 128 wave 0 runs router_tail itself.  A
+    // wait that ran out raises flag_s instead.  w_s holds the raw top-k
+    // probabilities until select_renorm.
+    const bool rank_sel = E <= 128;
+    auto select_a = [&](unsigned long long epoch) {
+        int failed = 0;
+        if (lane == 0) failed = wait_count(a.ctr + kFCtrSel + 16 * xcc_id(), epoch, a.err, a.wait_ticks) ? 0 : 1;
+        failed = __builtin_amdgcn_readfirstlane(failed);
+        if (failed) {
+            if (lane == 0) flag_s = 1;
+            return;
+        }
+        if (!rank_sel) {
+            router_tail<true, false>(a.logits, E, k, a.renorm, sel_s, w_s, 0);
+            return;
+        }
+        float p0 = lane < E ? __hip_atomic_load(a.logits + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : -INFINITY;
+        float p1 = lane + 64 < E
+                       ? __hip_atomic_load(a.logits + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : -INFINITY;
+        const float mx = wave_max_f(p0 > p1 ? p0 : p1);
+        double sum = 0.0;
+        if (lane < E) {
+            p0 = expf(p0 - mx);
+            sum += (double)p0;
+        }
+        if (lane + 64 < E) {
+            p1 = expf(p1 - mx);
+            sum += (double)p1;
+        }
+        sum = wave_sum_d(sum);
+        const float sc = (float)(1.0 / sum);
+        ps[lane] = lane < E ? p0 * sc : -1.0f;  // absent experts below every probability
+        ps[lane + 64] = lane + 64 < E ? p1 * sc : -1.0f;
+        if (lane < 16) sel_s[lane] = -1;
+    };
+    auto select_b = [&]() {
+        if (!rank_sel || flag_s) return;
+        const int e = tid >> 2, q = tid & 3;  // four threads per expert, 32 comparisons each
+        const float pe = ps[e];
+        int r = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 v = *reinterpret_cast<const float4 *>(ps + 32 * q + 4 * c);
+            const int e4 = 32 * q + 4 * c;
+            r += (v.x > pe) | ((v.x == pe) & (e4 < e));
+            r += (v.y > pe) | ((v.y == pe) & (e4 + 1 < e));
+            r += (v.z > pe) | ((v.z == pe) & (e4 + 2 < e));
+            r += (v.w > pe) | ((v.w == pe) & (e4 + 3 < e));
+        }
+        r = group4_sum(r);
+        if (e < E && q == 0 && r < k) {
+            sel_s[r] = e;
+            w_s[r] = pe;
+        }
+    };
+    // (wave 0, after the rank is visible) router_tail's renorm of the weights
+    auto select_renorm = [&]() {
+        if (!rank_sel || !a.renorm) return;
+        float ws = 0.0f, wj = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            const float v = w_s[j];
+            ws = ws + v;
+            if (j == lane) wj = v;
+        }
+        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every lane has read w_s
+        if (lane < k) w_s[lane] = wj / ws;
+    };
     const unsigned xcc = xcc_id();
     const FusedRoles R = fused_roles(E, k, nff, N);
     const unsigned long long Gx = (unsigned long long)(R.route + R.gu + R.down);
@@ -406,12 +489,11 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             stamp(5);
             return;
         }
-        // the last router workgroup: softmax, top-k, renorm; then the selection is
-        // published to every XCD
+        // the last router workgroup: every logit is acknowledged, so "complete"
+        // goes to every XCD at once; then the caller's sel / wsel
         if (wave == 0) {
-            router_tail<true>(a.logits, E, k, a.renorm, a.sel, a.wsel, 0);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             if (lane < kFXcds) ctr_store(a.ctr + kFCtrSel + 16 * lane, ep + 1ull);
+            router_tail<true>(a.logits, E, k, a.renorm, a.sel, a.wsel, 0);
         }
         stamp(4);
         stamp(5);
@@ -434,12 +516,14 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
                 const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
                 wave_quantize_q8l_regs(v, &q8[b]);
             }
-        } else if (tid == 0) {
-            if (!wait_count(a.ctr + kFCtrSel + 16 * xcc, ep + 1ull, a.err, a.wait_ticks)) flag_s = 1;
-            stamp(2);
+        } else if (wave == 0) {
+            select_a(ep + 1ull);
         }
         __syncthreads();
-        const int id = __hip_atomic_load(a.sel + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        select_b();
+        __syncthreads();
+        stamp(2);
+        const int id = sel_s[j];
         const bool bad = flag_s || id < 0 || id >= a.gate.n_ids;
         if (!bad && wave < 4) {
             // gate rows on waves 0-1, up rows on waves 2-3
@@ -485,13 +569,16 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     uint8_t *wd = smem;  // [k][8 rows]
     Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes);
     float *ys = reinterpret_cast<float *>(q8h + k * NBH);
-    if (tid == 0 && !wait_count(a.ctr + kFCtrSel + 16 * xcc, ep + 1ull, a.err, a.wait_ticks)) flag_s = 1;
+    if (wave == 0) select_a(ep + 1ull);
     __syncthreads();
+    select_b();
+    __syncthreads();
+    if (wave == 0) select_renorm();
     stamp(2);
     int bad = flag_s;
     for (int u = wave; u < k; u += 8) {
         // expert u's 8 rows from wave u: copies in different pages do not wait on each other
-        const int id = __hip_atomic_load(a.sel + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int id = sel_s[u];
         if (id < 0 || id >= a.down.n_ids) {
             bad = 1;
             continue;
@@ -536,8 +623,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     if (tid < kFDownRows) {
         const int r = tid, d = d0 + r;
         float acc = 0.0f;
-        for (int j = 0; j < k; ++j)
-            acc = acc + __hip_atomic_load(a.wsel + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * ys[j * kFDownRows + r];
+        for (int j = 0; j < k; ++j) acc = acc + w_s[j] * ys[j * kFDownRows + r];
         a.out[d] = acc + a.res[d];
     }
     stamp(5);

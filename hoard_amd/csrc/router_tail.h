@@ -19,11 +19,13 @@ constexpr int kMaxK = 16;
 // and the top-k argmax are order-independent; the double-precision sum of
 // the probabilities is exact unless they span more than 2^29 in magnitude,
 // and its float reciprocal absorbs the remaining rounding differences.
-// AGENT: the logits come from other workgroups of the same launch and sel /
-// wsel go to one: they are read and written at device (agent) scope, which
-// bypasses the per-XCD L2, instead of behind a cache-flushing fence.
+// AGENT: the logits come from other workgroups of the same launch and are read
+// at device (agent) scope, which bypasses the per-XCD L2, instead of behind a
+// cache-flushing fence.  STORE_AGENT: sel / wsel go to other workgroups and
+// are written at device scope; otherwise plain stores (global memory of this
+// workgroup's own use, or LDS).
 // NT: experts per lane the body is compiled for (E <= 64 NT, E <= 1024).
-template <bool AGENT, int NT>
+template <bool AGENT, int NT, bool STORE_AGENT = AGENT>
 __device__ inline void router_tail_nt(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel,
                                       int tok) {
     const int lane = threadIdx.x & 63;
@@ -96,7 +98,7 @@ __device__ inline void router_tail_nt(const float *logits, int E, int k, int ren
         my_w = my_w / ws;
     }
     if (lane < k) {
-        if constexpr (AGENT) {
+        if constexpr (STORE_AGENT) {
             __hip_atomic_store(sel + (size_t)tok * k + lane, my_sel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(wsel + (size_t)tok * k + lane, my_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
@@ -106,18 +108,18 @@ __device__ inline void router_tail_nt(const float *logits, int E, int k, int ren
     }
 }
 
-template <bool AGENT = false>
+template <bool AGENT = false, bool STORE_AGENT = AGENT>
 __device__ inline void router_tail(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel, int tok) {
     if (E <= 64)
-        router_tail_nt<AGENT, 1>(logits, E, k, renorm, sel, wsel, tok);
+        router_tail_nt<AGENT, 1, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 128)
-        router_tail_nt<AGENT, 2>(logits, E, k, renorm, sel, wsel, tok);
+        router_tail_nt<AGENT, 2, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 256)
-        router_tail_nt<AGENT, 4>(logits, E, k, renorm, sel, wsel, tok);
+        router_tail_nt<AGENT, 4, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 512)
-        router_tail_nt<AGENT, 8>(logits, E, k, renorm, sel, wsel, tok);
+        router_tail_nt<AGENT, 8, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else
-        router_tail_nt<AGENT, kMaxExpertsPerLane>(logits, E, k, renorm, sel, wsel, tok);
+        router_tail_nt<AGENT, kMaxExpertsPerLane, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
 }
 
 }  // namespace hoard
