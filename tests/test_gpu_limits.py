@@ -25,6 +25,9 @@ CASES = [
     W.Shape("e61_k7", 9, 2048, 61, 7, 768, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1),
     W.Shape("e60_k4_shared", 10, 2048, 60, 4, 1536, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1,
             n_ff_shexp=1024),
+    # more than 128 experts without a shared expert: the one-launch layer's gate/up
+    # and down workgroups run the one-wave router tail instead of the rank
+    W.Shape("e256_k8", 11, 2048, 256, 8, 512, 1, H.TYPE_Q4_K, H.TYPE_Q4_K, H.TYPE_Q6_K, 1),
 ]
 
 

@@ -326,7 +326,11 @@ def test_decode_splits_the_range_where_layer_types_change(orc):
         st.close()
 
 
-@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE], ids=lambda s: s.name)
+# more than 128 experts: the one-launch layer's waiting workgroups run the router tail
+E256 = W.Shape("e256_k8", 11, 2048, 256, 8, 512, 1, W.TYPE_Q4_K, W.TYPE_Q4_K, W.TYPE_Q6_K, 1)
+
+
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE, E256], ids=lambda s: s.name)
 def test_fused_layer_matches_three_launches(orc, shape):
     """hoard_moe_layer in one launch (router, gate/up and down workgroups in the
     order they start) against the three launches per layer: the same output,
