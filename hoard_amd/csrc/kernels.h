@@ -205,7 +205,7 @@ struct FusedLayerArgs {
     const float *router;       // [E][n_embd]
     MatDesc gate, up, down;    // routed experts (stride per expert)
     int n_embd, E, k, renorm;
-    float *logits;             // [E] scratch
+    uint64_t *lgw;             // [8][E] logits as tagged words {value, launch epoch}, one copy per XCD
     float *h;                  // [k][n_ff] scratch
     unsigned long long *ctr;   // kFusedCounterWords zeroed words: tickets, completion counts and flags
     int *err;                  // raised by a wait that runs out
@@ -213,7 +213,7 @@ struct FusedLayerArgs {
     unsigned long long *trace; // optional [workgroup][kFusedStamps] wall-clock stamps, by ticket order per XCD
 };
 constexpr int kFusedStamps = 6;  // xcd * 65536 + role slot, start, 3 role events, end
-constexpr int kFusedCounterWords = 16 * (8 + 1 + 16 + 8 + 8);
+constexpr int kFusedCounterWords = 16 * (8 + 16 + 8);
 bool fused_layer_ok(const FusedLayerArgs &a);
 int fused_layer_groups(const FusedLayerArgs &a);  // workgroups of one launch
 hipError_t launch_fused_layer(const FusedLayerArgs &a, hipStream_t s);

@@ -281,10 +281,11 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 // only for roles with lower tickets on its own XCD, which started before it,
 // or for roles that come first on every XCD, which need nothing from later
 // ones; so every wait ends whatever the number of workgroups resident at once.
-// The last router workgroup to finish publishes "logits complete"; every
-// gate/up and down workgroup then forms the top-k itself from the logits (the
-// same code on the same words, so the same experts and weights), and the last
-// router workgroup forms it once more for the caller's sel / wsel.
+// Router workgroups store their logits as tagged words {value, launch
+// epoch}, one copy per XCD; every gate/up and down workgroup polls its XCD's
+// copy of all of them and forms the top-k itself (the same code on the same
+// words, so the same experts and weights), and the first down workgroup of
+// XCD 0 forms it once more for the caller's sel / wsel.
 // The counters grow across launches: launch e (ticket / workgroups per XCD)
 // waits for the counts of launch e.  Every value crosses workgroups through
 // device-scope stores and loads (past the per-XCD L2), each counted only after
@@ -297,10 +298,8 @@ constexpr int kFDownRows = 8;   // output rows per down workgroup
 constexpr int kFXcds = 8;
 // counter words (16 to a 128-byte line)
 constexpr int kFCtrTicket = 0;               // line x: tickets of XCD x
-constexpr int kFCtrRoute = 16 * 8;           // router workgroups done
-constexpr int kFCtrH = 16 * 9;               // line 9 + j: gate/up workgroups of slot j done
-constexpr int kFCtrSel = 16 * 25;            // line 25 + x: the logits complete, copy for XCD x
-constexpr int kFCtrHDone = 16 * 33;          // line 33 + x, word j: slot j's h complete, copy for XCD x
+constexpr int kFCtrH = 16 * 8;               // line 8 + j: gate/up workgroups of slot j done
+constexpr int kFCtrHDone = 16 * 24;          // line 24 + x, word j: slot j's h complete, copy for XCD x
 static_assert(kFCtrHDone + 16 * kFXcds == kFusedCounterWords, "counter lines");
 
 __device__ __forceinline__ unsigned long long ctr_load(const unsigned long long *p) {
@@ -367,6 +366,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
     __shared__ float ps[128];
+    __shared__ float lg_s[1024];  // this launch's logits, gathered from the XCD's tagged copy
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, k = a.k, nff = a.gate.rows;
     // The selection in the gate/up and down roles.  select_a (wave 0) waits
@@ -380,22 +380,39 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     // probabilities until select_renorm.
     const bool rank_sel = E <= 128;
     auto select_a = [&](unsigned long long epoch) {
-        int failed = 0;
-        if (lane == 0) failed = wait_count(a.ctr + kFCtrSel + 16 * xcc_id(), epoch, a.err, a.wait_ticks) ? 0 : 1;
-        failed = __builtin_amdgcn_readfirstlane(failed);
-        if (failed) {
+        // every logit of this launch, from this XCD's copy: lanes take experts
+        // lane, lane + 64, ...; a probe that finds a word of an earlier launch
+        // sleeps and probes again
+        const unsigned tg = (unsigned)epoch;
+        const uint64_t *src = a.lgw + (size_t)xcc_id() * E;
+        const int per = (E + 63) >> 6;
+        const bool got = poll(
+            [&]() {
+                bool r = true;
+                for (int t = 0; t < per; ++t) {
+                    const int e = lane + 64 * t;
+                    if (e < E) {
+                        const uint64_t w = ld_dev64(src + e);
+                        r = r & (tag_seq(w) == tg);
+                        lg_s[e] = tag_val(w);
+                    }
+                }
+                if (__all(r)) return true;
+                __builtin_amdgcn_s_sleep(2);
+                return false;
+            },
+            a.err, a.wait_ticks);
+        if (!got) {
             if (lane == 0) flag_s = 1;
             return;
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // lg_s written by this wave
         if (!rank_sel) {
-            router_tail<true, false>(a.logits, E, k, a.renorm, sel_s, w_s, 0);
+            router_tail<false, false>(lg_s, E, k, a.renorm, sel_s, w_s, 0);
             return;
         }
-        float p0 = lane < E ? __hip_atomic_load(a.logits + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                            : -INFINITY;
-        float p1 = lane + 64 < E
-                       ? __hip_atomic_load(a.logits + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : -INFINITY;
+        float p0 = lane < E ? lg_s[lane] : -INFINITY;
+        float p1 = lane + 64 < E ? lg_s[lane + 64] : -INFINITY;
         const float mx = wave_max_f(p0 > p1 ? p0 : p1);
         double sum = 0.0;
         if (lane < E) {
@@ -466,35 +483,36 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
 
     if (lt < R.route) {
         // -- router rows [4 i, +4): a half-wave per row in ggml's x86 f32 order --
+        // the rows (waves 0-3, one each) and x (wave 4) go to LDS in one burst,
+        // so every load is in flight at once
         const int i = (int)xcc * R.route + lt;
+        const int nrows = min(kFRouteRows, E - i * kFRouteRows);
+        float *wl = reinterpret_cast<float *>(smem);  // [4][N]
+        float *xl = wl + kFRouteRows * N;             // [N]
+        if (wave < nrows)
+            wave_copy(reinterpret_cast<uint8_t *>(wl + wave * N),
+                      reinterpret_cast<const uint8_t *>(a.router + (size_t)(i * kFRouteRows + wave) * N), N * 4);
+        else if (wave == kFRouteRows)
+            wave_copy(reinterpret_cast<uint8_t *>(xl), reinterpret_cast<const uint8_t *>(a.xin), N * 4);
         const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
-        const int row = i * kFRouteRows + (tid >> 5), l = tid & 31;
-        if (tid < 32 * kFRouteRows && row < E) {
-            const float *wr = a.router + (size_t)row * N + l;
-            const float *xr = a.xin + l;
+        lds_dma_wait();
+        __syncthreads();
+        const int rr = tid >> 5, row = i * kFRouteRows + rr, l = tid & 31;
+        if (rr < nrows) {
+            const float *wr = wl + rr * N + l;
+            const float *xr = xl + l;
             float acc = 0.0f;
 #pragma unroll 16
             for (int c = 0; c < N; c += 32) acc = fmaf(wr[c], xr[c] * scale, acc);
             acc = acc + __shfl_xor(acc, 16);
             acc = row16_ggml_fold(acc);
-            if (l == 0) __hip_atomic_store(a.logits + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // the logit is exact in the half-wave's first lane; lanes 0..7 of the
+            // half-wave store the copies of the 8 XCDs
+            const float lv = __shfl(acc, lane & 32);
+            if (l < kFXcds) st_dev64(a.lgw + (size_t)l * E + row, tag(lv, (unsigned)(ep + 1ull)));
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logits are acknowledged
-        __syncthreads();
         stamp(2);
-        if (tid == 0) flag_s = ctr_add(a.ctr + kFCtrRoute) + 1ull == (ep + 1ull) * (unsigned long long)n_route;
-        __syncthreads();
         stamp(3);
-        if (!flag_s) {
-            stamp(5);
-            return;
-        }
-        // the last router workgroup: every logit is acknowledged, so "complete"
-        // goes to every XCD at once; then the caller's sel / wsel
-        if (wave == 0) {
-            if (lane < kFXcds) ctr_store(a.ctr + kFCtrSel + 16 * lane, ep + 1ull);
-            router_tail<true>(a.logits, E, k, a.renorm, a.sel, a.wsel, 0);
-        }
         stamp(4);
         stamp(5);
         return;
@@ -575,6 +593,10 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     if (wave == 0) select_renorm();
     stamp(2);
+    // the first down workgroup of XCD 0 also gives the caller sel / wsel, formed
+    // from the gathered logits as the route kernel forms them (a selection that
+    // could not be gathered reads as no expert, weight NaN)
+    const bool caller_sel = xcc == 0 && lt == R.route + R.gu;
     int bad = flag_s;
     for (int u = wave; u < k; u += 8) {
         // expert u's 8 rows from wave u: copies in different pages do not wait on each other
@@ -585,6 +607,16 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         }
         if (!flag_s) wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kDnRowBytes,
                                kSegBytes);
+    }
+    if (caller_sel && wave == 0) {
+        if (flag_s) {
+            if (lane < k) {
+                a.sel[lane] = 0x7fffffff;
+                a.wsel[lane] = __builtin_nanf("");
+            }
+        } else {
+            router_tail<false, false>(lg_s, E, k, a.renorm, a.sel, a.wsel, 0);
+        }
     }
     if (wave == 0 && !flag_s) {
         // every slot's h complete: lane j watches slot j's word of this XCD's line
@@ -715,7 +747,9 @@ size_t fused_lds_bytes(const FusedLayerArgs &a) {
     const size_t gu = 2 * kFGuRows * (size_t)(8 * kQ4KBytes) + 8 * sizeof(Q8L) + 2 * kFGuRows * sizeof(float);
     const size_t dn = (size_t)a.k * kFDownRows * nbh * block_bytes(a.down.type) + (size_t)a.k * nbh * sizeof(Q8L) +
                       (size_t)a.k * kFDownRows * sizeof(float);
-    return gu > dn ? gu : dn;
+    const size_t rt = (size_t)(kFRouteRows + 1) * a.n_embd * sizeof(float);  // router rows and x
+    const size_t m = gu > dn ? gu : dn;
+    return m > rt ? m : rt;
 }
 
 }  // namespace

@@ -109,6 +109,7 @@ struct hoard_moe {
     bool layer_fused = true;           // HOARD_OPT_LAYER_FUSED: one launch per layer where it applies
     bool chip_ok = false;              // gfx950 with 8 XCDs of 32 CUs, every expert resident
     unsigned long long *fctr = nullptr;  // the one-launch layer's counters, then its error word
+    uint64_t *flgw = nullptr;            // its tagged logits, one copy per XCD
     unsigned long long *ftrace = nullptr;  // its phase stamps while tracing
     size_t ftrace_words = 0, ftrace_last = 0;
     bool coop_launch = true;           // HOARD_OPT_DECODE_LAUNCH 0: cooperative one-launch decode
@@ -174,6 +175,7 @@ struct hoard_moe {
         hipFree(perr);
         hipFree(seqw);
         hipFree(fctr);
+        hipFree(flgw);
         hipFree(ftrace);
         hipFree(ptrace);
         hipHostFree(pin_sel);
@@ -378,7 +380,7 @@ int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, flo
     a.E = c.n_expert;
     a.k = c.n_used;
     a.renorm = c.renorm;
-    a.logits = h->logits;
+    a.lgw = h->flgw;
     a.h = h->hbuf;
     a.ctr = h->fctr;
     a.err = reinterpret_cast<int *>(h->fctr + hoard::kFusedCounterWords);
@@ -859,6 +861,10 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     rc = rc ? rc : dev_alloc((void **)&h->fctr, sizeof(unsigned long long) * (hoard::kFusedCounterWords + 1));
     if (!rc && hipMemset(h->fctr, 0, sizeof(unsigned long long) * (hoard::kFusedCounterWords + 1)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset fused counters");
+    // tags start at 0 and the first launch's epoch tag is 1: zeroed words never match
+    rc = rc ? rc : dev_alloc((void **)&h->flgw, sizeof(uint64_t) * 8 * c.n_expert);
+    if (!rc && hipMemset(h->flgw, 0, sizeof(uint64_t) * 8 * c.n_expert) != hipSuccess)
+        rc = fail(HOARD_ERR_HIP, "hipMemset fused logits");
     if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
     if (!rc && c.pool_k > 0) {
