@@ -69,15 +69,14 @@ __device__ __forceinline__ double row16_sum_d(double v) {
     v = v + dpp_d<kDppRowMirror>(v);
     return v;
 }
+// v_max_f32 (fmaxf) per step, one instruction where a compare and a select
+// were two on the dependent chain; a NaN lane never wins unless every lane is
+// NaN (the callers sanitise or only meet all-NaN inputs).
 __device__ __forceinline__ float row16_max_f(float v) {
-    float o = dpp_f<kDppQuadXor1>(v);
-    v = o > v ? o : v;
-    o = dpp_f<kDppQuadXor2>(v);
-    v = o > v ? o : v;
-    o = dpp_f<kDppRowHalfMirror>(v);
-    v = o > v ? o : v;
-    o = dpp_f<kDppRowMirror>(v);
-    v = o > v ? o : v;
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
     return v;
 }
 
@@ -88,12 +87,8 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 __device__ __forceinline__ float wave_max_f(float v) {
     v = row16_max_f(v);
-    float m = readlane_f(v, 0);
-    const float a = readlane_f(v, 16), b = readlane_f(v, 32), c = readlane_f(v, 48);
-    m = a > m ? a : m;
-    m = b > m ? b : m;
-    m = c > m ? c : m;
-    return m;
+    const float a = readlane_f(v, 0), b = readlane_f(v, 16), c = readlane_f(v, 32), d = readlane_f(v, 48);
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // Wave-uniform argmax of (value, index): larger value first, lower index on
