@@ -204,9 +204,12 @@ struct FusedLayerArgs {
     float *wsel;               // [k] their weights (written)
     const float *router;       // [E][n_embd]
     MatDesc gate, up, down;    // routed experts (stride per expert)
+    MatDesc sh_gate, sh_up, sh_down;  // the shared expert (sh_gate.base == nullptr: none)
+    const float *sh_gate_inp;  // [n_embd] f32 gate row of the shared expert
+    float *sgate;              // [1] scratch: sigmoid(sh_gate_inp . fx)
     int n_embd, E, k, renorm;
     uint64_t *lgw;             // [8][E] logits as tagged words {value, launch epoch}, one copy per XCD
-    float *h;                  // [k][n_ff] scratch
+    float *h;                  // [k (+1 shared)][n_ff] scratch
     unsigned long long *ctr;   // kFusedCounterWords zeroed words: tickets, completion counts and flags
     int *err;                  // raised by a wait that runs out
     long long wait_ticks;

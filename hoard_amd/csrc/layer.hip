@@ -178,23 +178,25 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
 
 // -- down + combine -----------------------------------------------------------
 // Rows [0, n) of type T with NB super-blocks, row r at base + r * row bytes,
-// dotted with unit (u0 + r / 8)'s Q8_K(h); results to ys[u0 * 8 + r].
-template <int T, int NB>
+// dotted with unit (u0 + r / 8)'s Q8_K(h); results to ys[u0 * 8 + r].  NT
+// threads of the workgroup take part.
+template <int T, int NB, int NT>
 __device__ __forceinline__ void down_rows(const uint8_t *base, int n, int u0, const Q8L *q8h, float *ys) {
+    static_assert(NT % 128 == 0, "whole wave pairs");
     constexpr int kRowBytes = NB * QType<T>::bytes;
     const int wave = threadIdx.x >> 6, grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
     if constexpr (T == kTypeQ6K) {
         // 8 lanes per row; a wave takes rows of one parity so that its 2-byte
         // aligned rows share their 4-byte alignment
         const int par = wave & 1, G = (wave >> 1) * 8 + (grp & 7);
-        for (int m = G; m < n / 2; m += 64) {
+        for (int m = G; m < n / 2; m += NT / 16) {
             const int r = 2 * m + par, u = u0 + r / kDownRows;
             const float y = g8_row_q6k_u<NB>(base + r * kRowBytes, q8h + u * NB, t8);
             if (t8 == 0) ys[u0 * kDownRows + r] = y;
         }
     } else {
         // one 8-lane group per row, lane t taking super-block t
-        for (int r = grp; r < n; r += 128) {
+        for (int r = grp; r < n; r += NT / 8) {
             const int u = u0 + r / kDownRows;
             const Q8L &xb = q8h[u * NB + (t8 < NB ? t8 : 0)];
             float y;
@@ -259,10 +261,10 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
         return;
     }
     if constexpr (TS == TD) {
-        down_rows<TD, NBH>(wd, nu * kDownRows, 0, q8h, ys);  // the shared segment follows the routed ones
+        down_rows<TD, NBH, 1024>(wd, nu * kDownRows, 0, q8h, ys);  // the shared segment follows the routed ones
     } else {
-        down_rows<TD, NBH>(wd, k * kDownRows, 0, q8h, ys);
-        if (has_sh) down_rows<TS, NBH>(wd + k * kSegBytes, kDownRows, k, q8h, ys);
+        down_rows<TD, NBH, 1024>(wd, k * kDownRows, 0, q8h, ys);
+        if (has_sh) down_rows<TS, NBH, 1024>(wd + k * kSegBytes, kDownRows, k, q8h, ys);
     }
     __syncthreads();
     if (threadIdx.x < kDownRows) {
@@ -344,21 +346,30 @@ __device__ __forceinline__ float rms_scale(const float *x, int n, float eps, dou
     return 1.0f / sqrtf(mean + eps);
 }
 
-// Workgroups of each role per XCD.
+// Workgroups of each role per XCD; ns = gate/up units (the routed slots and
+// the shared expert).
 struct FusedRoles {
     int route, gu, down;
 };
-__host__ __device__ __forceinline__ FusedRoles fused_roles(int E, int k, int n_ff, int n_embd) {
-    const int r = (E + kFRouteRows - 1) / kFRouteRows, g = k * (n_ff / kFGuRows), d = n_embd / kFDownRows;
+__host__ __device__ __forceinline__ FusedRoles fused_roles(int E, int ns, int n_ff, int n_embd) {
+    const int r = (E + kFRouteRows - 1) / kFRouteRows, g = ns * (n_ff / kFGuRows), d = n_embd / kFDownRows;
     return {(r + kFXcds - 1) / kFXcds, (g + kFXcds - 1) / kFXcds, (d + kFXcds - 1) / kFXcds};
 }
+__host__ __device__ __forceinline__ int fused_units(const FusedLayerArgs &a) {
+    return a.k + (a.sh_gate.base ? 1 : 0);
+}
 
-template <int TD, int NBH>
+// Gate/up rows of type TG (Q4_K or Q3_K, 8 super-blocks); down rows of type TD
+// with NBH super-blocks; SH: a shared expert, whose down rows have type TS and
+// the same width.
+template <int TG, int TD, int NBH, int TS, bool SH>
 __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     constexpr int N = 2048, NB = N / QK;
-    constexpr int kGuRowBytes = NB * kQ4KBytes;
+    constexpr int kGuRowBytes = NB * QType<TG>::bytes;
     constexpr int kDnRowBytes = NBH * QType<TD>::bytes;
-    constexpr int kSegBytes = kFDownRows * kDnRowBytes;  // 8 rows of one expert
+    constexpr int kSegBytes = kFDownRows * kDnRowBytes;                 // 8 rows of one expert
+    constexpr int kSegBytesS = kFDownRows * NBH * QType<TS>::bytes;     // 8 rows of the shared expert
+    static_assert(kGuRowBytes % 16 == 0 && kSegBytes % 16 == 0 && kSegBytesS % 16 == 0, "16-byte copies");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ unsigned long long tk_s;
     __shared__ int flag_s;
@@ -463,7 +474,9 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         if (lane < k) w_s[lane] = wj / ws;
     };
     const unsigned xcc = xcc_id();
-    const FusedRoles R = fused_roles(E, k, nff, N);
+    constexpr bool has_sh = SH;
+    const int ns = k + (SH ? 1 : 0);  // gate/up and down units: the k slots, then the shared expert
+    const FusedRoles R = fused_roles(E, ns, nff, N);
     const unsigned long long Gx = (unsigned long long)(R.route + R.gu + R.down);
     if (tid == 0) {
         tk_s = ctr_add(a.ctr + kFCtrTicket + 16 * xcc);
@@ -472,7 +485,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     const unsigned long long ep = tk_s / Gx;
     const int lt = (int)(tk_s - ep * Gx);  // role slot within this XCD's share
-    const int n_route = R.route * kFXcds, gu_per = nff / kFGuRows, n_gu = k * gu_per;
+    const int gu_per = nff / kFGuRows, n_gu = ns * gu_per;
     // phase stamps: [xcc * Gx + lt][id, start, e1, e2, e3, end]
     unsigned long long *st = a.trace ? a.trace + ((size_t)xcc * Gx + lt) * kFusedStamps : nullptr;
     auto stamp = [&](int i) {
@@ -519,13 +532,27 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     }
 
     if (lt < R.route + R.gu) {
-        // -- gate/up rows [16 r, +16) of slot j, SwiGLU --
+        // -- gate/up rows [16 r, +16) of slot j (j = k: the shared expert), SwiGLU --
         const int i = (int)xcc * R.gu + (lt - R.route);
         if (i >= n_gu) return;  // padding of the XCD shares
-        const int j = i / gu_per, r0 = (i - j * gu_per) * kFGuRows;
+        // the shared expert's workgroups come first: they wait for no selection,
+        // so their rows stream while the router runs
+        const bool shared = has_sh && i < gu_per;
+        const int q = has_sh ? i - gu_per : i;
+        const int j = shared ? k : q / gu_per, r0 = (shared ? i : q - j * gu_per) * kFGuRows;
         uint8_t *wt = smem;  // [2][16 rows]
         Q8L *q8 = reinterpret_cast<Q8L *>(smem + 2 * kFGuRows * kGuRowBytes);
         float *gu = reinterpret_cast<float *>(q8 + NB);
+        // gate rows on waves 0-1, up rows on waves 2-3
+        auto copy_rows = [&](const MatDesc &G, const MatDesc &U, int id) {
+            constexpr int half = (kFGuRows * kGuRowBytes / 2 + 1023) & ~1023;
+            const int m = wave >> 1, off = (wave & 1) * half;
+            const int len = min(half, kFGuRows * kGuRowBytes - off);
+            const uint8_t *src =
+                (m ? U.base + (size_t)id * U.stride : G.base + (size_t)id * G.stride) + (size_t)r0 * kGuRowBytes;
+            wave_copy(wt + m * kFGuRows * kGuRowBytes + off, src + off, len);
+        };
+        if (shared && wave < 4) copy_rows(a.sh_gate, a.sh_up, 0);
         const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
         if (wave >= 4) {
             // Q8_K of fx while the selection is awaited and the rows are copied
@@ -534,31 +561,40 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
                 const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
                 wave_quantize_q8l_regs(v, &q8[b]);
             }
-        } else if (wave == 0) {
+        } else if (wave == 0 && !shared) {
             select_a(ep + 1ull);
+        } else if (wave == 0 && r0 == 0 && lane < 32) {
+            // the shared expert's sigmoid gate: its f32 row against fx in the
+            // router's order, for the down workgroups (counted with this h)
+            const float *wr = a.sh_gate_inp + lane;
+            const float *xr = a.xin + lane;
+            float acc = 0.0f;
+#pragma unroll 16
+            for (int c = 0; c < N; c += 32) acc = fmaf(wr[c], xr[c] * scale, acc);
+            acc = acc + __shfl_xor(acc, 16);
+            acc = row16_ggml_fold(acc);
+            if (lane == 0)
+                __hip_atomic_store(a.sgate, 1.0f / (1.0f + expf(-acc)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
-        select_b();
+        if (!shared) select_b();
         __syncthreads();
         stamp(2);
-        const int id = sel_s[j];
-        const bool bad = flag_s || id < 0 || id >= a.gate.n_ids;
-        if (!bad && wave < 4) {
-            // gate rows on waves 0-1, up rows on waves 2-3
-            constexpr int half = (kFGuRows * kGuRowBytes / 2 + 1023) & ~1023;
-            const int m = wave >> 1, off = (wave & 1) * half;
-            const int len = min(half, kFGuRows * kGuRowBytes - off);
-            const uint8_t *src = (m ? a.up.base + (size_t)id * a.up.stride : a.gate.base + (size_t)id * a.gate.stride) +
-                                 (size_t)r0 * kGuRowBytes;
-            wave_copy(wt + m * kFGuRows * kGuRowBytes + off, src + off, len);
-            lds_dma_wait();
-        }
+        const int id = shared ? 0 : sel_s[j];
+        const bool bad = !shared && (flag_s || id < 0 || id >= a.gate.n_ids);
+        if (!shared && !bad && wave < 4) copy_rows(a.gate, a.up, id);
+        if (wave < 4) lds_dma_wait();
         __syncthreads();
         stamp(3);
         if (!bad && (tid >> 3) < 2 * kFGuRows) {
             const int grp = tid >> 3, t8 = tid & 7;
             const int m = grp >= kFGuRows, row = grp - m * kFGuRows;
-            const float v = lpb_row_q4k_mem<NB>(wt + (m * kFGuRows + row) * kGuRowBytes, q8[t8], t8);
+            const uint8_t *wr = wt + (m * kFGuRows + row) * kGuRowBytes;
+            float v;
+            if constexpr (TG == kTypeQ3K)
+                v = lpb_row_q3k_mem<NB>(wr, q8[t8], t8);
+            else
+                v = lpb_row_q4k_mem<NB>(wr, q8[t8], t8);
             if (t8 == NB - 1) gu[grp] = v;
         }
         __syncthreads();
@@ -580,13 +616,17 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         return;
     }
 
-    // -- down rows [8 i, +8) of every selected expert, then the combine --
+    // -- down rows [8 i, +8) of every selected expert (and the shared one), then the combine --
     const int i = (int)xcc * R.down + (lt - R.route - R.gu);
     if (i * kFDownRows >= N) return;  // padding of the XCD shares
     const int d0 = i * kFDownRows;
-    uint8_t *wd = smem;  // [k][8 rows]
-    Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes);
-    float *ys = reinterpret_cast<float *>(q8h + k * NBH);
+    uint8_t *wd = smem;  // [k][8 rows], then the shared expert's 8 rows
+    Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes + (has_sh ? kSegBytesS : 0));
+    float *ys = reinterpret_cast<float *>(q8h + ns * NBH);
+    // the shared expert's rows need no selection: copied at once (not by wave
+    // 0, whose probes would queue behind the copy)
+    if (has_sh && wave == 7)
+        wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kFDownRows), kSegBytesS);
     if (wave == 0) select_a(ep + 1ull);
     __syncthreads();
     select_b();
@@ -623,7 +663,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         const unsigned long long *hd = a.ctr + kFCtrHDone + 16 * xcc;
         const bool ok = poll(
             [&]() {
-                const bool r = lane >= k || reached(ctr_load(hd + lane), ep + 1ull);
+                const bool r = lane >= ns || reached(ctr_load(hd + lane), ep + 1ull);
                 if (__all(r)) return true;
                 __builtin_amdgcn_s_sleep(8);
                 return false;
@@ -634,7 +674,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     stamp(3);
     // Q8_K of every unit's h, read past the L2 (it was written on other XCDs)
-    for (int q = wave; q < k * NBH; q += 8) {
+    for (int q = wave; q < ns * NBH; q += 8) {
         const int u = q / NBH, b = q - u * NBH;
         const float *hp = a.h + (size_t)u * nff + b * QK + 4 * lane;
         float v[4];
@@ -650,13 +690,23 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         return;
     }
     stamp(4);
-    down_rows<TD, NBH>(wd, k * kFDownRows, 0, q8h, ys);
+    if constexpr (TS == TD) {
+        down_rows<TD, NBH, 512>(wd, ns * kFDownRows, 0, q8h, ys);  // the shared segment follows the routed ones
+    } else {
+        down_rows<TD, NBH, 512>(wd, k * kFDownRows, 0, q8h, ys);
+        if (has_sh) down_rows<TS, NBH, 512>(wd + k * kSegBytes, kFDownRows, k, q8h, ys);
+    }
     __syncthreads();
     if (tid < kFDownRows) {
         const int r = tid, d = d0 + r;
         float acc = 0.0f;
         for (int j = 0; j < k; ++j) acc = acc + w_s[j] * ys[j * kFDownRows + r];
-        a.out[d] = acc + a.res[d];
+        if (has_sh) {
+            const float sg = __hip_atomic_load(a.sgate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a.out[d] = (acc + ys[k * kFDownRows + r] * sg) + a.res[d];
+        } else {
+            a.out[d] = acc + a.res[d];
+        }
     }
     stamp(5);
 }
@@ -743,10 +793,12 @@ namespace hoard {
 namespace {
 
 size_t fused_lds_bytes(const FusedLayerArgs &a) {
-    const int nbh = a.down.cols / QK;
-    const size_t gu = 2 * kFGuRows * (size_t)(8 * kQ4KBytes) + 8 * sizeof(Q8L) + 2 * kFGuRows * sizeof(float);
-    const size_t dn = (size_t)a.k * kFDownRows * nbh * block_bytes(a.down.type) + (size_t)a.k * nbh * sizeof(Q8L) +
-                      (size_t)a.k * kFDownRows * sizeof(float);
+    const int nbh = a.down.cols / QK, ns = fused_units(a);
+    const size_t gu = 2 * kFGuRows * (size_t)(8 * block_bytes(a.gate.type)) + 8 * sizeof(Q8L) +
+                      2 * kFGuRows * sizeof(float);
+    const size_t seg_s = a.sh_gate.base ? (size_t)kFDownRows * nbh * block_bytes(a.sh_down.type) : 0;
+    const size_t dn = (size_t)a.k * kFDownRows * nbh * block_bytes(a.down.type) + seg_s +
+                      (size_t)ns * nbh * sizeof(Q8L) + (size_t)ns * kFDownRows * sizeof(float);
     const size_t rt = (size_t)(kFRouteRows + 1) * a.n_embd * sizeof(float);  // router rows and x
     const size_t m = gu > dn ? gu : dn;
     return m > rt ? m : rt;
@@ -754,46 +806,64 @@ size_t fused_lds_bytes(const FusedLayerArgs &a) {
 
 }  // namespace
 
-// The shapes of the fused launch: n_embd 2048, Q4_K gate/up with n_ff a
-// multiple of 16, down Q6_K with 2-4 super-blocks, Q5_K with 2 or 4, or Q4_K
-// with 4 per row; no shared expert; 16-byte aligned tensors and activations.
+// The shapes of the fused launch: n_embd 2048, at most 1024 experts; gate/up
+// Q4_K or Q3_K with n_ff a multiple of 16; down Q6_K with 2-4 super-blocks,
+// Q5_K with 2 or 4, or Q4_K with 4 per row; a shared expert of the same gate/up
+// type and width, whose down rows have the routed type (or Q6_K beside Q5_K
+// with 2), at most 16 units in all; 16-byte aligned tensors and activations.
 bool fused_layer_ok(const FusedLayerArgs &a) {
-    if (a.n_embd != 2048 || a.gate.type != kTypeQ4K || a.up.type != kTypeQ4K || a.gate.rows % kFGuRows ||
-        a.gate.rows != a.up.rows || a.k > 16 || a.k < 1)
+    const bool gu_type = (a.gate.type == kTypeQ4K || a.gate.type == kTypeQ3K) && a.up.type == a.gate.type;
+    if (a.n_embd != 2048 || !gu_type || a.gate.rows % kFGuRows || a.gate.rows != a.up.rows || a.k < 1 ||
+        fused_units(a) > 16 || a.E < a.k || a.E > 1024)
         return false;
     const int nbh = a.down.cols / QK;
     const bool q6 = a.down.type == kTypeQ6K && nbh >= 2 && nbh <= 4;
     const bool q4 = a.down.type == kTypeQ4K && nbh == 4;
     const bool q5 = a.down.type == kTypeQ5K && (nbh == 2 || nbh == 4);
     if (!q6 && !q4 && !q5) return false;
-    const uintptr_t al = reinterpret_cast<uintptr_t>(a.gate.base) | reinterpret_cast<uintptr_t>(a.up.base) |
-                         reinterpret_cast<uintptr_t>(a.down.base) | a.gate.stride | a.up.stride | a.down.stride |
-                         reinterpret_cast<uintptr_t>(a.xin) | reinterpret_cast<uintptr_t>(a.h);
+    uintptr_t al = reinterpret_cast<uintptr_t>(a.gate.base) | reinterpret_cast<uintptr_t>(a.up.base) |
+                   reinterpret_cast<uintptr_t>(a.down.base) | a.gate.stride | a.up.stride | a.down.stride |
+                   reinterpret_cast<uintptr_t>(a.xin) | reinterpret_cast<uintptr_t>(a.h);
+    if (a.sh_gate.base) {
+        if (a.sh_gate.type != a.gate.type || a.sh_up.type != a.gate.type || a.sh_gate.rows != a.gate.rows ||
+            a.sh_up.rows != a.gate.rows || !a.sh_up.base || !a.sh_down.base || !a.sh_gate_inp || !a.sgate ||
+            a.sh_down.cols != a.down.cols)
+            return false;
+        if (a.sh_down.type != a.down.type && !(a.down.type == kTypeQ5K && a.sh_down.type == kTypeQ6K && nbh == 2))
+            return false;
+        al |= reinterpret_cast<uintptr_t>(a.sh_gate.base) | reinterpret_cast<uintptr_t>(a.sh_up.base) |
+              reinterpret_cast<uintptr_t>(a.sh_down.base);
+    }
     return (al & 15) == 0 && fused_lds_bytes(a) <= 65536;
 }
 
 int fused_layer_groups(const FusedLayerArgs &a) {
-    const FusedRoles R = fused_roles(a.E, a.k, a.gate.rows, a.n_embd);
+    const FusedRoles R = fused_roles(a.E, fused_units(a), a.gate.rows, a.n_embd);
     return kFXcds * (R.route + R.gu + R.down);
 }
 
 hipError_t launch_fused_layer(const FusedLayerArgs &a, hipStream_t s) {
     if (!fused_layer_ok(a)) return hipErrorInvalidConfiguration;
     const int nbh = a.down.cols / QK;
-    const FusedRoles R = fused_roles(a.E, a.k, a.gate.rows, a.n_embd);
-    const unsigned G = (unsigned)(kFXcds * (R.route + R.gu + R.down));
+    const int ts = a.sh_gate.base ? a.sh_down.type : a.down.type;
+    const unsigned G = (unsigned)fused_layer_groups(a);
     const size_t lds = fused_lds_bytes(a);
-#define HOARD_FUSED(TD, NBH)                                                                  \
-    if (a.down.type == TD && nbh == NBH) {                                                    \
-        hipLaunchKernelGGL((fused_layer_kernel<TD, NBH>), dim3(G), dim3(512), lds, s, a);    \
-        return hipGetLastError();                                                             \
+    const bool sh = a.sh_gate.base != nullptr;
+#define HOARD_FUSED(TG, TD, NBH, TS, SH)                                                                  \
+    if (a.gate.type == TG && a.down.type == TD && nbh == NBH && ts == TS && sh == SH) {                   \
+        hipLaunchKernelGGL((fused_layer_kernel<TG, TD, NBH, TS, SH>), dim3(G), dim3(512), lds, s, a);    \
+        return hipGetLastError();                                                                         \
     }
-    HOARD_FUSED(kTypeQ6K, 2)
-    HOARD_FUSED(kTypeQ6K, 3)
-    HOARD_FUSED(kTypeQ6K, 4)
-    HOARD_FUSED(kTypeQ4K, 4)
-    HOARD_FUSED(kTypeQ5K, 2)
-    HOARD_FUSED(kTypeQ5K, 4)
+    HOARD_FUSED(kTypeQ4K, kTypeQ6K, 2, kTypeQ6K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ6K, 3, kTypeQ6K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ6K, 4, kTypeQ6K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ4K, 4, kTypeQ4K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ5K, 2, kTypeQ5K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ5K, 4, kTypeQ5K, false)
+    HOARD_FUSED(kTypeQ3K, kTypeQ5K, 4, kTypeQ5K, false)
+    HOARD_FUSED(kTypeQ3K, kTypeQ4K, 4, kTypeQ4K, false)
+    HOARD_FUSED(kTypeQ4K, kTypeQ6K, 2, kTypeQ6K, true)
+    HOARD_FUSED(kTypeQ4K, kTypeQ5K, 2, kTypeQ6K, true)
 #undef HOARD_FUSED
     return hipErrorInvalidConfiguration;
 }

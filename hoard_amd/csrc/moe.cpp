@@ -357,13 +357,14 @@ int run_ffn(hoard_moe *h, const Layer &L, const float *fx, const int32_t *ids, c
 
 // The whole layer in one launch (router, gate/up and down workgroups in the
 // order they start, layer.hip) where the shape and handle admit it: every
-// expert resident, no shared expert.  *done reports whether it ran.  xin is fx,
-// or with rms the residual x whose rms_norm is fx.
+// expert resident, a shared expert as wide as the routed ones.  *done reports
+// whether it ran.  xin is fx, or with rms the residual x whose rms_norm is fx.
 int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, float eps, const float *res, float *out,
                     int32_t *sel, float *w, hipStream_t s, bool *done) {
     *done = false;
     const hoard_moe_cfg &c = h->cfg;
-    if (!h->layer_fused || !h->layer_kernels || !h->chip_ok || c.pool_k > 0 || c.n_ff_shexp > 0) return HOARD_OK;
+    if (!h->layer_fused || !h->layer_kernels || !h->chip_ok || c.pool_k > 0) return HOARD_OK;
+    if (c.n_ff_shexp > 0 && c.n_ff_shexp != c.n_ff) return HOARD_OK;
     hoard::FusedLayerArgs a{};
     a.xin = xin;
     a.rms = rms;
@@ -376,6 +377,13 @@ int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, flo
     a.gate = mat(L.gate, L.gstride, L.gate_type, c.n_ff, c.n_embd, c.n_expert);
     a.up = mat(L.up, L.ustride, L.up_type, c.n_ff, c.n_embd, c.n_expert);
     a.down = mat(L.down, L.dstride, L.down_type, c.n_embd, c.n_ff, c.n_expert);
+    if (c.n_ff_shexp > 0) {
+        a.sh_gate = mat(L.sh_gate, 0, L.sh_gate_type, c.n_ff_shexp, c.n_embd, 1);
+        a.sh_up = mat(L.sh_up, 0, L.sh_up_type, c.n_ff_shexp, c.n_embd, 1);
+        a.sh_down = mat(L.sh_down, 0, L.sh_down_type, c.n_embd, c.n_ff_shexp, 1);
+        a.sh_gate_inp = L.sh_gate_inp;
+        a.sgate = h->sgate;
+    }
     a.n_embd = c.n_embd;
     a.E = c.n_expert;
     a.k = c.n_used;

@@ -6,6 +6,8 @@ quantisation and integer super-block sums, and the router logits in the CPU
 dot's fma order, so in practice most outputs are bit-identical; the printed
 bit_identical fraction tracks that.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -328,14 +330,27 @@ def test_decode_splits_the_range_where_layer_types_change(orc):
 
 # more than 128 experts: the one-launch layer's waiting workgroups run the router tail
 E256 = W.Shape("e256_k8", 11, 2048, 256, 8, 512, 1, W.TYPE_Q4_K, W.TYPE_Q4_K, W.TYPE_Q6_K, 1)
+# more than 8 experts per token without a shared expert: more than 64 down rows
+# per workgroup, Q6_K rows (pairs of rows per 8-lane group) and Q4_K rows
+E128_K10 = W.Shape("e128_k10", 12, 2048, 128, 10, 768, 1, W.TYPE_Q4_K, W.TYPE_Q4_K, W.TYPE_Q6_K, 1)
+E64_K10_Q4 = W.Shape("e64_k10_q4", 13, 2048, 64, 10, 1024, 0, W.TYPE_Q4_K, W.TYPE_Q4_K, W.TYPE_Q4_K, 1)
 
 
-@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE, E256], ids=lambda s: s.name)
+def _kernel_launches(st):
+    import hoard_amd as H
+    kt = H.KernelTimes()
+    H.check(st.lib.hoard_moe_profile_read(st.h, ctypes.byref(kt)))
+    return list(kt.launches)
+
+
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.OLMOE, E256, E128_K10, E64_K10_Q4, W.QWEN3_NEXT, W.QWEN35,
+                                   W.OLMOE_Q3], ids=lambda s: s.name)
 def test_fused_layer_matches_three_launches(orc, shape):
     """hoard_moe_layer in one launch (router, gate/up and down workgroups in the
-    order they start) against the three launches per layer: the same output,
-    selection and weights bit for bit, for several tokens and layers in a row
-    (the launches' counters carry over), and the per-layer decode the same way."""
+    order they start; the shared expert's workgroups first) against the three
+    launches per layer: the same output, selection and weights bit for bit, for
+    several tokens and layers in a row (the launches' counters carry over), and
+    the per-layer decode the same way."""
     import hoard_amd as H
     nl = 3
     layers = {l: W.make_layer(shape, 14, l) for l in range(nl)}
@@ -347,7 +362,11 @@ def test_fused_layer_matches_three_launches(orc, shape):
                 fx, res = W.make_hidden(shape, 14, l, t)
                 print(f"fused layer {shape.name} token {t} layer {l}", flush=True)
                 st.set_option(H.OPT_LAYER_FUSED, 1)
+                H.check(st.lib.hoard_moe_profile(st.h, 1))
                 o1, s1, w1 = st.layer(l, fx, res)
+                launches = _kernel_launches(st)
+                H.check(st.lib.hoard_moe_profile(st.h, 0))
+                assert launches[H.KERNEL_LAYER] == 1 and launches[H.KERNEL_GATEUP] == 0, launches
                 st.set_option(H.OPT_LAYER_FUSED, 0)
                 o0, s0, w0 = st.layer(l, fx, res)
                 assert np.array_equal(s1, s0) and np.array_equal(w1.view(np.uint32), w0.view(np.uint32))
