@@ -386,9 +386,10 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     // scale), and select_b (every thread) ranks it: expert e's rank is the
     // number of experts of larger probability or of equal probability and a
     // lower index, the order of router_tail's repeated maxima, and ranks below
-    // k fill sel_s / w_s.  With E > 128 wave 0 runs router_tail itself.  A
-    // wait that ran out raises flag_s instead.  w_s holds the raw top-k
-    // probabilities until select_renorm.
+    // k fill sel_s / w_s.  With E > 128 wave 0 runs router_tail itself (a
+    // rank over more experts, in two steps or through a threshold, measured
+    // no faster on 512 threads).  A wait that ran out raises flag_s instead.
+    // With E <= 128, w_s holds the raw top-k probabilities until select_renorm.
     const bool rank_sel = E <= 128;
     auto select_a = [&](unsigned long long epoch) {
         // every logit of this launch, from this XCD's copy: lanes take experts
@@ -417,6 +418,12 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             if (lane == 0) flag_s = 1;
             return;
         }
+        // no expert, weight NaN, unless ranked: what router_tail gives for
+        // probabilities that are NaN (all of them are when any logit is not finite)
+        if (lane < kMaxK) {
+            sel_s[lane] = 0x7fffffff;
+            w_s[lane] = __builtin_nanf("");
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // lg_s written by this wave
         if (!rank_sel) {
             router_tail<false, false>(lg_s, E, k, a.renorm, sel_s, w_s, 0);
@@ -438,7 +445,6 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         const float sc = (float)(1.0 / sum);
         ps[lane] = lane < E ? p0 * sc : -1.0f;  // absent experts below every probability
         ps[lane + 64] = lane + 64 < E ? p1 * sc : -1.0f;
-        if (lane < 16) sel_s[lane] = -1;
     };
     auto select_b = [&]() {
         if (!rank_sel || flag_s) return;
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             r += (v.w > pe) | ((v.w == pe) & (e4 + 3 < e));
         }
         r = group4_sum(r);
-        if (e < E && q == 0 && r < k) {
+        if (e < E && q == 0 && r < k && pe == pe) {
             sel_s[r] = e;
             w_s[r] = pe;
         }
@@ -633,9 +639,8 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     if (wave == 0) select_renorm();
     stamp(2);
-    // the first down workgroup of XCD 0 also gives the caller sel / wsel, formed
-    // from the gathered logits as the route kernel forms them (a selection that
-    // could not be gathered reads as no expert, weight NaN)
+    // the first down workgroup of XCD 0 also gives the caller sel / wsel (a
+    // selection that could not be gathered reads as no expert, weight NaN)
     const bool caller_sel = xcc == 0 && lt == R.route + R.gu;
     int bad = flag_s;
     for (int u = wave; u < k; u += 8) {
@@ -648,15 +653,11 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         if (!flag_s) wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kDnRowBytes,
                                kSegBytes);
     }
-    if (caller_sel && wave == 0) {
-        if (flag_s) {
-            if (lane < k) {
-                a.sel[lane] = 0x7fffffff;
-                a.wsel[lane] = __builtin_nanf("");
-            }
-        } else {
-            router_tail<false, false>(lg_s, E, k, a.renorm, a.sel, a.wsel, 0);
-        }
+    if (caller_sel && wave == 0 && lane < k) {
+        // the renormed weights: lane j wrote w_s[j] itself in select_renorm
+        // (or router_tail's lane j did)
+        a.sel[lane] = flag_s ? 0x7fffffff : sel_s[lane];
+        a.wsel[lane] = flag_s ? __builtin_nanf("") : w_s[lane];
     }
     if (wave == 0 && !flag_s) {
         // every slot's h complete: lane j watches slot j's word of this XCD's line

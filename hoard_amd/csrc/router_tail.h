@@ -15,23 +15,14 @@ namespace hoard {
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 constexpr int kMaxK = 16;
 
-// Wave-uniform results: the reductions are DPP butterflies (wave.h).  The max
-// and the top-k argmax are order-independent; the double-precision sum of
-// the probabilities is exact unless they span more than 2^29 in magnitude,
-// and its float reciprocal absorbs the remaining rounding differences.
-// AGENT: the logits come from other workgroups of the same launch and are read
-// at device (agent) scope, which bypasses the per-XCD L2, instead of behind a
-// cache-flushing fence.  STORE_AGENT: sel / wsel go to other workgroups and
-// are written at device scope; otherwise plain stores (global memory of this
-// workgroup's own use, or LDS).
-// NT: experts per lane the body is compiled for (E <= 64 NT, E <= 1024).
-template <bool AGENT, int NT, bool STORE_AGENT = AGENT>
-__device__ inline void router_tail_nt(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel,
-                                      int tok) {
+// The softmax of one token's logits lg[0, E) on one wave: p[t] holds expert
+// lane + 64 t (experts past E hold -infinity).  The tail below and every
+// other selection of these probabilities form them here, so they agree bit
+// for bit.
+template <bool AGENT, int NT>
+__device__ inline void softmax_nt(const float *lg, int E, float (&p)[NT]) {
     const int lane = threadIdx.x & 63;
     const int nt = NT;
-    const float *lg = logits + (size_t)tok * E;
-    float p[NT];
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -61,6 +52,24 @@ __device__ inline void router_tail_nt(const float *logits, int E, int k, int ren
     const float sc = (float)(1.0 / sum);
 #pragma unroll
     for (int t = 0; t < NT; ++t) p[t] = p[t] * sc;
+}
+
+// Wave-uniform results: the reductions are DPP butterflies (wave.h).  The max
+// and the top-k argmax are order-independent; the double-precision sum of
+// the probabilities is exact unless they span more than 2^29 in magnitude,
+// and its float reciprocal absorbs the remaining rounding differences.
+// AGENT: the logits come from other workgroups of the same launch and are read
+// at device (agent) scope, which bypasses the per-XCD L2, instead of behind a
+// cache-flushing fence.  STORE_AGENT: sel / wsel go to other workgroups and
+// are written at device scope; otherwise plain stores (global memory of this
+// workgroup's own use, or LDS).
+// NT: experts per lane the body is compiled for (E <= 64 NT, E <= 1024).
+template <bool AGENT, int NT, bool STORE_AGENT = AGENT>
+__device__ inline void router_tail_nt(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel,
+                                      int tok) {
+    const int lane = threadIdx.x & 63;
+    float p[NT];
+    softmax_nt<AGENT, NT>(logits + (size_t)tok * E, E, p);
 
     // top-k: repeated wave max, larger probability first, lower index on ties.
     // A taken or absent expert holds -1 (probabilities are >= 0); the lowest

@@ -84,7 +84,7 @@ TIE_CASES = [(True, 2), (False, 2), (True, 3), (False, 3)]
 TIE_IDS = ["lower-2way", "higher-2way", "lower-3way", "higher-3way"]
 
 
-@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.QWEN3_NEXT, W.OLMOE], ids=lambda s: s.name)
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.QWEN3_NEXT, W.OLMOE, W.QWEN35], ids=lambda s: s.name)
 def test_route_tie_at_boundary(orc, shape):
     """hoard_moe_route (and hoard_moe_layer) on routers with exact ties at k / k+1."""
     st = _stage(shape, {})
@@ -338,8 +338,9 @@ def test_non_finite_router_input(orc, bad):
         print(f"non-finite router input {bad}: route / layer / batched", flush=True)
         sel, w = st.route(0, badfx)
         assert np.all(sel == INT32_MAX) and np.all(np.isnan(w)), (sel, w)
-        out, _, _ = st.layer(0, badfx, res)
+        out, lsel, lw = st.layer(0, badfx, res)
         assert np.all(np.isnan(out))
+        assert np.all(lsel == INT32_MAX) and np.all(np.isnan(lw)), (lsel, lw)
         bfx = np.stack([fx, badfx, fx])
         bres = np.stack([res, res, res])
         bout, bsel, _ = st.forward_batched(0, bfx, bres)
@@ -440,6 +441,39 @@ def test_failed_slot_upload_leaves_pool_consistent():
     finally:
         pool.close()
         res_st.close()
+
+
+@pytest.mark.parametrize("shape", [W.QWEN3_NEXT, W.QWEN35], ids=lambda s: s.name)
+def test_non_finite_router_input_fused_many_experts(orc, shape):
+    """The one-launch layer above 128 experts (two-step rank) and with a shared
+    expert: a NaN router input gives no expert (INT32_MAX), weight NaN and a NaN
+    row, as the three launches do; the next good token is exact."""
+    layers = {0: W.make_layer(shape, 28, 0)}
+    st = _stage(shape, layers)
+    try:
+        assert st.get_option(H.OPT_LAYER_FUSED) == 1
+        fx, res = W.make_hidden(shape, 28, 0, 0)
+        good, gsel, _ = st.layer(0, fx, res)
+        badfx = fx.copy()
+        badfx[77] = np.nan
+        print(f"non-finite router input, one-launch layer {shape.name}", flush=True)
+        out, sel, w = st.layer(0, badfx, res)
+        st.sync_check()
+        assert np.all(sel == INT32_MAX) and np.all(np.isnan(w)), (sel, w)
+        assert np.all(np.isnan(out))
+        st.set_option(H.OPT_LAYER_FUSED, 0)
+        out0, sel0, w0 = st.layer(0, badfx, res)
+        assert np.array_equal(sel0, sel) and np.all(np.isnan(w0)) and np.all(np.isnan(out0))
+        st.set_option(H.OPT_LAYER_FUSED, 1)
+        again, asel, _ = st.layer(0, fx, res)
+        st.sync_check()
+        assert np.array_equal(asel, gsel) and np.array_equal(again.view(np.uint32), good.view(np.uint32))
+        ref, sel_o, _ = orc.moe_layer(layers[0], fx, res)
+        assert np.array_equal(gsel, sel_o)
+        parity.assert_parity(good, ref, f"one-launch layer {shape.name}")
+    finally:
+        st.set_option(H.OPT_LAYER_FUSED, 1)
+        st.close()
 
 
 def test_fused_layer_wait_limit_zero_gives_up_cleanly(orc):
