@@ -482,17 +482,24 @@ __device__ __forceinline__ float lpb_row_q5k_mem(const uint8_t *row, const Q8L &
 // sum_{16} q3*q8, with q3 = q2 + 4*h - 4 and sum q3*q8 = sum (q2 + 4h)*q8 - 4*bsum.
 // kRolled: the halves one after the other (fewer live registers, for kernels
 // that keep it beside wait loops); otherwise both unrolled.
+// The block's words come from the 4-byte aligned address at or below it
+// (word i = alignbyte(w[i + 1], w[i], sh), no branch on the alignment), and
+// that address is formed by pointer arithmetic, so a block in LDS is read with
+// ds_read rather than through generic (flat) addresses.
 template <bool kRolled>
 __device__ __forceinline__ int q3k_block_isum_mem(const uint8_t *blk, const Q8L &x) {
-    const uint32_t s0 = lds_u32(blk + 96), s1 = lds_u32(blk + 100), s2 = lds_u32(blk + 104);
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(blk - sh);
+    auto word = [&](int i) -> uint32_t { return __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh); };
+    const uint32_t s0 = word(24), s1 = word(25), s2 = word(26);  // scales at byte 96
     const uint4 *xq = reinterpret_cast<const uint4 *>(x.qs);
     int isum = 0;
     auto half = [&](int n) {  // elements 128n .. 128n + 127
         uint32_t qw[8], hm[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            qw[t] = lds_u32(blk + 32 + 32 * n + 4 * t);
-            hm[t] = lds_u32(blk + 4 * t);
+            qw[t] = word(8 + 8 * n + t);  // qs at byte 32
+            hm[t] = word(t);              // hmask at byte 0
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // elements 128n + 32j + l: quant words 32n + 8j + t
