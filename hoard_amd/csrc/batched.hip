@@ -115,22 +115,12 @@ __device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ys
     if (tid == 0) a.n_unique[0] = wave_total;
 }
 
-// Grouping of a prefill-sized batch (all threads of one workgroup): the
-// computed (token, slot) pairs sorted by (expert, token) into ptok / pslot, the
-// groups (used experts in ascending order: uexp, ucount, goff) and the work
-// units (at most kUnitTokens pairs of one group each).  pe[p] (in LDS) is the
-// expert of pair p, or -1 for a pair that joins no group.  The order within an
-// expert comes from chunks of at most 32 tokens taken in token order: a pair's
-// place is its expert's running base plus the tokens of its chunk before it
-// that select the same expert (a token joins a group at most once).
-__device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
-    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
-    for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
-    __syncthreads();
-    for (int p = tid; p < P; p += nt)
-        if (pe[p] >= 0) atomicAdd(&g.cnt[pe[p]], 1u);
-    __syncthreads();
-    if (tid < 64) {
+// Groups and units in ascending expert order from the per-expert pair counts
+// g.cnt (wave 0 of the grouping workgroup): uexp / ucount / goff / units / hist,
+// n_unique / n_units, and g.base[e], the first sorted place of expert e.
+__device__ void group_units(const BatchedArgs &a, GroupLds &g) {
+    const int tid = threadIdx.x, E = a.n_ids;
+    {
         // groups and units in ascending expert order: lane owns a contiguous run of experts
         const int lane = tid, per = (E + 63) / 64, e0 = lane * per;
         int cg = 0, cu = 0, cp = 0;
@@ -173,6 +163,24 @@ __device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
             a.n_units[0] = iu;
         }
     }
+}
+
+// Grouping of a prefill-sized batch (all threads of one workgroup): the
+// computed (token, slot) pairs sorted by (expert, token) into ptok / pslot, the
+// groups (used experts in ascending order: uexp, ucount, goff) and the work
+// units (at most kUnitTokens pairs of one group each).  pe[p] (in LDS) is the
+// expert of pair p, or -1 for a pair that joins no group.  The order within an
+// expert comes from chunks of at most 32 tokens taken in token order: a pair's
+// place is its expert's running base plus the tokens of its chunk before it
+// that select the same expert (a token joins a group at most once).
+__device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
+    for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
+    __syncthreads();
+    for (int p = tid; p < P; p += nt)
+        if (pe[p] >= 0) atomicAdd(&g.cnt[pe[p]], 1u);
+    __syncthreads();
+    if (tid < 64) group_units(a, g);
     __syncthreads();
     const int tpc = min(32, max(1, nt / k));  // tokens per chunk: one mask bit each
     for (int t0 = 0; t0 < a.M; t0 += tpc) {
@@ -391,13 +399,61 @@ __global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
 
 // The grouping of a prefill-sized batch, in one workgroup: the pairs' experts
 // are copied into LDS first, so every pass reads them from there.
+// The same order with every chunk's masks formed in one pass (when the
+// chunks' masks of all experts fit kGroupChunkWords): chunk c (tokens
+// [32 c, 32 c + 32)) of expert e has mask cm[c E + e] and starts at cb[c E + e]
+// within the expert's run, so a pair's place is its expert's first place, its
+// chunk's start and the tokens of its chunk before it that select the expert.
+// Three barriers in all, where the chunk loop takes four per chunk.
+constexpr int kGroupChunkWords = 4096;
+__device__ void group_large_chunks(const BatchedArgs &a, GroupLds &g, const int *pe, unsigned *cm, int *cb) {
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
+    const int nch = (a.M + 31) >> 5;
+    for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
+    for (int i = tid; i < nch * E; i += nt) cm[i] = 0u;
+    __syncthreads();
+    for (int p = tid; p < P; p += nt) {
+        const int e = pe[p];
+        if (e < 0) continue;
+        const int t = p / k;
+        atomicAdd(&g.cnt[e], 1u);
+        atomicOr(&cm[(t >> 5) * E + e], 1u << (t & 31));
+    }
+    __syncthreads();
+    if (tid < 64) {
+        group_units(a, g);
+    } else {
+        for (int e = tid - 64; e < E; e += nt - 64) {
+            int run = 0;
+            for (int c = 0; c < nch; ++c) {
+                cb[c * E + e] = run;
+                run += __popc(cm[c * E + e]);
+            }
+        }
+    }
+    __syncthreads();
+    for (int p = tid; p < P; p += nt) {
+        const int e = pe[p];
+        if (e < 0) continue;
+        const int t = p / k, c = t >> 5;
+        const int pos = g.base[e] + cb[c * E + e] + __popc(cm[c * E + e] & ((1u << (t & 31)) - 1u));
+        a.ptok[pos] = t;
+        a.pslot[pos] = p - t * k;
+    }
+}
+
 __global__ __launch_bounds__(1024) void group_kernel(BatchedArgs a) {
     __shared__ GroupLds g;
     __shared__ int pe[kBatchedMaxTokensLarge * kMaxK];
+    __shared__ unsigned cm[kGroupChunkWords];
+    __shared__ int cb[kGroupChunkWords];
     const int P = a.M * a.k;
     for (int p = threadIdx.x; p < P; p += blockDim.x) pe[p] = a.pexp[p];
     __syncthreads();
-    group_large(a, g, pe);
+    if (((a.M + 31) >> 5) * a.n_ids <= kGroupChunkWords)
+        group_large_chunks(a, g, pe, cm, cb);
+    else
+        group_large(a, g, pe);
 }
 
 // -- caller ids: Q8_K of fx (workgroups 0..M-1, a wave per block) and the

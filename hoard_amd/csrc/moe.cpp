@@ -1191,7 +1191,7 @@ void bind_batched(hoard::BatchedArgs &a, const BatchedLayout &L, uint8_t *q8x, u
 
 // Checks common to the batched entry points, and their arguments but the
 // selection and the scratch: the shapes and types the kernels are built for,
-// 16-byte aligned fx and weights.
+// 16-byte aligned fx, res, out and weights.
 int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev, float *out_dev,
                   bool pooled_ok, int max_m, hoard::BatchedArgs *out) {
     int rc = check_layer(h, layer);
@@ -1207,7 +1207,8 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
-    if (((uintptr_t)fx_dev & 15) != 0) return fail(HOARD_ERR_INVALID, "fx must be 16-byte aligned");
+    if ((((uintptr_t)fx_dev | (uintptr_t)res_dev | (uintptr_t)out_dev) & 15) != 0)
+        return fail(HOARD_ERR_INVALID, "fx, res and out must be 16-byte aligned");
     // the weight tiles are copied to LDS in 16-byte units
     if (((uintptr_t)L.gate | (uintptr_t)L.up | (uintptr_t)L.down | (uintptr_t)L.gstride | (uintptr_t)L.ustride |
          (uintptr_t)L.dstride) & 15)

@@ -303,19 +303,30 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
 
 // -- combine: out[t][d] = (sum_j w[t][j] * y[t][j][d]) + res[t][d], j ascending --
 __global__ __launch_bounds__(256) void pf_combine_kernel(BatchedArgs a) {
+    // four consecutive elements a thread (n_embd is a multiple of 1024): at
+    // hundreds of tokens the wider loads pay; at 16 tokens the one-element
+    // form of the batched path keeps more workgroups in flight
     const int t = blockIdx.y;
-    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    const int d = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
     if (d >= a.n_embd) return;
+    float4 *o = reinterpret_cast<float4 *>(a.out + (size_t)t * a.n_embd + d);
     if (a.bad && a.bad[t]) {  // an id outside the pool or expert set: the token's row is poisoned
-        a.out[(size_t)t * a.n_embd + d] = __builtin_nanf("");
+        const float nan = __builtin_nanf("");
+        *o = make_float4(nan, nan, nan, nan);
         return;
     }
-    float acc = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j = 0; j < a.k; ++j) {
         const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
-        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * a.k + js) * a.n_embd + d];
+        const float w = a.wsel[t * a.k + j];
+        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * a.k + js) * a.n_embd + d);
+        acc.x = acc.x + w * y.x;
+        acc.y = acc.y + w * y.y;
+        acc.z = acc.z + w * y.z;
+        acc.w = acc.w + w * y.w;
     }
-    a.out[(size_t)t * a.n_embd + d] = acc + a.res[(size_t)t * a.n_embd + d];
+    const float4 r = *reinterpret_cast<const float4 *>(a.res + (size_t)t * a.n_embd + d);
+    *o = make_float4(acc.x + r.x, acc.y + r.y, acc.z + r.z, acc.w + r.w);
 }
 
 }  // namespace
@@ -334,7 +345,7 @@ hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s) {
     HOARD_DOWN(kTypeQ6K, 3) HOARD_DOWN(kTypeQ6K, 2) HOARD_DOWN(kTypeQ6K, 4) HOARD_DOWN(kTypeQ4K, 4)
     HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
 #undef HOARD_DOWN
-    hipLaunchKernelGGL(pf_combine_kernel, dim3((a.n_embd + 255) / 256, a.M), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(pf_combine_kernel, dim3((a.n_embd + 1023) / 1024, a.M), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -140,7 +140,7 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
    expert into 64-pair units), and the expert products run on per-token int8
    dots or int8 MFMA; each token's result is the single-token
    hoard_moe_layer's bit for bit.  M > 512 returns HOARD_ERR_INVALID.  fx_dev, res_dev, out_dev:
-   [M][n_embd] (out may alias res); sel_dev / w_dev ([M][n_used]) receive the
+   [M][n_embd], 16-byte aligned (out may alias res); sel_dev / w_dev ([M][n_used]) receive the
    routing when non-NULL.  The call's per-expert token histogram and unique
    expert count are reported by hoard_moe_get_stats.  Needs pool_k == 0 and no
    shared expert. */
