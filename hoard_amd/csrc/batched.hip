@@ -286,10 +286,16 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 // which fold them in ggml's order, so every logit is the single-token router's.
 constexpr int kTileE = 16, kTileT = 16, kTileK = 256;
 
+// K steps in LDS: the current one and the next in flight (four, three in
+// flight, measured the same: with one wave per SIMD the dots' own chains, not
+// the copies, set the pace once one step is prefetched)
+constexpr int kGemmBufs = 2;
 __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
-    __shared__ __align__(16) float wl[kTileE][kTileK];
-    __shared__ __align__(16) float xl[kTileT][kTileK];
-    constexpr int n = kRouteN;
+    __shared__ __align__(16) float wl[kGemmBufs][kTileE][kTileK];
+    __shared__ __align__(16) float xl[kGemmBufs][kTileT][kTileK];
+    constexpr int n = kRouteN, kSteps = n / kTileK;
+    static_assert(kSteps >= kGemmBufs, "the ring is filled before the first step");
+    constexpr int kRowsPerWave = (kTileE + kTileT) / 4;  // copies each wave issues per step
     const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = tid >> 6, lane = tid & 63;
     const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
     const int re = (q & 3) * 4, rt = (q >> 2) * 8;  // this group's 4 experts and 8 tokens within the tile
@@ -298,31 +304,48 @@ __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
-#pragma unroll 1
-    for (int k0 = 0; k0 < n; k0 += kTileK) {
-        // 32 rows of 1 KB: expert rows then token rows, one wave per 8 rows;
-        // rows past the end repeat the last one (their results are not stored)
+    // 32 rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
+    // rows past the end repeat the last one (their results are not stored).  The
+    // next steps' rows are in flight while the current one is dotted.
+    auto issue = [&](int k0, int buf) {
         for (int r = wave; r < kTileE + kTileT; r += 4) {
             const float *src = r < kTileE ? a.router + (size_t)min(e0 + r, a.E - 1) * n
                                           : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
-            float *dst = r < kTileE ? wl[r] : xl[r - kTileE];
+            float *dst = r < kTileE ? wl[buf][r] : xl[buf][r - kTileE];
             dma_chunk(reinterpret_cast<uint8_t *>(dst), reinterpret_cast<const uint8_t *>(src + k0));
         }
-        lds_dma_wait();
+    };
+#pragma unroll
+    for (int b = 0; b < kGemmBufs - 1; ++b) issue(b * kTileK, b);
+#pragma unroll 1
+    for (int st = 0; st < kSteps; ++st) {
+        const int buf = st % kGemmBufs;
+        const int nx = st + kGemmBufs - 1;
+        if (nx < kSteps) issue(nx * kTileK, nx % kGemmBufs);
+        // this step's copies landed: the wave's newer copies (up to kGemmBufs - 1 steps) may still fly
+        const int newer = min(kSteps - 1 - st, kGemmBufs - 1);
+        if (newer == 3)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kRowsPerWave) : "memory");
+        else if (newer == 2)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kRowsPerWave) : "memory");
+        else if (newer == 1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave) : "memory");
+        else
+            lds_dma_wait();
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < kTileK / 32; ++i) {
             float wv[4], xv[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) wv[r] = wl[re + r][32 * i + l];
+            for (int r = 0; r < 4; ++r) wv[r] = wl[buf][re + r][32 * i + l];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) xv[t] = xl[rt + t][32 * i + l];
+            for (int t = 0; t < 8; ++t) xv[t] = xl[buf][rt + t][32 * i + l];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
                 for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
         }
-        __syncthreads();
+        __syncthreads();  // every wave is done with this buffer before it is refilled
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
