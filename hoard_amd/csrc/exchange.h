@@ -54,6 +54,18 @@ __device__ __forceinline__ uint64_t ld_dev64(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Four consecutive words at base + off_bytes (16-byte aligned), read past the
+// L2 like ld_dev64 (cache policy sc1) in one 16-byte buffer load, where four
+// 4-byte loads of lanes 16 bytes apart would each touch every line of the
+// span.  base must be the same in every lane (the buffer descriptor lives in
+// scalar registers); offsets at or past span_bytes read as zero.
+__device__ __forceinline__ float4 ld_dev_f4(const float *base, unsigned span_bytes, unsigned off_bytes) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, (int)span_bytes, 0x00020000);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off_bytes, 0, 16 /* sc1 */);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+
 // Sequence base of a one-launch decode, kept in device memory so that a
 // launch needs no host-side state and a launch replayed from a captured
 // graph tags its words afresh: seq[0] holds the base of the next launch,

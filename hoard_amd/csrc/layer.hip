@@ -675,13 +675,25 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     stamp(3);
     // Q8_K of every unit's h, read past the L2 (it was written on other XCDs)
-    for (int q = wave; q < ns * NBH; q += 8) {
-        const int u = q / NBH, b = q - u * NBH;
-        const float *hp = a.h + (size_t)u * nff + b * QK + 4 * lane;
-        float v[4];
+    // (a wave requests up to four of its blocks, 16 bytes a lane, before it
+    // quantises the first: one round trip for them, not one per block)
+    constexpr int kHBatch = 4;
+    const int nq = ns * NBH;
+    for (int q0 = wave; q0 < nq; q0 += 8 * kHBatch) {
+        float v[kHBatch][4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = __hip_atomic_load(hp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wave_quantize_q8l_regs(v, &q8h[q]);
+        for (int t = 0; t < kHBatch; ++t) {
+            const int q = q0 + 8 * t < nq ? q0 + 8 * t : q0;  // past the last block: the first again
+            const int u = q / NBH, b = q - u * NBH;
+            const float4 f = ld_dev_f4(a.h, (unsigned)(ns * nff * 4), (unsigned)((u * nff + b * QK + 4 * lane) * 4));
+            v[t][0] = f.x;
+            v[t][1] = f.y;
+            v[t][2] = f.z;
+            v[t][3] = f.w;
+        }
+#pragma unroll
+        for (int t = 0; t < kHBatch; ++t)
+            if (q0 + 8 * t < nq) wave_quantize_q8l_regs(v[t], &q8h[q0 + 8 * t]);
     }
     lds_dma_wait();
     if (bad) atomicOr(&flag_s, 1);

@@ -542,25 +542,46 @@ __device__ __forceinline__ float lpb_row_q3k_mem(const uint8_t *row, const Q8L &
     return group_chain_sum<NB>(p, t);
 }
 
+// Wave max of non-negative IEEE floats held as their bit patterns (for such
+// values the order of the patterns is the order of the values, so integer
+// max needs no NaN handling): unsigned max inside each 16-lane row, then
+// across rows through row_bcast:15 (rows 1, 3 take lane 15 / 47) and
+// row_bcast:31 (rows 2, 3 take lane 31); lane 63 ends with the result.
+__device__ __forceinline__ unsigned wave_max_bits(unsigned u) {
+    u = max(u, (unsigned)dpp_i<kDppQuadXor1>((int)u));
+    u = max(u, (unsigned)dpp_i<kDppQuadXor2>((int)u));
+    u = max(u, (unsigned)dpp_i<kDppRowHalfMirror>((int)u));
+    u = max(u, (unsigned)dpp_i<kDppRowMirror>((int)u));
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp((int)u, (int)u, kDppRowBcast15, 0xa, 0xf, false));
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp((int)u, (int)u, kDppRowBcast31, 0xc, 0xf, false));
+    return (unsigned)__builtin_amdgcn_readlane((int)u, 63);
+}
+
 // Q8_K quantisation of 256 values held 4 per lane (lane l: elements 4l..4l+3).
-// The scale comes from the first element (lowest index) of largest magnitude:
-// a wave max of |x|, then the lowest lane holding it and its first component.
+// The scale comes from the first element (lowest index) of largest magnitude;
+// NaN elements never set it.  Magnitudes are compared as bit patterns (NaN
+// patterns cleared to 0 first), which orders them as the values would be, so
+// the wave max is an integer max and the element that holds it is found with
+// one compare per element, one ballot and one read of its lane.
 __device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out) {
     const int lane = threadIdx.x & 63;
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    if (!(amax >= 0.0f)) amax = 0.0f;  // NaN elements never set the scale
-    amax = wave_max_f(amax);
-    if (!(amax > 0.0f)) {  // all zero (or NaN): d = 0, q = 0
+    unsigned b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned m = __float_as_uint(v[i]) & 0x7fffffffu;
+        b[i] = m <= 0x7f800000u ? m : 0u;
+    }
+    const unsigned am = wave_max_bits(max(max(b[0], b[1]), max(b[2], b[3])));
+    if (am == 0u) {  // all zero (or NaN): d = 0, q = 0
         out->qs[lane] = 0;
         if (lane < 16) out->bsums[lane] = 0;
         if (lane == 0) out->d = 0.0f;
         return;
     }
-    const bool has = fabsf(v[0]) == amax || fabsf(v[1]) == amax || fabsf(v[2]) == amax || fabsf(v[3]) == amax;
-    const int src = __ffsll((unsigned long long)__builtin_amdgcn_ballot_w64(has)) - 1;
-    const float c0 = readlane_f(v[0], src), c1 = readlane_f(v[1], src), c2 = readlane_f(v[2], src),
-                c3 = readlane_f(v[3], src);
-    const float mval = fabsf(c0) == amax ? c0 : (fabsf(c1) == amax ? c1 : (fabsf(c2) == amax ? c2 : c3));
+    const bool h0 = b[0] == am, h1 = b[1] == am, h2 = b[2] == am, h3 = b[3] == am;
+    const float c = h0 ? v[0] : (h1 ? v[1] : (h2 ? v[2] : v[3]));
+    const int src = __ffsll((unsigned long long)__builtin_amdgcn_ballot_w64(h0 | h1 | h2 | h3)) - 1;
+    const float mval = readlane_f(c, src);
     const float iscale = -127.0f / mval;
     uint32_t packed = 0;
     int s = 0;

@@ -20,6 +20,8 @@ constexpr int kDppRowRor8 = 0x128;
 constexpr int kDppRowRor12 = 0x12C;  // lane i reads lane i + 4
 constexpr int kDppRowRor14 = 0x12E;  // lane i reads lane i + 2
 constexpr int kDppRowRor15 = 0x12F;  // lane i reads lane i + 1
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row to the next row (row_mask picks rows)
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
 
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
