@@ -206,15 +206,18 @@ struct FusedLayerArgs {
     MatDesc gate, up, down;    // routed experts (stride per expert)
     MatDesc sh_gate, sh_up, sh_down;  // the shared expert (sh_gate.base == nullptr: none)
     const float *sh_gate_inp;  // [n_embd] f32 gate row of the shared expert
-    float *sgate;              // [1] scratch: sigmoid(sh_gate_inp . fx)
+    uint64_t *sgt;             // [1] sigmoid(sh_gate_inp . fx) as a tagged word {value, launch epoch}
     int n_embd, E, k, renorm;
     uint64_t *lgw;             // [8][E] logits as tagged words {value, launch epoch}, one copy per XCD
-    float *h;                  // [k (+1 shared)][n_ff] scratch
+    uint64_t *ht;              // [k (+1 shared)][n_ff] h as tagged words (each block in its XCD's L2)
+    uint32_t *q8d;             // [units * n_ff / 256][kFusedQ8Words] Q8_K(h) blocks
+    uint64_t *q8f;             // [8][128] block flags as tagged words, one line per XCD
     unsigned long long *ctr;   // kFusedCounterWords zeroed words: tickets, completion counts and flags
     int *err;                  // raised by a wait that runs out
     long long wait_ticks;
     unsigned long long *trace; // optional [workgroup][kFusedStamps] wall-clock stamps, by ticket order per XCD
 };
+constexpr int kFusedQ8Words = 76;  // a Q8_K block (256 int8, 16 int16 sums, d, padding) in 32-bit words
 constexpr int kFusedStamps = 6;  // xcd * 65536 + role slot, start, 3 role events, end
 constexpr int kFusedCounterWords = 16 * (8 + 16 + 8);
 bool fused_layer_ok(const FusedLayerArgs &a);

@@ -287,45 +287,29 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 // epoch}, one copy per XCD; every gate/up and down workgroup polls its XCD's
 // copy of all of them and forms the top-k itself (the same code on the same
 // words, so the same experts and weights), and the first down workgroup of
-// XCD 0 forms it once more for the caller's sel / wsel.
-// The counters grow across launches: launch e (ticket / workgroups per XCD)
-// waits for the counts of launch e.  Every value crosses workgroups through
-// device-scope stores and loads (past the per-XCD L2), each counted only after
-// its stores are acknowledged.  What many workgroups wait for (the selection,
-// each slot's h) is published once per XCD, so the waiting spreads over eight
-// lines, and waiters sleep between probes.
+// XCD 0 writes the caller's sel / wsel from its selection.
+// h is formed in 256-row blocks (one Q8_K block each), and a XCD holds whole
+// blocks: the 16 gate/up workgroups of a block store their h as tagged words
+// into its L2, and the block's last workgroup (the latest ticket of the
+// block) waits for them, quantises the block once and publishes it past the
+// L2 with a flag in every XCD's line, which the down workgroups poll
+// (sleeping between probes) before they read the blocks.  The ticket
+// counters grow across launches, so launch e = ticket / workgroups per XCD
+// and every tag is e + 1: words of earlier launches never match.
 constexpr int kFRouteRows = 4;  // router rows per router workgroup
 constexpr int kFGuRows = 16;    // gate rows (and up rows) per gate/up workgroup
 constexpr int kFDownRows = 8;   // output rows per down workgroup
 constexpr int kFXcds = 8;
+constexpr int kFBlockGroups = QK / kFGuRows;         // gate/up workgroups of one 256-row block of h
+constexpr int kQ8Words = kFusedQ8Words;              // a Q8_K block in 32-bit words
+static_assert(kQ8Words * 4 == (int)sizeof(Q8L), "Q8L layout");
+constexpr int kFQ8FlagStride = 128;                   // words per XCD line of block flags (>= blocks)
 // counter words (16 to a 128-byte line)
 constexpr int kFCtrTicket = 0;               // line x: tickets of XCD x
-constexpr int kFCtrH = 16 * 8;               // line 8 + j: gate/up workgroups of slot j done
-constexpr int kFCtrHDone = 16 * 24;          // line 24 + x, word j: slot j's h complete, copy for XCD x
-static_assert(kFCtrHDone + 16 * kFXcds == kFusedCounterWords, "counter lines");
+static_assert(kFCtrTicket + 16 * kFXcds <= kFusedCounterWords, "counter lines");
 
-__device__ __forceinline__ unsigned long long ctr_load(const unsigned long long *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ unsigned long long ctr_add(unsigned long long *p) {
     return __hip_atomic_fetch_add(p, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ctr_store(unsigned long long *p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool reached(unsigned long long v, unsigned long long target) {
-    return (long long)(v - target) >= 0;
-}
-// Bounded wait of one thread for *p to reach `target`, sleeping ~0.2 us between probes.
-__device__ __forceinline__ bool wait_count(const unsigned long long *p, unsigned long long target, int *err,
-                                           long long limit) {
-    return poll(
-        [&]() {
-            if (reached(ctr_load(p), target)) return true;
-            __builtin_amdgcn_s_sleep(8);
-            return false;
-        },
-        err, limit);
 }
 
 // rms_norm scale of x (every thread takes part): mean of x*x in double,
@@ -352,8 +336,9 @@ struct FusedRoles {
     int route, gu, down;
 };
 __host__ __device__ __forceinline__ FusedRoles fused_roles(int E, int ns, int n_ff, int n_embd) {
-    const int r = (E + kFRouteRows - 1) / kFRouteRows, g = ns * (n_ff / kFGuRows), d = n_embd / kFDownRows;
-    return {(r + kFXcds - 1) / kFXcds, (g + kFXcds - 1) / kFXcds, (d + kFXcds - 1) / kFXcds};
+    const int r = (E + kFRouteRows - 1) / kFRouteRows, nq = ns * (n_ff / QK), d = n_embd / kFDownRows;
+    // gate/up: whole blocks per XCD (blocks q = x, x + 8, ... on XCD x)
+    return {(r + kFXcds - 1) / kFXcds, kFBlockGroups * ((nq + kFXcds - 1) / kFXcds), (d + kFXcds - 1) / kFXcds};
 }
 __host__ __device__ __forceinline__ int fused_units(const FusedLayerArgs &a) {
     return a.k + (a.sh_gate.base ? 1 : 0);
@@ -376,18 +361,20 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __shared__ double red[8];
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
-    __shared__ float ps[128];
+    __shared__ unsigned sk_s[kMaxK];  // the taken experts' keys, probabilities and ids (index order)
+    __shared__ float sp_s[kMaxK];
+    __shared__ int si_s[kMaxK];
     __shared__ float lg_s[1024];  // this launch's logits, gathered from the XCD's tagged copy
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, k = a.k, nff = a.gate.rows;
     // The selection in the gate/up and down roles.  select_a (wave 0) waits
     // until every logit of this launch is stored; with E <= 128 it forms the
-    // softmax into ps, as router_tail does (the same loads, reductions and
-    // scale), and select_b (every thread) ranks it: expert e's rank is the
-    // number of experts of larger probability or of equal probability and a
-    // lower index, the order of router_tail's repeated maxima, and ranks below
-    // k fill sel_s / w_s.  With E > 128 wave 0 runs router_tail itself (a
-    // rank over more experts, in two steps or through a threshold, measured
+    // softmax as router_tail does (the same loads, reductions and scale) and
+    // the top-k on the same wave: a bitwise search for the k-th largest
+    // probability, then the taken experts ranked in the order of
+    // router_tail's repeated maxima (larger probability first, lower index on
+    // ties), filling sel_s / w_s.  With E > 128 wave 0 runs router_tail itself
+    // (a rank over more experts, in two steps or through a threshold, measured
     // no faster on 512 threads).  A wait that ran out raises flag_s instead.
     // With E <= 128, w_s holds the raw top-k probabilities until select_renorm.
     const bool rank_sel = E <= 128;
@@ -443,25 +430,56 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         }
         sum = wave_sum_d(sum);
         const float sc = (float)(1.0 / sum);
-        ps[lane] = lane < E ? p0 * sc : -1.0f;  // absent experts below every probability
-        ps[lane + 64] = lane + 64 < E ? p1 * sc : -1.0f;
-    };
-    auto select_b = [&]() {
-        if (!rank_sel || flag_s) return;
-        const int e = tid >> 2, q = tid & 3;  // four threads per expert, 32 comparisons each
-        const float pe = ps[e];
-        int r = 0;
+        p0 = p0 * sc;
+        p1 = p1 * sc;
+        // Top-k on this wave.  Key = probability bits + 1 (the probabilities are
+        // non-negative, so their bit patterns order as they do), 0 for absent
+        // experts and NaN probabilities (all of them are NaN when any is, and
+        // then nothing is selected).  T, the k-th largest key, is found bit by
+        // bit from ballot counts; every key above T is taken, and of those equal
+        // to T the lowest indices, as router_tail's repeated maxima take them.
+        const unsigned k0 = (lane < E && p0 == p0) ? __float_as_uint(p0) + 1u : 0u;
+        const unsigned k1 = (lane + 64 < E && p1 == p1) ? __float_as_uint(p1) + 1u : 0u;
+        unsigned T = 0;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float4 v = *reinterpret_cast<const float4 *>(ps + 32 * q + 4 * c);
-            const int e4 = 32 * q + 4 * c;
-            r += (v.x > pe) | ((v.x == pe) & (e4 < e));
-            r += (v.y > pe) | ((v.y == pe) & (e4 + 1 < e));
-            r += (v.z > pe) | ((v.z == pe) & (e4 + 2 < e));
-            r += (v.w > pe) | ((v.w == pe) & (e4 + 3 < e));
+        for (int bit = 30; bit >= 0; --bit) {
+            const unsigned c = T | (1u << bit);
+            const int cnt = __popcll(__builtin_amdgcn_ballot_w64(k0 >= c)) + __popcll(__builtin_amdgcn_ballot_w64(k1 >= c));
+            T = cnt >= k ? c : T;
         }
-        r = group4_sum(r);
-        if (e < E && q == 0 && r < k && pe == pe) {
+        if (T == 0u) return;  // NaN probabilities: no expert
+        const unsigned long long g0 = __builtin_amdgcn_ballot_w64(k0 > T), g1 = __builtin_amdgcn_ballot_w64(k1 > T);
+        const unsigned long long q0 = __builtin_amdgcn_ballot_w64(k0 == T), q1 = __builtin_amdgcn_ballot_w64(k1 == T);
+        const int need = k - __popcll(g0) - __popcll(g1);  // taken from the keys equal to T, lowest index first
+        const unsigned long long below = (1ull << lane) - 1ull;
+        const bool t0 = k0 > T || (k0 == T && __popcll(q0 & below) < need);
+        const bool t1 = k1 > T || (k1 == T && __popcll(q0) + __popcll(q1 & below) < need);
+        // the k taken experts, in index order, into LDS; then lane i < k ranks
+        // entry i among them: larger key first, lower index (entry) on ties
+        const unsigned long long s0 = __builtin_amdgcn_ballot_w64(t0), s1 = __builtin_amdgcn_ballot_w64(t1);
+        if (t0) {
+            const int at = __popcll(s0 & below);
+            sk_s[at] = k0;
+            sp_s[at] = p0;
+            si_s[at] = lane;
+        }
+        if (t1) {
+            const int at = __popcll(s0) + __popcll(s1 & below);
+            sk_s[at] = k1;
+            sp_s[at] = p1;
+            si_s[at] = lane + 64;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane < k) {
+            const unsigned ki = sk_s[lane];
+            int r = 0;
+            for (int jj = 0; jj < k; ++jj) {
+                const unsigned kj = sk_s[jj];
+                r += (kj > ki) | ((kj == ki) & (jj < lane));
+            }
+            const int e = si_s[lane];
+            const float pe = sp_s[lane];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every lane has read its entry
             sel_s[r] = e;
             w_s[r] = pe;
         }
@@ -491,7 +509,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __syncthreads();
     const unsigned long long ep = tk_s / Gx;
     const int lt = (int)(tk_s - ep * Gx);  // role slot within this XCD's share
-    const int gu_per = nff / kFGuRows, n_gu = ns * gu_per;
+    const int nq = ns * NBH;  // 256-row blocks of h over the units
     // phase stamps: [xcc * Gx + lt][id, start, e1, e2, e3, end]
     unsigned long long *st = a.trace ? a.trace + ((size_t)xcc * Gx + lt) * kFusedStamps : nullptr;
     auto stamp = [&](int i) {
@@ -538,17 +556,21 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     }
 
     if (lt < R.route + R.gu) {
-        // -- gate/up rows [16 r, +16) of slot j (j = k: the shared expert), SwiGLU --
-        const int i = (int)xcc * R.gu + (lt - R.route);
-        if (i >= n_gu) return;  // padding of the XCD shares
-        // the shared expert's workgroups come first: they wait for no selection,
-        // so their rows stream while the router runs
-        const bool shared = has_sh && i < gu_per;
-        const int q = has_sh ? i - gu_per : i;
-        const int j = shared ? k : q / gu_per, r0 = (shared ? i : q - j * gu_per) * kFGuRows;
+        // -- gate/up rows [16 r, +16) of super-block b of unit j, SwiGLU --
+        // A XCD holds whole 256-row blocks: its share is blocks q = x, x + 8, ...
+        // (the shared expert's first), 16 workgroups each, so a block's h stays in
+        // this XCD's L2 and its last workgroup (r = 15, the latest ticket of the
+        // block) quantises it once for every down workgroup.
+        const int g = lt - R.route, r = g % kFBlockGroups, q = (g / kFBlockGroups) * kFXcds + (int)xcc;
+        if (q >= nq) return;  // padding of the XCD shares
+        const bool shared = has_sh && q < NBH;
+        const int j = shared ? k : (q - (has_sh ? NBH : 0)) / NBH;
+        const int b = shared ? q : (q - (has_sh ? NBH : 0)) % NBH;
+        const int r0 = b * QK + r * kFGuRows;
         uint8_t *wt = smem;  // [2][16 rows]
         Q8L *q8 = reinterpret_cast<Q8L *>(smem + 2 * kFGuRows * kGuRowBytes);
         float *gu = reinterpret_cast<float *>(q8 + NB);
+        Q8L *q8b = reinterpret_cast<Q8L *>(gu + 2 * kFGuRows);  // the block's Q8_K(h) (quantiser)
         // gate rows on waves 0-1, up rows on waves 2-3
         auto copy_rows = [&](const MatDesc &G, const MatDesc &U, int id) {
             constexpr int half = (kFGuRows * kGuRowBytes / 2 + 1023) & ~1023;
@@ -562,16 +584,16 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
         if (wave >= 4) {
             // Q8_K of fx while the selection is awaited and the rows are copied
-            for (int b = wave - 4; b < NB; b += 4) {
-                const float4 x4 = *reinterpret_cast<const float4 *>(a.xin + b * QK + 4 * lane);
+            for (int bb = wave - 4; bb < NB; bb += 4) {
+                const float4 x4 = *reinterpret_cast<const float4 *>(a.xin + bb * QK + 4 * lane);
                 const float v[4] = {x4.x * scale, x4.y * scale, x4.z * scale, x4.w * scale};
-                wave_quantize_q8l_regs(v, &q8[b]);
+                wave_quantize_q8l_regs(v, &q8[bb]);
             }
         } else if (wave == 0 && !shared) {
             select_a(ep + 1ull);
         } else if (wave == 0 && r0 == 0 && lane < 32) {
             // the shared expert's sigmoid gate: its f32 row against fx in the
-            // router's order, for the down workgroups (counted with this h)
+            // router's order, for the down workgroups (a tagged word)
             const float *wr = a.sh_gate_inp + lane;
             const float *xr = a.xin + lane;
             float acc = 0.0f;
@@ -579,11 +601,8 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             for (int c = 0; c < N; c += 32) acc = fmaf(wr[c], xr[c] * scale, acc);
             acc = acc + __shfl_xor(acc, 16);
             acc = row16_ggml_fold(acc);
-            if (lane == 0)
-                __hip_atomic_store(a.sgate, 1.0f / (1.0f + expf(-acc)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) st_dev64(a.sgt, tag(1.0f / (1.0f + expf(-acc)), (unsigned)(ep + 1ull)));
         }
-        __syncthreads();
-        if (!shared) select_b();
         __syncthreads();
         stamp(2);
         const int id = shared ? 0 : sel_s[j];
@@ -604,20 +623,47 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             if (t8 == NB - 1) gu[grp] = v;
         }
         __syncthreads();
+        uint64_t *hb = a.ht + (size_t)j * nff + b * QK;  // the block's tagged h, in this XCD's L2
+        const unsigned tg = (unsigned)(ep + 1ull);
         if (tid < kFGuRows) {
-            const float g = gu[tid], u = gu[kFGuRows + tid];
-            const float hv = bad ? __builtin_nanf("") : g / (1.0f + expf(-g)) * u;
-            __hip_atomic_store(a.h + (size_t)j * nff + r0 + tid, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float gv = gu[tid], uv = gu[kFGuRows + tid];
+            const float hv = bad ? __builtin_nanf("") : gv / (1.0f + expf(-gv)) * uv;
+            st_l2(hb + r * kFGuRows + tid, tag(hv, tg));
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // h is acknowledged before it is counted
-        __syncthreads();
         stamp(4);
-        if (tid == 0) {
-            // the slot's last gate/up workgroup publishes the slot's h to every XCD
-            const unsigned long long c = ctr_add(a.ctr + kFCtrH + 16 * j) + 1ull;
-            if (c == (ep + 1ull) * (unsigned long long)gu_per)
-                for (int x = 0; x < kFXcds; ++x) ctr_store(a.ctr + kFCtrHDone + 16 * x + j, ep + 1ull);
+        if (r != kFBlockGroups - 1) {
+            stamp(5);
+            return;
         }
+        // -- the block's quantiser: all 256 h of the block (4 a lane), Q8_K once,
+        // published as tagged words for the down workgroups of every XCD --
+        if (wave == 1) {  // not the wave that stored h: its poll does not wait for those stores
+            uint64_t w[4];
+            const bool got = poll(
+                [&]() {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) w[c] = ld_l2(hb + 4 * lane + c);
+                    bool ok4 = true;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ok4 = ok4 & (tag_seq(w[c]) == tg);
+                    return (bool)__all(ok4);
+                },
+                a.err, a.wait_ticks);
+            const float v[4] = {tag_val(w[0]), tag_val(w[1]), tag_val(w[2]), tag_val(w[3])};
+            wave_quantize_q8l_regs(v, q8b);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the block is in LDS
+            if (got) {
+                // the block's words past the L2, then (once they are acknowledged)
+                // its flag in every XCD's line, which the down workgroups poll
+                const uint32_t *qw = reinterpret_cast<const uint32_t *>(q8b);
+                uint32_t *dst = a.q8d + (size_t)q * kQ8Words;
+                st_dev_u32(dst + lane, qw[lane]);
+                if (lane < kQ8Words - 64) st_dev_u32(dst + 64 + lane, qw[64 + lane]);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                if (lane < kFXcds) st_dev64(a.q8f + (size_t)lane * kFQ8FlagStride + q, tag(0.0f, tg));
+            }
+        }
+        __syncthreads();  // the stamp below marks the block published
         stamp(5);
         return;
     }
@@ -634,8 +680,6 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     if (has_sh && wave == 7)
         wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kFDownRows), kSegBytesS);
     if (wave == 0) select_a(ep + 1ull);
-    __syncthreads();
-    select_b();
     __syncthreads();
     if (wave == 0) select_renorm();
     stamp(2);
@@ -659,49 +703,46 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         a.sel[lane] = flag_s ? 0x7fffffff : sel_s[lane];
         a.wsel[lane] = flag_s ? __builtin_nanf("") : w_s[lane];
     }
-    if (wave == 0 && !flag_s) {
-        // every slot's h complete: lane j watches slot j's word of this XCD's line
-        const unsigned long long *hd = a.ctr + kFCtrHDone + 16 * xcc;
-        const bool ok = poll(
+    // every unit's Q8_K(h), published once per block by its quantiser: wave 0
+    // polls this XCD's line of block flags (sleeping between probes), then every
+    // thread moves 16-byte pieces of the blocks into LDS, read past the L2
+    const unsigned tg = (unsigned)(ep + 1ull);
+    float sgate = 0.0f;
+    if (!flag_s && wave == 0) {
+        const uint64_t *fl = a.q8f + (size_t)xcc * kFQ8FlagStride;
+        const bool got = poll(
             [&]() {
-                const bool r = lane >= ns || reached(ctr_load(hd + lane), ep + 1ull);
+                bool r = true;
+                for (int qq = lane; qq < nq; qq += 64) r = r & (tag_seq(ld_dev64(fl + qq)) == tg);
+                if (has_sh && lane == 0) r = r & (tag_seq(ld_dev64(a.sgt)) == tg);
                 if (__all(r)) return true;
-                __builtin_amdgcn_s_sleep(8);
+                __builtin_amdgcn_s_sleep(1);
                 return false;
             },
             a.err, a.wait_ticks);
-        if (!ok && lane == 0) flag_s = 1;
+        if (!got && lane == 0) flag_s = 1;
     }
     __syncthreads();
-    stamp(3);
-    // Q8_K of every unit's h, read past the L2 (it was written on other XCDs)
-    // (a wave requests up to four of its blocks, 16 bytes a lane, before it
-    // quantises the first: one round trip for them, not one per block)
-    constexpr int kHBatch = 4;
-    const int nq = ns * NBH;
-    for (int q0 = wave; q0 < nq; q0 += 8 * kHBatch) {
-        float v[kHBatch][4];
-#pragma unroll
-        for (int t = 0; t < kHBatch; ++t) {
-            const int q = q0 + 8 * t < nq ? q0 + 8 * t : q0;  // past the last block: the first again
-            const int u = q / NBH, b = q - u * NBH;
-            const float4 f = ld_dev_f4(a.h, (unsigned)(ns * nff * 4), (unsigned)((u * nff + b * QK + 4 * lane) * 4));
-            v[t][0] = f.x;
-            v[t][1] = f.y;
-            v[t][2] = f.z;
-            v[t][3] = f.w;
+    if (!flag_s) {
+        // block q (publication order, the shared expert's first) goes to its place
+        // in unit order (routed slots, then the shared expert)
+        constexpr int kPieces = kQ8Words / 4;  // 16-byte pieces of a block
+        for (int c = tid; c < nq * kPieces; c += 512) {
+            const int qq = c / kPieces, pc = c - qq * kPieces;
+            const int pos = has_sh ? (qq < NBH ? k * NBH + qq : qq - NBH) : qq;
+            const float4 f = ld_dev_f4(reinterpret_cast<const float *>(a.q8d), (unsigned)(nq * kQ8Words * 4),
+                                       (unsigned)((qq * kQ8Words + 4 * pc) * 4));
+            *reinterpret_cast<float4 *>(reinterpret_cast<uint32_t *>(q8h + pos) + 4 * pc) = f;
         }
-#pragma unroll
-        for (int t = 0; t < kHBatch; ++t)
-            if (q0 + 8 * t < nq) wave_quantize_q8l_regs(v[t], &q8h[q0 + 8 * t]);
+        if (has_sh) sgate = tag_val(ld_dev64(a.sgt));
     }
-    lds_dma_wait();
     if (bad) atomicOr(&flag_s, 1);
     __syncthreads();
     if (flag_s) {
         if (tid < kFDownRows) a.out[d0 + tid] = __builtin_nanf("");
         return;
     }
+    stamp(3);
     stamp(4);
     if constexpr (TS == TD) {
         down_rows<TD, NBH, 512>(wd, ns * kFDownRows, 0, q8h, ys);  // the shared segment follows the routed ones
@@ -711,12 +752,11 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     }
     __syncthreads();
     if (tid < kFDownRows) {
-        const int r = tid, d = d0 + r;
+        const int rr = tid, d = d0 + rr;
         float acc = 0.0f;
-        for (int j = 0; j < k; ++j) acc = acc + w_s[j] * ys[j * kFDownRows + r];
+        for (int jj = 0; jj < k; ++jj) acc = acc + w_s[jj] * ys[jj * kFDownRows + rr];
         if (has_sh) {
-            const float sg = __hip_atomic_load(a.sgate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            a.out[d] = (acc + ys[k * kFDownRows + r] * sg) + a.res[d];
+            a.out[d] = (acc + ys[k * kFDownRows + rr] * sgate) + a.res[d];
         } else {
             a.out[d] = acc + a.res[d];
         }
@@ -808,7 +848,7 @@ namespace {
 size_t fused_lds_bytes(const FusedLayerArgs &a) {
     const int nbh = a.down.cols / QK, ns = fused_units(a);
     const size_t gu = 2 * kFGuRows * (size_t)(8 * block_bytes(a.gate.type)) + 8 * sizeof(Q8L) +
-                      2 * kFGuRows * sizeof(float);
+                      2 * kFGuRows * sizeof(float) + sizeof(Q8L);
     const size_t seg_s = a.sh_gate.base ? (size_t)kFDownRows * nbh * block_bytes(a.sh_down.type) : 0;
     const size_t dn = (size_t)a.k * kFDownRows * nbh * block_bytes(a.down.type) + seg_s +
                       (size_t)ns * nbh * sizeof(Q8L) + (size_t)ns * kFDownRows * sizeof(float);
@@ -820,13 +860,13 @@ size_t fused_lds_bytes(const FusedLayerArgs &a) {
 }  // namespace
 
 // The shapes of the fused launch: n_embd 2048, at most 1024 experts; gate/up
-// Q4_K or Q3_K with n_ff a multiple of 16; down Q6_K with 2-4 super-blocks,
+// Q4_K or Q3_K with n_ff a multiple of 256; down Q6_K with 2-4 super-blocks,
 // Q5_K with 2 or 4, or Q4_K with 4 per row; a shared expert of the same gate/up
 // type and width, whose down rows have the routed type (or Q6_K beside Q5_K
 // with 2), at most 16 units in all; 16-byte aligned tensors and activations.
 bool fused_layer_ok(const FusedLayerArgs &a) {
     const bool gu_type = (a.gate.type == kTypeQ4K || a.gate.type == kTypeQ3K) && a.up.type == a.gate.type;
-    if (a.n_embd != 2048 || !gu_type || a.gate.rows % kFGuRows || a.gate.rows != a.up.rows || a.k < 1 ||
+    if (a.n_embd != 2048 || !gu_type || a.gate.rows % QK || a.gate.rows != a.up.rows || a.k < 1 ||
         fused_units(a) > 16 || a.E < a.k || a.E > 1024)
         return false;
     const int nbh = a.down.cols / QK;
@@ -836,10 +876,11 @@ bool fused_layer_ok(const FusedLayerArgs &a) {
     if (!q6 && !q4 && !q5) return false;
     uintptr_t al = reinterpret_cast<uintptr_t>(a.gate.base) | reinterpret_cast<uintptr_t>(a.up.base) |
                    reinterpret_cast<uintptr_t>(a.down.base) | a.gate.stride | a.up.stride | a.down.stride |
-                   reinterpret_cast<uintptr_t>(a.xin) | reinterpret_cast<uintptr_t>(a.h);
+                   reinterpret_cast<uintptr_t>(a.xin);
+    if (!a.ht || !a.q8d || !a.q8f || !a.sgt || fused_units(a) * (a.gate.rows / QK) > kFQ8FlagStride) return false;
     if (a.sh_gate.base) {
         if (a.sh_gate.type != a.gate.type || a.sh_up.type != a.gate.type || a.sh_gate.rows != a.gate.rows ||
-            a.sh_up.rows != a.gate.rows || !a.sh_up.base || !a.sh_down.base || !a.sh_gate_inp || !a.sgate ||
+            a.sh_up.rows != a.gate.rows || !a.sh_up.base || !a.sh_down.base || !a.sh_gate_inp ||
             a.sh_down.cols != a.down.cols)
             return false;
         if (a.sh_down.type != a.down.type && !(a.down.type == kTypeQ5K && a.sh_down.type == kTypeQ6K && nbh == 2))

@@ -110,6 +110,10 @@ struct hoard_moe {
     bool chip_ok = false;              // gfx950 with 8 XCDs of 32 CUs, every expert resident
     unsigned long long *fctr = nullptr;  // the one-launch layer's counters, then its error word
     uint64_t *flgw = nullptr;            // its tagged logits, one copy per XCD
+    uint64_t *fht = nullptr;             // its tagged h, [n_used+1][hstride]
+    uint32_t *fq8d = nullptr;            // its Q8_K(h) blocks, [n_used+1][hstride/256][kFusedQ8Words]
+    uint64_t *fq8f = nullptr;            // their flags (tagged words), [8][128]
+    uint64_t *fsgt = nullptr;            // its tagged shared-expert gate
     unsigned long long *ftrace = nullptr;  // its phase stamps while tracing
     size_t ftrace_words = 0, ftrace_last = 0;
     bool coop_launch = true;           // HOARD_OPT_DECODE_LAUNCH 0: cooperative one-launch decode
@@ -176,6 +180,10 @@ struct hoard_moe {
         hipFree(seqw);
         hipFree(fctr);
         hipFree(flgw);
+        hipFree(fht);
+        hipFree(fq8d);
+        hipFree(fq8f);
+        hipFree(fsgt);
         hipFree(ftrace);
         hipFree(ptrace);
         hipHostFree(pin_sel);
@@ -382,14 +390,16 @@ int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, flo
         a.sh_up = mat(L.sh_up, 0, L.sh_up_type, c.n_ff_shexp, c.n_embd, 1);
         a.sh_down = mat(L.sh_down, 0, L.sh_down_type, c.n_embd, c.n_ff_shexp, 1);
         a.sh_gate_inp = L.sh_gate_inp;
-        a.sgate = h->sgate;
     }
     a.n_embd = c.n_embd;
     a.E = c.n_expert;
     a.k = c.n_used;
     a.renorm = c.renorm;
     a.lgw = h->flgw;
-    a.h = h->hbuf;
+    a.ht = h->fht;
+    a.q8d = h->fq8d;
+    a.q8f = h->fq8f;
+    a.sgt = h->fsgt;
     a.ctr = h->fctr;
     a.err = reinterpret_cast<int *>(h->fctr + hoard::kFusedCounterWords);
     a.wait_ticks = h->wait_ticks;
@@ -873,6 +883,20 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
     rc = rc ? rc : dev_alloc((void **)&h->flgw, sizeof(uint64_t) * 8 * c.n_expert);
     if (!rc && hipMemset(h->flgw, 0, sizeof(uint64_t) * 8 * c.n_expert) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset fused logits");
+    // the one-launch layer's tagged h, Q8_K(h) blocks and shared gate: zeroed,
+    // so no word carries a launch epoch (those start at 1) before it is written
+    {
+        const size_t nht = (size_t)(c.n_used + 1) * h->hstride;
+        const size_t nq8 = (size_t)(c.n_used + 1) * ((h->hstride + 255) / 256) * hoard::kFusedQ8Words;
+        rc = rc ? rc : dev_alloc((void **)&h->fht, sizeof(uint64_t) * nht);
+        rc = rc ? rc : dev_alloc((void **)&h->fq8d, sizeof(uint32_t) * nq8);
+        rc = rc ? rc : dev_alloc((void **)&h->fq8f, sizeof(uint64_t) * 8 * 128);
+        rc = rc ? rc : dev_alloc((void **)&h->fsgt, sizeof(uint64_t));
+        if (!rc && (hipMemset(h->fht, 0, sizeof(uint64_t) * nht) != hipSuccess ||
+                    hipMemset(h->fq8f, 0, sizeof(uint64_t) * 8 * 128) != hipSuccess ||
+                    hipMemset(h->fsgt, 0, sizeof(uint64_t)) != hipSuccess))
+            rc = fail(HOARD_ERR_HIP, "hipMemset one-launch layer exchange words");
+    }
     if (!rc && hipMemset(h->counters, 0, T * sizeof(unsigned)) != hipSuccess)
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
     if (!rc && c.pool_k > 0) {

@@ -212,8 +212,10 @@ int hoard_moe_phase_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, in
    xcd * 65536 + role slot, then the 100 MHz wall clock at its start, three
    role events and its end.  Role slots count router, gate/up and down
    workgroups in that order; the events are the logits stored (router, all
-   three), the selection formed / rows landed / h stored (gate/up), and the
-   selection formed / every h seen / Q8_K(h) formed (down). */
+   three), the selection formed / rows landed / h stored (gate/up, whose end
+   is the block's Q8_K(h) published for the last workgroup of each 256-row
+   block), and the selection formed / every Q8_K(h) block read and rows
+   landed (twice) (down). */
 int hoard_moe_fused_trace_read(hoard_moe *h, uint64_t *out, size_t max_words, size_t *n_words);
 
 /* Options.  HOARD_OPT_PERSISTENT_DECODE selects how hoard_moe_decode runs:
