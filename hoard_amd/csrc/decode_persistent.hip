@@ -179,18 +179,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             // x of this layer: the XCD's 32 workgroups published 64 rows each; gathered
             // by waves 4-7 (wave 0 has just stored its combined rows)
             const uint64_t *xsrc = a.X + ((size_t)cur * kXcds + xcc) * n;
-            // both of the thread's 4-word chunks in one probe: one round trip
-            // once the data is there, not one per chunk
-            static_assert(kEmbd == 8 * (kThreads / 2), "two 4-word chunks per gathering thread");
-            const int i0 = 4 * (tid - kThreads / 2), i1 = i0 + 4 * (kThreads / 2);
+            // all four of the thread's word pairs in one probe (one round trip
+            // once the data is there), each a 16-byte load; pair c of thread t
+            // is words 2 (t + 256 c) and the next, so a wave's load covers 1 KB
+            static_assert(kEmbd == 8 * (kThreads / 2), "four word pairs per gathering thread");
+            const int t = tid - kThreads / 2;
             uint64_t w[8];
             const bool got = poll(
                 [&]() {
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        w[c] = ld_l2(xsrc + i0 + c);
-                        w[4 + c] = ld_l2(xsrc + i1 + c);
-                    }
+                    for (int c = 0; c < 4; ++c)
+                        ld_dev64x2(xsrc, (unsigned)kEmbd, (unsigned)(2 * (t + (kThreads / 2) * c)), w[2 * c], w[2 * c + 1]);
                     bool r = true;
 #pragma unroll
                     for (int c = 0; c < 8; ++c) r = r & (tag_seq(w[c]) == seq - 1u);
@@ -199,12 +198,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
                 a.err, a.wait_ticks);
             if (!got) sh_fail = 1;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const float v[4] = {tag_val(w[4 * h]), tag_val(w[4 * h + 1]), tag_val(w[4 * h + 2]),
-                                    tag_val(w[4 * h + 3])};
-                *reinterpret_cast<float4 *>(xs + (h ? i1 : i0)) = make_float4(v[0], v[1], v[2], v[3]);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) ss += (double)(v[c] * v[c]);
+            for (int c = 0; c < 4; ++c) {
+                const float v0 = tag_val(w[2 * c]), v1 = tag_val(w[2 * c + 1]);
+                *reinterpret_cast<float2 *>(xs + 2 * (t + (kThreads / 2) * c)) = make_float2(v0, v1);
+                ss += (double)(v0 * v0);
+                ss += (double)(v1 * v1);
             }
         }
         ss = wave_sum_d(ss);
@@ -439,15 +437,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             // -- P5: Q8_K(h) of the XCD's expert, down rows, publish y rows --
             if (wave < nbh) {
                 uint64_t w[4];
-                const uint64_t *hsrc = Hx + wave * QK + 4 * lane;
                 const bool got = poll(
                     [&]() {
+                        // words 4 lane .. 4 lane + 3 of block `wave`, two 16-byte loads
+                        ld_dev64x2(Hx, (unsigned)a.n_ff, (unsigned)(wave * QK + 4 * lane), w[0], w[1]);
+                        ld_dev64x2(Hx, (unsigned)a.n_ff, (unsigned)(wave * QK + 4 * lane + 2), w[2], w[3]);
                         bool r = true;
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            w[c] = ld_l2(hsrc + c);
-                            r = r && tag_seq(w[c]) == seq + 1u;
-                        }
+                        for (int c = 0; c < 4; ++c) r = r && tag_seq(w[c]) == seq + 1u;
                         return (bool)__all(r);
                     },
                     a.err, a.wait_ticks);

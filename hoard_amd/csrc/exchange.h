@@ -66,6 +66,19 @@ __device__ __forceinline__ float4 ld_dev_f4(const float *base, unsigned span_byt
     return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
 }
 
+// Two consecutive tagged words base[i], base[i + 1] (i even, base 16-byte
+// aligned), read as ld_l2 / ld_dev64 read one (cache policy sc1) in one
+// 16-byte load; each aligned 8-byte word comes whole from the one transfer.
+// base must be the same in every lane; words at or past span_words read as 0.
+__device__ __forceinline__ void ld_dev64x2(const uint64_t *base, unsigned span_words, unsigned i, uint64_t &w0,
+                                           uint64_t &w1) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t *>(base), 0, (int)(span_words * 8u), 0x00020000);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(i * 8u), 0, 16 /* sc1 */);
+    w0 = ((uint64_t)v[1] << 32) | v[0];
+    w1 = ((uint64_t)v[3] << 32) | v[2];
+}
+
 // Sequence base of a one-launch decode, kept in device memory so that a
 // launch needs no host-side state and a launch replayed from a captured
 // graph tags its words afresh: seq[0] holds the base of the next launch,

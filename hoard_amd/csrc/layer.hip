@@ -641,8 +641,8 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             uint64_t w[4];
             const bool got = poll(
                 [&]() {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) w[c] = ld_l2(hb + 4 * lane + c);
+                    ld_dev64x2(hb, QK, 4 * lane, w[0], w[1]);
+                    ld_dev64x2(hb, QK, 4 * lane + 2, w[2], w[3]);
                     bool ok4 = true;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) ok4 = ok4 & (tag_seq(w[c]) == tg);
