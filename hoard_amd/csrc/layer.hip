@@ -361,22 +361,22 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __shared__ double red[8];
     __shared__ int sel_s[16];
     __shared__ float w_s[16];
-    __shared__ unsigned sk_s[kMaxK];  // the taken experts' keys, probabilities and ids (index order)
-    __shared__ float sp_s[kMaxK];
-    __shared__ int si_s[kMaxK];
+    __shared__ __align__(16) float ps[128];
     __shared__ float lg_s[1024];  // this launch's logits, gathered from the XCD's tagged copy
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, k = a.k, nff = a.gate.rows;
     // The selection in the gate/up and down roles.  select_a (wave 0) waits
     // until every logit of this launch is stored; with E <= 128 it forms the
-    // softmax as router_tail does (the same loads, reductions and scale) and
-    // the top-k on the same wave: a bitwise search for the k-th largest
-    // probability, then the taken experts ranked in the order of
-    // router_tail's repeated maxima (larger probability first, lower index on
-    // ties), filling sel_s / w_s.  With E > 128 wave 0 runs router_tail itself
-    // (a rank over more experts, in two steps or through a threshold, measured
-    // no faster on 512 threads).  A wait that ran out raises flag_s instead.
-    // With E <= 128, w_s holds the raw top-k probabilities until select_renorm.
+    // softmax into ps, as router_tail does (the same loads, reductions and
+    // scale), and select_b (every thread) ranks it: expert e's rank is the
+    // number of experts of larger probability or of equal probability and a
+    // lower index, the order of router_tail's repeated maxima, and ranks below
+    // k fill sel_s / w_s (a bitwise search for the k-th probability on wave
+    // 0 alone measured 0.6 us a layer slower).  With E > 128 wave 0 runs
+    // router_tail itself (a rank over more experts, in two steps or through a
+    // threshold, measured no faster on 512 threads).  A wait that ran out
+    // raises flag_s instead.  With E <= 128, w_s holds the raw top-k
+    // probabilities until select_renorm.
     const bool rank_sel = E <= 128;
     auto select_a = [&](unsigned long long epoch) {
         // every logit of this launch, from this XCD's copy: lanes take experts
@@ -430,56 +430,25 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         }
         sum = wave_sum_d(sum);
         const float sc = (float)(1.0 / sum);
-        p0 = p0 * sc;
-        p1 = p1 * sc;
-        // Top-k on this wave.  Key = probability bits + 1 (the probabilities are
-        // non-negative, so their bit patterns order as they do), 0 for absent
-        // experts and NaN probabilities (all of them are NaN when any is, and
-        // then nothing is selected).  T, the k-th largest key, is found bit by
-        // bit from ballot counts; every key above T is taken, and of those equal
-        // to T the lowest indices, as router_tail's repeated maxima take them.
-        const unsigned k0 = (lane < E && p0 == p0) ? __float_as_uint(p0) + 1u : 0u;
-        const unsigned k1 = (lane + 64 < E && p1 == p1) ? __float_as_uint(p1) + 1u : 0u;
-        unsigned T = 0;
+        ps[lane] = lane < E ? p0 * sc : -1.0f;  // absent experts below every probability
+        ps[lane + 64] = lane + 64 < E ? p1 * sc : -1.0f;
+    };
+    auto select_b = [&]() {
+        if (!rank_sel || flag_s) return;
+        const int e = tid >> 2, q = tid & 3;  // four threads per expert, 32 comparisons each
+        const float pe = ps[e];
+        int r = 0;
 #pragma unroll
-        for (int bit = 30; bit >= 0; --bit) {
-            const unsigned c = T | (1u << bit);
-            const int cnt = __popcll(__builtin_amdgcn_ballot_w64(k0 >= c)) + __popcll(__builtin_amdgcn_ballot_w64(k1 >= c));
-            T = cnt >= k ? c : T;
+        for (int c = 0; c < 8; ++c) {
+            const float4 v = *reinterpret_cast<const float4 *>(ps + 32 * q + 4 * c);
+            const int e4 = 32 * q + 4 * c;
+            r += (v.x > pe) | ((v.x == pe) & (e4 < e));
+            r += (v.y > pe) | ((v.y == pe) & (e4 + 1 < e));
+            r += (v.z > pe) | ((v.z == pe) & (e4 + 2 < e));
+            r += (v.w > pe) | ((v.w == pe) & (e4 + 3 < e));
         }
-        if (T == 0u) return;  // NaN probabilities: no expert
-        const unsigned long long g0 = __builtin_amdgcn_ballot_w64(k0 > T), g1 = __builtin_amdgcn_ballot_w64(k1 > T);
-        const unsigned long long q0 = __builtin_amdgcn_ballot_w64(k0 == T), q1 = __builtin_amdgcn_ballot_w64(k1 == T);
-        const int need = k - __popcll(g0) - __popcll(g1);  // taken from the keys equal to T, lowest index first
-        const unsigned long long below = (1ull << lane) - 1ull;
-        const bool t0 = k0 > T || (k0 == T && __popcll(q0 & below) < need);
-        const bool t1 = k1 > T || (k1 == T && __popcll(q0) + __popcll(q1 & below) < need);
-        // the k taken experts, in index order, into LDS; then lane i < k ranks
-        // entry i among them: larger key first, lower index (entry) on ties
-        const unsigned long long s0 = __builtin_amdgcn_ballot_w64(t0), s1 = __builtin_amdgcn_ballot_w64(t1);
-        if (t0) {
-            const int at = __popcll(s0 & below);
-            sk_s[at] = k0;
-            sp_s[at] = p0;
-            si_s[at] = lane;
-        }
-        if (t1) {
-            const int at = __popcll(s0) + __popcll(s1 & below);
-            sk_s[at] = k1;
-            sp_s[at] = p1;
-            si_s[at] = lane + 64;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane < k) {
-            const unsigned ki = sk_s[lane];
-            int r = 0;
-            for (int jj = 0; jj < k; ++jj) {
-                const unsigned kj = sk_s[jj];
-                r += (kj > ki) | ((kj == ki) & (jj < lane));
-            }
-            const int e = si_s[lane];
-            const float pe = sp_s[lane];
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every lane has read its entry
+        r = group4_sum(r);
+        if (e < E && q == 0 && r < k && pe == pe) {
             sel_s[r] = e;
             w_s[r] = pe;
         }
@@ -604,6 +573,8 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             if (lane == 0) st_dev64(a.sgt, tag(1.0f / (1.0f + expf(-acc)), (unsigned)(ep + 1ull)));
         }
         __syncthreads();
+        if (!shared) select_b();
+        __syncthreads();
         stamp(2);
         const int id = shared ? 0 : sel_s[j];
         const bool bad = !shared && (flag_s || id < 0 || id >= a.gate.n_ids);
@@ -680,6 +651,8 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     if (has_sh && wave == 7)
         wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kFDownRows), kSegBytesS);
     if (wave == 0) select_a(ep + 1ull);
+    __syncthreads();
+    select_b();
     __syncthreads();
     if (wave == 0) select_renorm();
     stamp(2);
