@@ -301,6 +301,156 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
     }
 }
 
+// -- down, Q6_K rows folded for v_mfma_i32_16x16x64_i8 --------------------------
+// Lane l of a wave supplies A[l % 16][16 g .. + 15] (g = l / 16) of each 64-element
+// chunk jc of a super-block: elements 64 jc + 16 g .. + 15 of row l % 16, whose
+// 6-bit values are nibble (jc % 2) of ql bytes 64 (jc / 2) + 16 g .. + 15 with
+// bits 4 (jc % 2) + 2 (g / 2) .. + 1 of qh bytes 128 + 32 (jc / 2) + 16 (g % 2) ..
+// + 15 on top, and which share one group scale, sc = scales[4 jc + g].  The
+// per-token path forms isum = sum_g sc_g * sum_{e in g} (q_e - 32) x_e.  Here
+// w = sc * q (|w| <= 8128) is split as w = 64 hi + lo with lo in [-32, 31] and
+// hi in [-127, 127], both int8, and the zero point comes from a third MFMA with
+// sc broadcast over the lane's 16 elements (the token's group sums):
+// isum = 64 D_hi + D_lo - 32 D_sc, exactly.  A super-block of the tile is
+// folded once and used for every token chunk of the unit.
+struct Q6Fold {
+    v4i hi[4], lo[4], sc[4];
+    float d[4];  // factors of the four rows whose results the lane receives
+};
+
+// 16 bytes at a 2-byte aligned LDS address, as four words.
+__device__ __forceinline__ uint4 lds_u128_a2(const uint8_t *p) {
+    const uint2 a = lds_u64_a2(p), b = lds_u64_a2(p + 8);
+    return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+__device__ __forceinline__ void q6_fold(const uint8_t *T, size_t rb, int b, Q6Fold &o) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const uint8_t *blk = T + (size_t)r * rb + (size_t)b * kQ6KBytes;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        const uint4 ql = lds_u128_a2(blk + 64 * (jc >> 1) + 16 * g);
+        const uint4 qh = lds_u128_a2(blk + 128 + 32 * (jc >> 1) + 16 * (g & 1));
+        const int sc = (int)(int8_t)blk[192 + 4 * jc + g];
+        const uint32_t nsh = 4u * (uint32_t)(jc & 1), hsh = 4u * (uint32_t)(jc & 1) + 2u * (uint32_t)(g >> 1);
+        const uint32_t sc16 = ((uint32_t)sc & 0xffffu) * 0x00010001u;  // sc in both 16-bit halves
+        const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+        int hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = ((qlw[k] >> nsh) & 0x0f0f0f0fu) | (((qhw[k] >> hsh) & 0x03030303u) << 4);
+            // bytes 0, 2 and 1, 3 in 16-bit halves; w = sc * q in each half
+            const uint32_t w02 = __builtin_amdgcn_perm(0u, q, 0x0c020c00u) ;
+            const uint32_t w13 = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);
+            typedef short v2s __attribute__((ext_vector_type(2)));
+            const v2s s2 = __builtin_bit_cast(v2s, sc16);
+            const v2s a02 = __builtin_bit_cast(v2s, w02) * s2, a13 = __builtin_bit_cast(v2s, w13) * s2;
+            // hi = (w + 32) >> 6 (arithmetic), lo = w - 64 hi
+            const v2s h02 = (a02 + (v2s){32, 32}) >> (v2s){6, 6}, h13 = (a13 + (v2s){32, 32}) >> (v2s){6, 6};
+            const v2s l02 = a02 - (h02 << (v2s){6, 6}), l13 = a13 - (h13 << (v2s){6, 6});
+            // back to bytes: result byte 2i from the 02 half i, byte 2i + 1 from the 13 half i
+            hw[k] = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h13), __builtin_bit_cast(uint32_t, h02),
+                                               0x06020400u);
+            lw[k] = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, l13), __builtin_bit_cast(uint32_t, l02),
+                                               0x06020400u);
+        }
+        o.hi[jc] = v4i{hw[0], hw[1], hw[2], hw[3]};
+        o.lo[jc] = v4i{lw[0], lw[1], lw[2], lw[3]};
+        const int s4 = (int)splat_byte((uint32_t)sc & 0xffu);
+        o.sc[jc] = v4i{s4, s4, s4, s4};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint8_t *blk_i = T + (size_t)(4 * g + i) * rb + (size_t)b * kQ6KBytes;
+        o.d[i] = half_bits_to_float((uint32_t)blk_i[208] | ((uint32_t)blk_i[209] << 8));
+    }
+}
+
+// The lane's B operands of one token's Q8_K block: qs bytes 64 jc + 16 g .. + 15.
+struct Q6XB {
+    v4i x[4];
+    float xd;
+};
+__device__ __forceinline__ void q6_load_xb(const Q8L &x, Q6XB &o) {
+    const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) o.x[jc] = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
+    o.xd = x.d;
+}
+
+__device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, float acc[4]) {
+    v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0}, ds = {0, 0, 0, 0};
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        dh = mfma_16x16x64(w.hi[jc], x.x[jc], dh);
+        dl = mfma_16x16x64(w.lo[jc], x.x[jc], dl);
+        ds = mfma_16x16x64(w.sc[jc], x.x[jc], ds);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int isum = 64 * dh[i] + dl[i] - 32 * ds[i];
+        acc[i] = acc[i] + (w.d[i] * x.xd) * (float)isum;
+    }
+}
+
+// grid (n_embd / 64, max units), block 256: as pf_down_kernel for Q6_K rows,
+// super-block major: each super-block of the wave's 16 rows is folded once,
+// then run against every token chunk of the unit.
+template <int NBH>
+__global__ __launch_bounds__(256) void pf_down_q6_kernel(BatchedArgs a) {
+    constexpr int kRowBytes = NBH * kQ6KBytes;
+    constexpr int kTileBytes = kDnRows * kRowBytes;
+    static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
+    __shared__ __align__(16) uint8_t tile[kTileBytes];
+    Unit w;
+    if (!load_unit(a, blockIdx.y, w)) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int rt0 = blockIdx.x * kDnRows;
+    {
+        const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
+        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
+        for (int ck = wave; ck < kChunksTotal; ck += 4)
+            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk(tile + ck * 1024, src + (size_t)ck * 1024);
+        lds_dma_wait();
+    }
+    __syncthreads();
+    const uint8_t *T = tile + wave * kWaveRows * kRowBytes;
+    const int nch = (w.n + 15) >> 4;
+    const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
+    auto x_of = [&](int ch, int b) -> const Q8L & {
+        return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
+    };
+    float acc[kChunks][4];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
+#pragma unroll 1
+    for (int b = 0; b < NBH; ++b) {
+        Q6XB xc;
+        q6_load_xb(x_of(0, b), xc);
+        Q6Fold f;
+        q6_fold(T, kRowBytes, b, f);
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch) {
+            if (ch >= nch) break;
+            Q6XB xn;
+            if (ch + 1 < nch) q6_load_xb(x_of(ch + 1, b), xn);
+            q6_fold_step(f, xc, acc[ch]);
+            xc = xn;
+        }
+    }
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+        const int idx = ch * 16 + c;
+        if (ch < nch && idx < w.n) {
+            const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
+            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * a.k + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
+                make_float4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
+        }
+    }
+}
+
 // -- combine: out[t][d] = (sum_j w[t][j] * y[t][j][d]) + res[t][d], j ascending --
 __global__ __launch_bounds__(256) void pf_combine_kernel(BatchedArgs a) {
     // four consecutive elements a thread (n_embd is a multiple of 1024): at
@@ -342,8 +492,14 @@ hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s) {
     if (a.d_type == T && nbh == N) {                                             \
         hipLaunchKernelGGL((pf_down_kernel<T, N>), dg, dim3(256), 0, s, a);     \
     } else
-    HOARD_DOWN(kTypeQ6K, 3) HOARD_DOWN(kTypeQ6K, 2) HOARD_DOWN(kTypeQ6K, 4) HOARD_DOWN(kTypeQ4K, 4)
-    HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
+    if (a.d_type == kTypeQ6K && nbh == 3) {
+        hipLaunchKernelGGL((pf_down_q6_kernel<3>), dg, dim3(256), 0, s, a);
+    } else if (a.d_type == kTypeQ6K && nbh == 2) {
+        hipLaunchKernelGGL((pf_down_q6_kernel<2>), dg, dim3(256), 0, s, a);
+    } else if (a.d_type == kTypeQ6K && nbh == 4) {
+        hipLaunchKernelGGL((pf_down_q6_kernel<4>), dg, dim3(256), 0, s, a);
+    } else
+    HOARD_DOWN(kTypeQ4K, 4) HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
 #undef HOARD_DOWN
     hipLaunchKernelGGL(pf_combine_kernel, dim3((a.n_embd + 1023) / 1024, a.M), dim3(256), 0, s, a);
     return hipGetLastError();
