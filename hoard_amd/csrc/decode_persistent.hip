@@ -336,8 +336,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
         __builtin_amdgcn_s_waitcnt(0);
         if (has_expert) {
             for (int c = wave; c < kGuChunks; c += kWaves) {
-                dma_chunk(smem + S.gate + c * 1024, gsrc + (size_t)c * 1024);
-                dma_chunk(smem + S.up + c * 1024, usrc + (size_t)c * 1024);
+                dma_chunk_nt(smem + S.gate + c * 1024, gsrc + (size_t)c * 1024);
+                dma_chunk_nt(smem + S.up + c * 1024, usrc + (size_t)c * 1024);
             }
         }
         // Q8_K(fx) while the rows are in flight
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             };
             if constexpr (kCounted) {
                 if (wave == kWaves - 2) {
-                    for (int c = 0; c < kDownChunks; ++c) dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+                    for (int c = 0; c < kDownChunks; ++c) dma_chunk_nt(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
                 } else if (wave < kGuWaves) {
                     gateup_rows();
                     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's gu writes precede its count
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(PersistentArgs a) {
             } else {
                 if (wave >= kWaves - 2)
                     for (int c = wave - (kWaves - 2); c < kDownChunks; c += 2)
-                        dma_chunk(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
+                        dma_chunk_nt(smem + S.down + c * 1024, dsrc + (size_t)c * 1024);
                 gateup_rows();
                 lds_barrier();
                 if (wave == kPublishWave) publish_h();  // not a wave that polls h

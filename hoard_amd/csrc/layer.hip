@@ -40,6 +40,12 @@ __device__ __forceinline__ void wave_copy(uint8_t *dst, const uint8_t *src, int 
     for (int c = 0; c * 1024 < nbytes; ++c)
         if (c * 1024 + 16 * lane < nbytes) dma_chunk(dst + c * 1024, src + (size_t)c * 1024);
 }
+// The same for expert weights, streamed (non-temporal cache policy).
+__device__ __forceinline__ void wave_copy_nt(uint8_t *dst, const uint8_t *src, int nbytes) {
+    const int lane = threadIdx.x & 63;
+    for (int c = 0; c * 1024 < nbytes; ++c)
+        if (c * 1024 + 16 * lane < nbytes) dma_chunk_nt(dst + c * 1024, src + (size_t)c * 1024);
+}
 
 // -- route --------------------------------------------------------------------
 // grid = ceil(E / 4), block = 128.  xin is fx, or (xin_is_residual) x, whose
@@ -547,7 +553,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             const int len = min(half, kFGuRows * kGuRowBytes - off);
             const uint8_t *src =
                 (m ? U.base + (size_t)id * U.stride : G.base + (size_t)id * G.stride) + (size_t)r0 * kGuRowBytes;
-            wave_copy(wt + m * kFGuRows * kGuRowBytes + off, src + off, len);
+            wave_copy_nt(wt + m * kFGuRows * kGuRowBytes + off, src + off, len);
         };
         if (shared && wave < 4) copy_rows(a.sh_gate, a.sh_up, 0);
         const float scale = a.rms ? rms_scale(a.xin, N, a.eps, red) : 1.0f;
@@ -667,8 +673,9 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
             bad = 1;
             continue;
         }
-        if (!flag_s) wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kDnRowBytes,
-                               kSegBytes);
+        if (!flag_s)
+            wave_copy_nt(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kDnRowBytes,
+                         kSegBytes);
     }
     if (caller_sel && wave == 0 && lane < k) {
         // the renormed weights: lane j wrote w_s[j] itself in select_renorm

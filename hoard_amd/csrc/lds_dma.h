@@ -31,6 +31,17 @@ __device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src) {
     dma_lanes(dst, src + (threadIdx.x & 63) * 16);
 }
 
+// The same copy with the non-temporal (streaming) cache policy, for expert
+// weights that are read once per call: the caches keep what is read again
+// (router rows, activations, exchange words) rather than the stream.
+__device__ __forceinline__ void dma_chunk_nt(uint8_t *dst, const uint8_t *src) {
+    const lds_void *lp = (const lds_void *)dst;
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lp);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds),
+                 "v"(src + (threadIdx.x & 63) * 16)
+                 : "memory", "m0");
+}
+
 // Copy nbytes (a multiple of 16) from src to dst with the calling wave alone.
 __device__ __forceinline__ void dma_wave_copy(uint8_t *dst, const uint8_t *src, int nbytes) {
     const int lane = threadIdx.x & 63;
