@@ -576,7 +576,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     const int *tok = a.utok + u * kMaxTok;
     const uint8_t *W = (wave ? a.up + (size_t)e * a.ustride : a.gate + (size_t)e * a.gstride) + (size_t)row0 * kRowBytes;
     if (m >= kMfmaMinTokens) {
-        dma_wave_copy(wt[wave], W, kTileBytes);
+        dma_wave_copy_nt(wt[wave], W, kTileBytes);
         const int c = lane & 15;
         const Q8L *xq = q8(a.q8x) + (size_t)tok[c < m ? c : 0] * NB;
         lds_dma_wait();
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
             const int mc = min(m - c0, kXChunk);
             if (c0 > 0) __syncthreads();  // both waves are done with the previous chunk
             gather_tokens<NB>(xs, a.q8x, tok, c0, mc, m, wave, 2);
-            if (c0 == 0) dma_wave_copy(wt[wave], W, kTileBytes);
+            if (c0 == 0) dma_wave_copy_nt(wt[wave], W, kTileBytes);
             lds_dma_wait();
             __syncthreads();
 #pragma unroll 1
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
     const int *tok = a.utok + u * kMaxTok, *slot = a.uslot + u * kMaxTok;
     const uint8_t *src = a.down + (size_t)e * a.dstride + (size_t)row0 * kRowBytes;
     if (m >= kMfmaMinTokens) {
-        dma_wave_copy(tile, src, kTileBytes);
+        dma_wave_copy_nt(tile, src, kTileBytes);
         const int c = lane & 15;
         const Q8L *xq = q8(a.q8h) + ((size_t)u * kMaxTok + (c < m ? c : 0)) * NBH;
         lds_dma_wait();
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
         const int mc = min(m - c0, kXChunk);
         // the group's Q8_K h rows are contiguous, token-major
         dma_wave_copy(xs, a.q8h + ((size_t)u * kMaxTok + c0) * NBH * sizeof(Q8L), mc * NBH * (int)sizeof(Q8L));
-        if (c0 == 0) dma_wave_copy(tile, src, kTileBytes);
+        if (c0 == 0) dma_wave_copy_nt(tile, src, kTileBytes);
         lds_dma_wait();
 #pragma unroll 1
         for (int c = 0; c < mc; ++c) {

@@ -112,11 +112,18 @@ struct SpreadShape {
 // round-robin to nw waves; the calling wave is number wrel of them.  Lanes
 // past the end copy nothing, so exactly [src, src + nbytes) is read.
 // Returns the chunk number after this segment.
+// NT: expert weights, copied with the non-temporal (streaming) cache policy.
+template <bool NT = false>
 __device__ __forceinline__ int dma_seg(uint8_t *dst, const uint8_t *src, int nbytes, int base, int wrel, int nw) {
     const int lane = threadIdx.x & 63;
     const int nch = (nbytes + 1023) >> 10;
     for (int c = ((wrel - base) % nw + nw) % nw; c < nch; c += nw)
-        if (c * 1024 + 16 * lane < nbytes) dma_chunk(dst + c * 1024, src + (size_t)c * 1024);
+        if (c * 1024 + 16 * lane < nbytes) {
+            if constexpr (NT)
+                dma_chunk_nt(dst + c * 1024, src + (size_t)c * 1024);
+            else
+                dma_chunk(dst + c * 1024, src + (size_t)c * 1024);
+        }
     return base + nch;
 }
 
@@ -227,8 +234,8 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
                         4 * RR * kEmbd, b, wrel, nw);
         if constexpr (SH) {
             b = dma_seg(smem + S::oSGR, reinterpret_cast<const uint8_t *>(L.sh_gate_inp), 4 * kEmbd, b, wrel, nw);
-            b = dma_seg(smem + S::oSHGU, L.sh_gate + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
-            b = dma_seg(smem + S::oSHGU + HS * RBG, L.sh_up + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
+            b = dma_seg<true>(smem + S::oSHGU, L.sh_gate + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
+            b = dma_seg<true>(smem + S::oSHGU + HS * RBG, L.sh_up + (size_t)g * HS * RBG, HS * RBG, b, wrel, nw);
         }
     };
 
@@ -408,10 +415,10 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
             __builtin_amdgcn_s_waitcnt(0);  // ordinary loads first: the copies retire behind them
             const size_t e0 = (size_t)expert(u0), e1 = n1 ? (size_t)expert(u0 + 1) : 0;
             int b = 0;
-            b = dma_seg(smem + S::oGU, L.gate + e0 * L.gstride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
-            if (n1) b = dma_seg(smem + S::oGU + n0 * RBG, L.gate + e1 * L.gstride, n1 * RBG, b, wave, 6);
-            b = dma_seg(smem + S::oGU + HR * RBG, L.up + e0 * L.ustride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
-            if (n1) b = dma_seg(smem + S::oGU + (HR + n0) * RBG, L.up + e1 * L.ustride, n1 * RBG, b, wave, 6);
+            b = dma_seg<true>(smem + S::oGU, L.gate + e0 * L.gstride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
+            if (n1) b = dma_seg<true>(smem + S::oGU + n0 * RBG, L.gate + e1 * L.gstride, n1 * RBG, b, wave, 6);
+            b = dma_seg<true>(smem + S::oGU + HR * RBG, L.up + e0 * L.ustride + (size_t)r0 * RBG, n0 * RBG, b, wave, 6);
+            if (n1) b = dma_seg<true>(smem + S::oGU + (HR + n0) * RBG, L.up + e1 * L.ustride, n1 * RBG, b, wave, 6);
         } else if (wave == 7) {
             // renormalise the weights (read only by the combine): every lane forms the
             // same left-to-right sum; lane j normalises weight j
@@ -452,10 +459,10 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
         const uint8_t *srcA = ua < K ? L.down + (size_t)expert(ua) * L.dstride : L.sh_down;
         const uint8_t *srcB = ua + 1 < K ? L.down + (size_t)expert(ua + 1) * L.dstride : L.sh_down;
         if (wave == 6) {
-            const int b = dma_seg(smem + S::oDN, srcA + (size_t)ba * BLK * RBa, na * BLK * RBa, 0, 0, 1);
-            if (nbb && !S::kTwoCopyWaves) dma_seg(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, b, 0, 1);
+            const int b = dma_seg<true>(smem + S::oDN, srcA + (size_t)ba * BLK * RBa, na * BLK * RBa, 0, 0, 1);
+            if (nbb && !S::kTwoCopyWaves) dma_seg<true>(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, b, 0, 1);
         } else if (S::kTwoCopyWaves && wave == 5) {
-            if (nbb) dma_seg(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, 0, 0, 1);
+            if (nbb) dma_seg<true>(smem + S::oDN + na * BLK * RBa, srcB, nbb * BLK * RBb, 0, 0, 1);
         } else if (wave < S::kGuWaves) {
             if (grp < NGU) {
                 // one row per 8-lane group: the lane reads its activation block as it goes

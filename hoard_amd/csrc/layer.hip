@@ -147,7 +147,7 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
         constexpr int half = (kGuRows * kRowBytes / 2 + 1023) & ~1023;
         const int m = wave >> 1, off = (wave & 1) * half;
         const int len = min(half, kGuRows * kRowBytes - off);
-        wave_copy(wt[m] + off, (m ? usrc : gsrc) + off, len);
+        wave_copy_nt(wt[m] + off, (m ? usrc : gsrc) + off, len);
         lds_dma_wait();
     } else {
         for (int b = wave - 4; b < NB; b += 4) wave_quantize_q8l(a.fx + b * QK, &q8[b]);
@@ -248,10 +248,10 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
                     bad = 1;
                     continue;
                 }
-                wave_copy(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kRowBytes,
+                wave_copy_nt(wd + u * kSegBytes, a.down.base + (size_t)id * a.down.stride + (size_t)d0 * kRowBytes,
                           kSegBytes);
             } else {
-                wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kDownRows), kSegBytesS);
+                wave_copy_nt(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kDownRows), kSegBytesS);
             }
         }
     } else {
@@ -655,7 +655,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     // the shared expert's rows need no selection: copied at once (not by wave
     // 0, whose probes would queue behind the copy)
     if (has_sh && wave == 7)
-        wave_copy(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kFDownRows), kSegBytesS);
+        wave_copy_nt(wd + k * kSegBytes, a.sh_down.base + (size_t)d0 * (kSegBytesS / kFDownRows), kSegBytesS);
     if (wave == 0) select_a(ep + 1ull);
     __syncthreads();
     select_b();

@@ -50,6 +50,14 @@ __device__ __forceinline__ void dma_wave_copy(uint8_t *dst, const uint8_t *src, 
     }
 }
 
+// dma_wave_copy with the non-temporal cache policy, for expert weights.
+__device__ __forceinline__ void dma_wave_copy_nt(uint8_t *dst, const uint8_t *src, int nbytes) {
+    const int lane = threadIdx.x & 63;
+    for (int c = 0; c < nbytes; c += 1024) {
+        if (c + 16 * lane < nbytes) dma_chunk_nt(dst + c, src + c);
+    }
+}
+
 // Workgroup barrier after this wave's LDS operations: the data the waves
 // exchange goes through LDS, so the vector-memory counters need not drain.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

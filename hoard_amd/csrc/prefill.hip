@@ -262,7 +262,7 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
         const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
         constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
         for (int ck = wave; ck < kChunksTotal; ck += 4)
-            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk(tile + ck * 1024, src + (size_t)ck * 1024);
+            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
         lds_dma_wait();
     }
     __syncthreads();
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256) void pf_down_q6_kernel(BatchedArgs a) {
         const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
         constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
         for (int ck = wave; ck < kChunksTotal; ck += 4)
-            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk(tile + ck * 1024, src + (size_t)ck * 1024);
+            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
         lds_dma_wait();
     }
     __syncthreads();
