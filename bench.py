@@ -8,10 +8,12 @@ activation chain never leaving the device.  Inputs are resident before the
 timed region starts.
 
 Prints ONE JSON line (rank 0).  `value` is microseconds per MoE layer per token
-(lower is better); `drop_in_layer_us` is the same layer through hoard_moe_layer
-(three launches per layer, the entry point an engine calls when attention runs
-between MoE layers); `roofline` covers the dominant kernel, timed with a HIP
-event pair around each of its launches on the stream it runs on;
+(lower is better); `step_layer_us` gives p10 / p50 / p90 of single steps
+(an event pair around each), per layer; `drop_in_layer_us` is the same layer
+through hoard_moe_layer (one launch per layer, the entry point an engine calls
+when attention runs between MoE layers); `roofline` covers the dominant
+kernel, timed with a HIP event pair around each of its launches on the stream
+it runs on;
 `cpu_baseline` is the C restatement of ggml-CPU's algorithm for the same stage
 on this host's cores.
 """
@@ -633,6 +635,16 @@ def main():
     drop_in_us = ev0.elapsed_time(ev1) * 1000.0 / (steps * n_layer)
     assert torch.isfinite(xl).all().item(), "non-finite hoard_moe_layer output"
 
+    # ---- the spread of single steps: an event pair around each of `steps` steps --
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        step(warm + i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    step_us = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in evs])
+    step_pct = {f"p{q}": round(float(np.percentile(step_us, q)) / n_layer, 3) for q in (10, 50, 90)}
+
     # ---- per-kernel durations: a HIP event pair around every launch, on its stream --
     H.check(lib.hoard_moe_profile(h, 1))
     for i in range(warm, warm + steps):
@@ -672,6 +684,7 @@ def main():
                                f"ff {shape.n_ff}, all experts resident in HBM",
                    "tokens_per_step": 1, "layers": n_layer},
         "tokens_per_s": round(1000.0 / ms_per_step, 2),
+        "step_layer_us": step_pct,
         "layer_hbm_gbps": round(layer_gbps, 1),
         "layer_hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "layer_bytes": layer_bytes,
