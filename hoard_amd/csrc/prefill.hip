@@ -314,8 +314,9 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
 // isum = 64 D_hi + D_lo - 32 D_sc, exactly.  A super-block of the tile is
 // folded once and used for every token chunk of the unit.
 struct Q6Fold {
-    v4i hi[4], lo[4], sc[4];
-    float d[4];  // factors of the four rows whose results the lane receives
+    v4i hi[4], lo[4];
+    uint32_t sc;  // byte jc: the group scale of the lane's elements of chunk jc
+    float d[4];   // factors of the four rows whose results the lane receives
 };
 
 // 16 bytes at a 2-byte aligned LDS address, as four words.
@@ -356,8 +357,8 @@ __device__ __forceinline__ void q6_fold(const uint8_t *T, size_t rb, int b, Q6Fo
         }
         o.hi[jc] = v4i{hw[0], hw[1], hw[2], hw[3]};
         o.lo[jc] = v4i{lw[0], lw[1], lw[2], lw[3]};
-        const int s4 = (int)splat_byte((uint32_t)sc & 0xffu);
-        o.sc[jc] = v4i{s4, s4, s4, s4};
+        if (jc == 0) o.sc = 0u;
+        o.sc |= ((uint32_t)sc & 0xffu) << (8 * jc);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -384,7 +385,8 @@ __device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, flo
     for (int jc = 0; jc < 4; ++jc) {
         dh = mfma_16x16x64(w.hi[jc], x.x[jc], dh);
         dl = mfma_16x16x64(w.lo[jc], x.x[jc], dl);
-        ds = mfma_16x16x64(w.sc[jc], x.x[jc], ds);
+        const int s4 = (int)splat_byte((w.sc >> (8 * jc)) & 0xffu);
+        ds = mfma_16x16x64(v4i{s4, s4, s4, s4}, x.x[jc], ds);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -395,9 +397,11 @@ __device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, flo
 
 // grid (n_embd / 64, max units), block 256: as pf_down_kernel for Q6_K rows,
 // super-block major: each super-block of the wave's 16 rows is folded once,
-// then run against every token chunk of the unit.
+// then run against every token chunk of the unit.  Three workgroups per CU
+// (148 VGPRs, no prefetch of the next chunk's operands): 227 against 231 us
+// a layer at M = 512 for two workgroups with the prefetch.
 template <int NBH>
-__global__ __launch_bounds__(256) void pf_down_q6_kernel(BatchedArgs a) {
+__global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     constexpr int kRowBytes = NBH * kQ6KBytes;
     constexpr int kTileBytes = kDnRows * kRowBytes;
     static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
@@ -427,17 +431,14 @@ __global__ __launch_bounds__(256) void pf_down_q6_kernel(BatchedArgs a) {
         for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
 #pragma unroll 1
     for (int b = 0; b < NBH; ++b) {
-        Q6XB xc;
-        q6_load_xb(x_of(0, b), xc);
         Q6Fold f;
         q6_fold(T, kRowBytes, b, f);
 #pragma unroll
         for (int ch = 0; ch < kChunks; ++ch) {
             if (ch >= nch) break;
-            Q6XB xn;
-            if (ch + 1 < nch) q6_load_xb(x_of(ch + 1, b), xn);
+            Q6XB xc;
+            q6_load_xb(x_of(ch, b), xc);
             q6_fold_step(f, xc, acc[ch]);
-            xc = xn;
         }
     }
 #pragma unroll
