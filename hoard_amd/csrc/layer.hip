@@ -299,7 +299,7 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
 // into its L2, and the block's last workgroup (the latest ticket of the
 // block) waits for them, quantises the block once and publishes it past the
 // L2 with a flag in every XCD's line, which the down workgroups poll
-// (sleeping between probes) before they read the blocks.  The ticket
+// before they read the blocks.  The ticket
 // counters grow across launches, so launch e = ticket / workgroups per XCD
 // and every tag is e + 1: words of earlier launches never match.
 constexpr int kFRouteRows = 4;  // router rows per router workgroup
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     auto select_a = [&](unsigned long long epoch) {
         // every logit of this launch, from this XCD's copy: lanes take experts
         // lane, lane + 64, ...; a probe that finds a word of an earlier launch
-        // sleeps and probes again
+        // probes again at once (a sleep between probes measured slower)
         const unsigned tg = (unsigned)epoch;
         const uint64_t *src = a.lgw + (size_t)xcc_id() * E;
         const int per = (E + 63) >> 6;
@@ -402,9 +402,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
                         lg_s[e] = tag_val(w);
                     }
                 }
-                if (__all(r)) return true;
-                __builtin_amdgcn_s_sleep(2);
-                return false;
+                return (bool)__all(r);
             },
             a.err, a.wait_ticks);
         if (!got) {
@@ -684,7 +682,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
         a.wsel[lane] = flag_s ? __builtin_nanf("") : w_s[lane];
     }
     // every unit's Q8_K(h), published once per block by its quantiser: wave 0
-    // polls this XCD's line of block flags (sleeping between probes), then every
+    // polls this XCD's line of block flags (no sleep between probes), then every
     // thread moves 16-byte pieces of the blocks into LDS, read past the L2
     const unsigned tg = (unsigned)(ep + 1ull);
     float sgate = 0.0f;
@@ -695,9 +693,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
                 bool r = true;
                 for (int qq = lane; qq < nq; qq += 64) r = r & (tag_seq(ld_dev64(fl + qq)) == tg);
                 if (has_sh && lane == 0) r = r & (tag_seq(ld_dev64(a.sgt)) == tg);
-                if (__all(r)) return true;
-                __builtin_amdgcn_s_sleep(1);
-                return false;
+                return (bool)__all(r);
             },
             a.err, a.wait_ticks);
         if (!got && lane == 0) flag_s = 1;
