@@ -414,20 +414,24 @@ def run_batched(args, shape, n_layer):
     kt = H.KernelTimes()
     H.check(lib.hoard_moe_profile_read(h, ctypes.byref(kt)))
     lib.hoard_moe_destroy(h)
-    eb = shape.expert_bytes()
-    layer_bytes = float(uniq.mean()) * eb + 4 * shape.n_expert * shape.n_embd + M * 4 * shape.n_embd * 2
+    # a shared expert (and its gate row) is read once per layer and taken by every token
+    eb, sb = shape.expert_bytes(), shape.shared_bytes() + (4 * shape.n_embd if shape.n_ff_shexp else 0)
+    layer_bytes = float(uniq.mean()) * eb + sb + 4 * shape.n_expert * shape.n_embd + M * 4 * shape.n_embd * 2
     kb = H.KERNEL_BATCHED
     bat_us = kt.total_ms[kb] / max(1, kt.launches[kb]) * 1000.0
-    bat_bytes = float(uniq.mean()) * eb + M * 4 * shape.n_embd * 2
+    bat_bytes = float(uniq.mean()) * eb + sb + M * 4 * shape.n_embd * 2
     gbps = bat_bytes / bat_us / 1e3
     macs_per_pair = 3 * shape.n_ff * shape.n_embd
-    int8_ops = 2 * macs_per_pair * int(hist.sum())
+    sh_pairs = M * n_layer if shape.n_ff_shexp else 0  # the shared expert's group: all M tokens
+    int8_ops = 2 * macs_per_pair * (int(hist.sum()) + sh_pairs)
     # verify-sized batches run groups of MFMA_MIN_TOKENS or more on MFMA; prefill-sized
     # ones (more than 16 tokens) run every group on MFMA
     mfma_groups = hist >= (MFMA_MIN_TOKENS if M <= 16 else 1)
-    mfma_ops = 2 * macs_per_pair * int(hist[mfma_groups].sum())
+    sh_mfma = sh_pairs if (M > 16 or M >= MFMA_MIN_TOKENS) else 0
+    mfma_ops = 2 * macs_per_pair * (int(hist[mfma_groups].sum()) + sh_mfma)
     result = {
-        "metric": f"batched MoE-layer us per step of {M} tokens + HBM GB/s, Qwen3-30B-A3B-shape Q4_K",
+        "metric": f"batched MoE-layer us per step of {M} tokens + HBM GB/s, "
+                  f"{MODEL_NAMES[shape.name]}-shape {TYPE_NAMES[shape.gate_type]}",
         "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_K/q6_K weights x q8_K activations (int8 dot / MFMA), f32 router/accumulate",

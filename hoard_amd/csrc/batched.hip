@@ -112,6 +112,19 @@ __device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ys
         a.utok[g * kMaxTok + c] = t;
         a.uslot[g * kMaxTok + c] = j;
     }
+    if (a.sh) {
+        // the shared expert: group n_unique (after the routed groups), every
+        // token, slot k
+        const int g = wave_total;
+        for (int t = tid; t < a.M; t += nt) {
+            a.utok[g * kMaxTok + t] = t;
+            a.uslot[g * kMaxTok + t] = a.k;
+        }
+        if (tid == 0) {
+            a.uexp[g] = a.n_ids;
+            a.ucount[g] = a.M;
+        }
+    }
     if (tid == 0) a.n_unique[0] = wave_total;
 }
 
@@ -119,7 +132,7 @@ __device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ys
 // g.cnt (wave 0 of the grouping workgroup): uexp / ucount / goff / units / hist,
 // n_unique / n_units, and g.base[e], the first sorted place of expert e.
 __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
-    const int tid = threadIdx.x, E = a.n_ids;
+    const int tid = threadIdx.x, E = a.n_ids + a.sh;
     {
         // groups and units in ascending expert order: lane owns a contiguous run of experts
         const int lane = tid, per = (E + 63) / 64, e0 = lane * per;
@@ -159,7 +172,7 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
             pi += c;
         }
         if (lane == 63) {
-            a.n_unique[0] = ig;
+            a.n_unique[0] = ig - a.sh;  // routed experts used
             a.n_units[0] = iu;
         }
     }
@@ -174,7 +187,7 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
 // place is its expert's running base plus the tokens of its chunk before it
 // that select the same expert (a token joins a group at most once).
 __device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
-    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids + a.sh, k = a.k + a.sh, P = a.M * k;
     for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
     __syncthreads();
     for (int p = tid; p < P; p += nt)
@@ -210,8 +223,9 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
     const int tg = blockIdx.y;
     const int t = tg * kRouteTok + wave;  // this wave's token; its half-waves take one row each
+    // rows 0..E-1 are the router's; row E (with a shared expert) is its gate row
     const int r0 = blockIdx.x * kRouteRows;
-    const int nrows = min(kRouteRows, E - r0);
+    const int nrows = min(kRouteRows, E + a.sh - r0);
     // the workgroup's token rows and router rows go to LDS in one burst, so
     // that every load is in flight at once; the dot then reads them in the
     // per-lane order the accumulation needs
@@ -219,10 +233,14 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     __shared__ __align__(16) float wl[kRouteRows][kRouteN];
     if (t < a.M) dma_wave_copy(reinterpret_cast<uint8_t *>(xl[wave]), reinterpret_cast<const uint8_t *>(a.fx + (size_t)t * n),
                                n * (int)sizeof(float));
-    {
-        const int wbytes = nrows * n * (int)sizeof(float), per = wbytes / 4;  // a quarter per wave
-        dma_wave_copy(reinterpret_cast<uint8_t *>(wl[0]) + wave * per,
-                      reinterpret_cast<const uint8_t *>(a.router + (size_t)r0 * n) + wave * per, per);
+    static_assert(kRouteRows == 2, "a row per wave pair");
+    if ((wave >> 1) < nrows) {
+        // half (wave & 1) of row r0 + (wave >> 1)
+        constexpr int half = n * (int)sizeof(float) / 2;
+        const int row = r0 + (wave >> 1);
+        const float *src = row < E ? a.router + (size_t)row * n : a.sh_gate_inp;
+        dma_wave_copy(reinterpret_cast<uint8_t *>(wl[wave >> 1]) + (wave & 1) * half,
+                      reinterpret_cast<const uint8_t *>(src) + (wave & 1) * half, half);
     }
     lds_dma_wait();
     __syncthreads();
@@ -240,6 +258,8 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
         acc = acc + __shfl_xor(acc, 2);
         if (l == 0 && row < E)
             __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else if (l == 0 && row == E && a.sh)
+            a.sgl[t] = acc;
         // Q8_K of fx: workgroup i of a token group quantises blocks i, i + gridDim.x, ...
         // of its tokens, so every block is formed whatever the expert count (grid width)
         for (int b = blockIdx.x; b < nb; b += gridDim.x) wave_quantize_q8l(x + b * QK, q8(a.q8x) + (size_t)t * nb + b);
@@ -306,10 +326,13 @@ __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
         for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
     // 32 rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
     // rows past the end repeat the last one (their results are not stored).  The
-    // next steps' rows are in flight while the current one is dotted.
+    // next steps' rows are in flight while the current one is dotted.  Expert
+    // row E (with a shared expert) is the shared expert's gate row.
+    const int er = a.E + a.sh;
     auto issue = [&](int k0, int buf) {
         for (int r = wave; r < kTileE + kTileT; r += 4) {
-            const float *src = r < kTileE ? a.router + (size_t)min(e0 + r, a.E - 1) * n
+            const int row = min(e0 + r, er - 1);
+            const float *src = r < kTileE ? (row < a.E ? a.router + (size_t)row * n : a.sh_gate_inp)
                                           : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
             float *dst = r < kTileE ? wl[buf][r] : xl[buf][r - kTileE];
             dma_chunk(reinterpret_cast<uint8_t *>(dst), reinterpret_cast<const uint8_t *>(src + k0));
@@ -356,8 +379,25 @@ __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
             v = row16_ggml_fold(v);
             const int e = e0 + re + r, tok = t0 + rt + t;
             if (l == 0 && e < a.E && tok < a.M) a.logits[(size_t)tok * a.E + e] = v;
+            if (l == 0 && e == a.E && a.sh && tok < a.M) a.sgl[tok] = v;
         }
     (void)lane;
+}
+
+// w . x over kRouteN elements in the router's order (lane l of 32 owns
+// elements l, l + 32, ...; ggml's f32 dot fold), from memory; every lane of
+// the wave returns it.
+__device__ __forceinline__ float router_order_dot(const float *w, const float *x) {
+    const int l = threadIdx.x & 31;
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int i = 0; i < kRouteN; i += 32) acc = fmaf(w[i + l], x[i + l], acc);
+    acc = acc + __shfl_xor(acc, 16);
+    acc = acc + __shfl_xor(acc, 8);
+    acc = acc + __shfl_xor(acc, 4);
+    acc = acc + __shfl_xor(acc, 1);
+    acc = acc + __shfl_xor(acc, 2);
+    return acc;
 }
 
 // One token per workgroup of 512 threads: wave 0 runs the router tail
@@ -390,7 +430,8 @@ __global__ __launch_bounds__(512) void route_tails_kernel(BatchedArgs a) {
                                                       __HIP_MEMORY_SCOPE_AGENT)
                                   : 0;
         const int e = pair_expert(id, lane, a.k, a.n_ids);
-        if (lane < a.k) a.pexp[(size_t)t * a.k + lane] = e;
+        const int kk = a.k + a.sh;  // pair (t, k): the shared expert, id n_ids
+        if (lane < kk) a.pexp[(size_t)t * kk + lane] = lane < a.k ? e : a.n_ids;
     }
     if (wave < nb) wave_quantize_q8l(a.fx + (size_t)t * kRouteN + wave * QK, q8(a.q8x) + (size_t)t * nb + wave);
 }
@@ -411,13 +452,20 @@ __global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
             const int o = __shfl(id, i);
             if (i < lane && o == id) first = i;
         }
+        const int kk = k + a.sh;  // pair (t, k): the shared expert, id n_ids
         if (lane < k) {
             a.ysrc[(size_t)t * k + lane] = first;
-            a.pexp[(size_t)t * k + lane] = (bad || first != lane) ? -1 : id;
+            a.pexp[(size_t)t * kk + lane] = (bad || first != lane) ? -1 : id;
+        } else if (lane < kk) {
+            a.pexp[(size_t)t * kk + lane] = a.n_ids;
         }
         if (lane == 0) a.bad[t] = bad ? 1 : 0;
     }
     if (wave < nb) wave_quantize_q8l(a.fx + (size_t)t * kRouteN + wave * QK, q8(a.q8x) + (size_t)t * nb + wave);
+    if (a.sh && wave == 1) {
+        const float v = router_order_dot(a.sh_gate_inp, a.fx + (size_t)t * kRouteN);
+        if (lane == 0) a.sgl[t] = v;
+    }
 }
 
 // The grouping of a prefill-sized batch, in one workgroup: the pairs' experts
@@ -430,7 +478,7 @@ __global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
 // Three barriers in all, where the chunk loop takes four per chunk.
 constexpr int kGroupChunkWords = 4096;
 __device__ void group_large_chunks(const BatchedArgs &a, GroupLds &g, const int *pe, unsigned *cm, int *cb) {
-    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids, P = a.M * a.k, k = a.k;
+    const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids + a.sh, k = a.k + a.sh, P = a.M * k;
     const int nch = (a.M + 31) >> 5;
     for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
     for (int i = tid; i < nch * E; i += nt) cm[i] = 0u;
@@ -470,10 +518,10 @@ __global__ __launch_bounds__(1024) void group_kernel(BatchedArgs a) {
     __shared__ int pe[kBatchedMaxTokensLarge * kMaxK];
     __shared__ unsigned cm[kGroupChunkWords];
     __shared__ int cb[kGroupChunkWords];
-    const int P = a.M * a.k;
+    const int P = a.M * (a.k + a.sh);
     for (int p = threadIdx.x; p < P; p += blockDim.x) pe[p] = a.pexp[p];
     __syncthreads();
-    if (((a.M + 31) >> 5) * a.n_ids <= kGroupChunkWords)
+    if (((a.M + 31) >> 5) * (a.n_ids + a.sh) <= kGroupChunkWords)
         group_large_chunks(a, g, pe, cm, cb);
     else
         group_large(a, g, pe);
@@ -492,6 +540,10 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
         const int t = blockIdx.x;
         for (int b = wave; b < nb; b += 8)
             wave_quantize_q8l(a.fx + (size_t)t * kRouteN + b * QK, q8(a.q8x) + (size_t)t * nb + b);
+        if (a.sh && wave == 0) {
+            const float v = router_order_dot(a.sh_gate_inp, a.fx + (size_t)t * kRouteN);
+            if ((threadIdx.x & 63) == 0) a.sgl[t] = v;
+        }
         return;
     }
     __shared__ int bad_s[kMaxTok];
@@ -527,7 +579,7 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
 // too keeps the compiler from moving their loads after the test (a group
 // always has an expert >= 0 and a token).
 __device__ __forceinline__ bool load_group(const BatchedArgs &a, int u, int &e, int &m) {
-    const int nu = a.n_unique[0];
+    const int nu = a.n_unique[0] + a.sh;  // the shared expert's group follows the routed ones
     e = a.uexp[u];
     m = min(a.ucount[u], kMaxTok);
     return (u < nu) & (e >= 0) & (m >= 1);
@@ -574,7 +626,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kRows;
     const int *tok = a.utok + u * kMaxTok;
-    const uint8_t *W = (wave ? a.up + (size_t)e * a.ustride : a.gate + (size_t)e * a.gstride) + (size_t)row0 * kRowBytes;
+    const uint8_t *W = (wave ? batched_up(a, e) : batched_gate(a, e)) + (size_t)row0 * kRowBytes;
     if (m >= kMfmaMinTokens) {
         dma_wave_copy_nt(wt[wave], W, kTileBytes);
         const int c = lane & 15;
@@ -616,7 +668,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
 // -- Q8_K of h per (expert, token) ---------------------------------------------
 __global__ __launch_bounds__(64) void quant_h_kernel(BatchedArgs a) {
     const int u = blockIdx.z, c = blockIdx.y, b = blockIdx.x;
-    if (u >= a.n_unique[0] || c >= min(a.ucount[u], kMaxTok)) return;
+    if (u >= a.n_unique[0] + a.sh || c >= min(a.ucount[u], kMaxTok)) return;
     const int nbh = a.n_ff / QK;
     const size_t uc = (size_t)u * kMaxTok + c;
     wave_quantize_q8l(a.hbuf + uc * a.n_ff + (size_t)b * QK, q8(a.q8h) + uc * nbh + b);
@@ -638,7 +690,8 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
     const int lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kTile;
     const int *tok = a.utok + u * kMaxTok, *slot = a.uslot + u * kMaxTok;
-    const uint8_t *src = a.down + (size_t)e * a.dstride + (size_t)row0 * kRowBytes;
+    const uint8_t *src = batched_down(a, e) + (size_t)row0 * kRowBytes;
+    const int kk = a.k + a.sh;  // output slots per token
     if (m >= kMfmaMinTokens) {
         dma_wave_copy_nt(tile, src, kTileBytes);
         const int c = lane & 15;
@@ -650,7 +703,7 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
         else
             tile_q6k<NBH>(tile, kRowBytes, xq, v);
         if (c < m) {
-            float *y = a.ybuf + ((size_t)tok[c] * a.k + slot[c]) * a.n_embd + row0;
+            float *y = a.ybuf + ((size_t)tok[c] * kk + slot[c]) * a.n_embd + row0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) y[4 * (lane >> 4) + i] = v[i];
         }
@@ -665,7 +718,7 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
         lds_dma_wait();
 #pragma unroll 1
         for (int c = 0; c < mc; ++c) {
-            float *y = a.ybuf + ((size_t)tok[c0 + c] * a.k + slot[c0 + c]) * a.n_embd + row0;
+            float *y = a.ybuf + ((size_t)tok[c0 + c] * kk + slot[c0 + c]) * a.n_embd + row0;
             if constexpr (TD == kTypeQ6K) {
 #pragma unroll 1
                 for (int p = 0; p < 2; ++p) {
@@ -695,10 +748,15 @@ __global__ __launch_bounds__(256) void combine_kernel(BatchedArgs a) {
         a.out[(size_t)t * a.n_embd + d] = __builtin_nanf("");
         return;
     }
+    const int kk = a.k + a.sh;
     float acc = 0.0f;
     for (int j = 0; j < a.k; ++j) {
         const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
-        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * a.k + js) * a.n_embd + d];
+        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * kk + js) * a.n_embd + d];
+    }
+    if (a.sh) {  // + sigmoid(gate logit) * shared expert output
+        const float sg = 1.0f / (1.0f + expf(-a.sgl[t]));
+        acc = acc + a.ybuf[((size_t)t * kk + a.k) * a.n_embd + d] * sg;
     }
     a.out[(size_t)t * a.n_embd + d] = acc + a.res[(size_t)t * a.n_embd + d];
 }
@@ -715,7 +773,7 @@ namespace {
 // The launches after the grouping: gate/up, Q8_K(h), down, combine.
 hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
     const int nbh = a.n_ff / QK;
-    const int umax = a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k;
+    const int umax = (a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k) + a.sh;
     hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, kMaxTok, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
@@ -732,7 +790,8 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
 
 bool args_ok(const BatchedArgs &a) {
     return a.M >= 1 && a.M <= kBatchedMaxTokensLarge && a.n_embd == kRouteN && a.gu_type == kTypeQ4K &&
-           a.k <= kMaxK && a.n_ids >= 1 && a.n_ids <= kMaxExperts && a.E <= kMaxExperts &&
+           a.k + a.sh <= kMaxK && a.n_ids >= 1 && a.n_ids + a.sh <= kMaxExperts && a.E + a.sh <= kMaxExperts &&
+           (!a.sh || (a.sh == 1 && a.sh_gate && a.sh_up && a.sh_down && a.sh_gate_inp && a.sgl)) &&
            (a.M <= kMaxTok || (a.goff && a.ptok && a.pslot && a.pexp && a.units && a.n_units && a.max_units >= 1));
 }
 
@@ -744,13 +803,13 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
         return hipErrorInvalidValue;
     if (a.M > kMaxTok) {
-        hipLaunchKernelGGL(route_gemm_kernel, dim3((a.E + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT),
+        hipLaunchKernelGGL(route_gemm_kernel, dim3((a.E + a.sh + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT),
                            dim3(256), 0, s, a);
         hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(512), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
     }
-    hipLaunchKernelGGL(route_kernel, dim3((a.E + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
+    hipLaunchKernelGGL(route_kernel, dim3((a.E + a.sh + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
                        dim3(256), 0, s, a);
     return launch_groups(a, s);
 }

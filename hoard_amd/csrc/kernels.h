@@ -82,7 +82,7 @@ struct BatchedArgs {
     uint8_t *q8x;           // Q8_K(fx): [M][n_embd/256] blocks of 304 bytes
     uint8_t *q8h;           // Q8_K(h):  [umax][16][n_ff/256] blocks
     float *hbuf;            // [umax][16][n_ff]
-    float *ybuf;            // [M][k][n_embd]
+    float *ybuf;            // [M][k + sh][n_embd]: slot k holds the shared expert's output
     int *n_unique;          // [1]
     int *slot_of;           // [E] scratch
     int *uexp, *ucount;     // [umax] expert of each group, tokens in it
@@ -100,7 +100,24 @@ struct BatchedArgs {
     int *units;             // [max_units][3] group, first pair within the group, pairs
     int *n_units;           // [1]
     int max_units;
+    // The gated shared expert (sh = 1): every token's pair (t, k) with the
+    // expert id n_ids, whose weights are these tensors (n_ff rows, the routed
+    // experts' types), and out = (sum_j w_j y_j + sigmoid(sgl[t]) * y_k) + res.
+    int sh;                       // 1 with a shared expert, else 0
+    const uint8_t *sh_gate, *sh_up, *sh_down;
+    const float *sh_gate_inp;     // [n_embd] f32 gate row of the shared expert
+    float *sgl;                   // [M] sh_gate_inp . fx[t] (the logit, before the sigmoid)
 };
+// Expert e's matrices in a batched call; e == n_ids is the shared expert.
+__device__ __forceinline__ const uint8_t *batched_gate(const BatchedArgs &a, int e) {
+    return a.sh && e == a.n_ids ? a.sh_gate : a.gate + (size_t)e * a.gstride;
+}
+__device__ __forceinline__ const uint8_t *batched_up(const BatchedArgs &a, int e) {
+    return a.sh && e == a.n_ids ? a.sh_up : a.up + (size_t)e * a.ustride;
+}
+__device__ __forceinline__ const uint8_t *batched_down(const BatchedArgs &a, int e) {
+    return a.sh && e == a.n_ids ? a.sh_down : a.down + (size_t)e * a.dstride;
+}
 constexpr int kBatchedMaxTokens = 16;         // the verify-sized path: per-token dots or MFMA per group
 constexpr int kBatchedMaxTokensLarge = 512;   // the prefill-sized path: sorted pairs, MFMA units
 constexpr int kUnitTokens = 64;               // pairs of one expert per prefill work unit

@@ -1146,12 +1146,14 @@ struct BatchedLayout {
     int T, Ts, umax, umax_s, max_units;
     size_t q8x, q8h, hbuf, ybuf, n_ints, hist, counters;  // bytes (n_ints: ints)
     size_t o_slot_of, o_uexp, o_ucount, o_utok, o_uslot, o_ysrc, o_bad, o_goff, o_ptok, o_pslot, o_pexp, o_units,
-        o_nunits;
+        o_nunits, o_sgl;
 };
 
 BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
     BatchedLayout L{};
-    const int k = c.n_used, E = c.n_expert;  // the slots of a pool never outnumber the experts
+    // a shared expert is one more expert id, paired with every token at slot n_used
+    const int sh = c.n_ff_shexp > 0 ? 1 : 0;
+    const int k = c.n_used + sh, E = c.n_expert + sh;  // the slots of a pool never outnumber the experts
     const int nb = c.n_embd / 256, nbh = c.n_ff / 256;
     L.T = T;
     L.Ts = std::min(T, hoard::kBatchedMaxTokens);
@@ -1182,6 +1184,7 @@ BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
     L.o_pexp = take(pairs);
     L.o_units = take((size_t)3 * L.max_units);
     L.o_nunits = take(1);
+    L.o_sgl = take(T);  // floats
     L.n_ints = o;
     L.hist = sizeof(unsigned) * E;
     L.counters = sizeof(unsigned) * hoard::kBatchedCounters;
@@ -1208,7 +1211,8 @@ void bind_batched(hoard::BatchedArgs &a, const BatchedLayout &L, uint8_t *q8x, u
     a.pexp = ints + L.o_pexp;
     a.units = ints + L.o_units;
     a.n_units = ints + L.o_nunits;
-    a.max_units = hoard::prefill_max_units(a.M, a.k, a.n_ids);
+    a.max_units = hoard::prefill_max_units(a.M, a.k + a.sh, a.n_ids + a.sh);
+    a.sgl = reinterpret_cast<float *>(ints + L.o_sgl);
     a.hist = hist;
     a.counters = counters;
 }
@@ -1226,8 +1230,20 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
         return fail(HOARD_ERR_INVALID, "M %d outside 1..min(max_tokens %d, %d)", M, c.max_tokens, max_m);
     if (c.pool_k > 0 && !pooled_ok)
         return fail(HOARD_ERR_UNSUPPORTED, "batched routing needs every expert resident (pool_k 0)");
-    if (c.n_ff_shexp > 0) return fail(HOARD_ERR_UNSUPPORTED, "batched path has no shared expert");
     const Layer &L = h->layers[layer];
+    const bool sh = c.n_ff_shexp > 0;
+    if (sh) {
+        // the shared expert runs as one more expert of the routed experts' kernels
+        if (c.n_ff_shexp != c.n_ff || L.sh_gate_type != L.gate_type || L.sh_up_type != L.up_type ||
+            L.sh_down_type != L.down_type)
+            return fail(HOARD_ERR_UNSUPPORTED,
+                        "batched path: the shared expert (n_ff %d, types %d/%d/%d) must match the routed experts'",
+                        c.n_ff_shexp, L.sh_gate_type, L.sh_up_type, L.sh_down_type);
+        if (c.n_used + 1 > 16) return fail(HOARD_ERR_UNSUPPORTED, "batched path: n_used %d with a shared expert", c.n_used);
+        if (((uintptr_t)L.sh_gate | (uintptr_t)L.sh_up | (uintptr_t)L.sh_down) & 15)
+            return fail(HOARD_ERR_UNSUPPORTED, "batched path: shared expert matrices must be 16-byte aligned");
+        if (!L.sh_gate_inp) return fail(HOARD_ERR_STATE, "shared expert gate row missing");
+    }
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
@@ -1258,6 +1274,11 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     a.gstride = L.gstride;
     a.ustride = L.ustride;
     a.dstride = L.dstride;
+    a.sh = sh ? 1 : 0;
+    a.sh_gate = L.sh_gate;
+    a.sh_up = L.sh_up;
+    a.sh_down = L.sh_down;
+    a.sh_gate_inp = L.sh_gate_inp;
     *out = a;
     return HOARD_OK;
 }

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * kGuRows + rt * kWaveRows;
     constexpr size_t rb = (size_t)NB * kQ4KBytes;
-    const uint8_t *W = (m ? a.up + (size_t)w.e * a.ustride : a.gate + (size_t)w.e * a.gstride) + (size_t)row0 * rb;
+    const uint8_t *W = (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)row0 * rb;
     const int nch = (w.n + 15) >> 4;
     // this lane's granules of the x copy: chunks wave, wave + 4, ...; only the
     // unit's token chunks are copied, token places past its end copy its last token
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
     const int rt0 = blockIdx.x * kDnRows;
     {
         // the burst split over the four waves, 1 KB chunks each
-        const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
+        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * kRowBytes;
         constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
         for (int ck = wave; ck < kChunksTotal; ck += 4)
             if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = TD == kTypeQ4K ? acc[i] - accm[i] : acc[i];
-                *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * a.k + j) * a.n_embd + rt0 + wave * kWaveRows +
+                *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows +
                                             4 * q) = make_float4(v[0], v[1], v[2], v[3]);
             }
 #pragma unroll
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
     {
-        const uint8_t *src = a.down + (size_t)w.e * a.dstride + (size_t)rt0 * kRowBytes;
+        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * kRowBytes;
         constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
         for (int ck = wave; ck < kChunksTotal; ck += 4)
             if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
         const int idx = ch * 16 + c;
         if (ch < nch && idx < w.n) {
             const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
-            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * a.k + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
+            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
                 make_float4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
         }
     }
@@ -466,15 +466,24 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(BatchedArgs a) {
         *o = make_float4(nan, nan, nan, nan);
         return;
     }
+    const int kk = a.k + a.sh;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j = 0; j < a.k; ++j) {
         const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
         const float w = a.wsel[t * a.k + j];
-        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * a.k + js) * a.n_embd + d);
+        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + js) * a.n_embd + d);
         acc.x = acc.x + w * y.x;
         acc.y = acc.y + w * y.y;
         acc.z = acc.z + w * y.z;
         acc.w = acc.w + w * y.w;
+    }
+    if (a.sh) {  // + sigmoid(gate logit) * shared expert output
+        const float sg = 1.0f / (1.0f + expf(-a.sgl[t]));
+        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + a.k) * a.n_embd + d);
+        acc.x = acc.x + y.x * sg;
+        acc.y = acc.y + y.y * sg;
+        acc.z = acc.z + y.z * sg;
+        acc.w = acc.w + y.w * sg;
     }
     const float4 r = *reinterpret_cast<const float4 *>(a.res + (size_t)t * a.n_embd + d);
     *o = make_float4(acc.x + r.x, acc.y + r.y, acc.z + r.z, acc.w + r.w);
@@ -487,7 +496,7 @@ hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s) {
     if (a.n_embd != 2048 || a.n_ff % kGuRows || a.n_embd % kDnRows || nbh > 4 || a.max_units < 1)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(pf_gateup_kernel<8>, dim3(a.n_ff / kGuRows, a.max_units), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(pf_quant_h_kernel, dim3(a.M * a.k), dim3(64 * nbh), 0, s, a);
+    hipLaunchKernelGGL(pf_quant_h_kernel, dim3(a.M * (a.k + a.sh)), dim3(64 * nbh), 0, s, a);
     const dim3 dg(a.n_embd / kDnRows, a.max_units);
 #define HOARD_DOWN(T, N)                                                         \
     if (a.d_type == T && nbh == N) {                                             \

@@ -142,8 +142,10 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
    hoard_moe_layer's bit for bit.  M > 512 returns HOARD_ERR_INVALID.  fx_dev, res_dev, out_dev:
    [M][n_embd], 16-byte aligned (out may alias res); sel_dev / w_dev ([M][n_used]) receive the
    routing when non-NULL.  The call's per-expert token histogram and unique
-   expert count are reported by hoard_moe_get_stats.  Needs pool_k == 0 and no
-   shared expert. */
+   expert count are reported by hoard_moe_get_stats.  Needs pool_k == 0.  A
+   shared expert (n_ff_shexp > 0) must have the routed experts' n_ff and types
+   and n_used <= 15: it runs as one more expert taken by every token, gated by
+   sigmoid(ffn_gate_inp_shexp . fx) as in hoard_moe_layer. */
 int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
                               float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 
@@ -168,8 +170,9 @@ int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const floa
    given (no renormalisation).  out[t] = res[t] + sum_j w[t][j] y(ids[t][j]), j
    ascending.  A token may repeat an id (the verify loop pads with a repeated id
    of weight 0); a token with an id outside the pool or expert set gets a NaN
-   row.  1 <= M <= min(max_tokens, 512).  Each token's result equals
-   hoard_moe_ffn_combine's for that token. */
+   row.  A shared expert adds its gated output as in hoard_moe_ffn_combine
+   (with hoard_moe_forward_batched's limits on it).  1 <= M <= min(max_tokens,
+   512).  Each token's result equals hoard_moe_ffn_combine's for that token. */
 int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const int32_t *ids_dev,
                                   const float *w_dev, const float *res_dev, float *out_dev, void *stream);
 

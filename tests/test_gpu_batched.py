@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.OLMOE], ids=lambda s: s.name)
+@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.OLMOE, W.QWEN3_NEXT], ids=lambda s: s.name)
 def stage(request):
     from hoard_amd.runtime import MoEStage
     shape = request.param
