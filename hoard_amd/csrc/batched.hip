@@ -23,7 +23,7 @@ namespace {
 constexpr int kTile = 16;                   // weight rows per MFMA tile
 constexpr int kMaxTok = kBatchedMaxTokens;  // token columns per MFMA tile
 constexpr int kMfmaMinTokens = 12;          // smallest expert group computed on MFMA
-constexpr int kXChunk = 4;                  // tokens of Q8_K x staged in LDS at a time
+constexpr int kXChunk = 1;                  // tokens of Q8_K x staged in LDS at a time
 constexpr int kMaxExperts = 1024;
 static_assert(sizeof(Q8L) == kQ8LBytes, "Q8_K block size shared with the host");
 
@@ -32,9 +32,10 @@ __device__ __forceinline__ Q8L *q8(uint8_t *p) { return reinterpret_cast<Q8L *>(
 // -- route: router logits, softmax / top-k, Q8_K of fx, grouping by expert ----
 // One launch replaces the router kernels and the grouping pass.  A workgroup
 // (4 waves) takes kRouteRows router rows against kRouteTok tokens, a wave per
-// token and a half-wave per row, with the single-token router's per-row
-// accumulation order
-// (lane l of 32 owns elements l, l+32, ...; ggml's f32 dot fold).  The last
+// token and a half-wave per row at a time, with the single-token router's
+// per-row accumulation order (lane l of 32 owns elements l, l+32, ...; ggml's
+// f32 dot fold).  Two rows per workgroup measured best at 4 and 16 tokens
+// (four: -0.5 us at 16 tokens, +1.2 us at 4; eight: slower at both).  The last
 // workgroup of a token group (device-scope counter) runs the tails of its
 // tokens; the last token group's tail workgroup then groups the (token, slot)
 // pairs by expert.  Waves with a spare slot quantise fx to Q8_K.
@@ -233,33 +234,37 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     __shared__ __align__(16) float wl[kRouteRows][kRouteN];
     if (t < a.M) dma_wave_copy(reinterpret_cast<uint8_t *>(xl[wave]), reinterpret_cast<const uint8_t *>(a.fx + (size_t)t * n),
                                n * (int)sizeof(float));
-    static_assert(kRouteRows == 2, "a row per wave pair");
-    if ((wave >> 1) < nrows) {
-        // half (wave & 1) of row r0 + (wave >> 1)
-        constexpr int half = n * (int)sizeof(float) / 2;
-        const int row = r0 + (wave >> 1);
-        const float *src = row < E ? a.router + (size_t)row * n : a.sh_gate_inp;
-        dma_wave_copy(reinterpret_cast<uint8_t *>(wl[wave >> 1]) + (wave & 1) * half,
-                      reinterpret_cast<const uint8_t *>(src) + (wave & 1) * half, half);
+    {
+        // the rows' 1 KB pieces, dealt to the four waves in turn
+        constexpr int kPieces = n * (int)sizeof(float) / 1024;
+        for (int c = wave; c < nrows * kPieces; c += 4) {
+            const int rr = c / kPieces, o = (c % kPieces) * 1024;
+            const float *src = r0 + rr < E ? a.router + (size_t)(r0 + rr) * n : a.sh_gate_inp;
+            dma_chunk(reinterpret_cast<uint8_t *>(wl[rr]) + o, reinterpret_cast<const uint8_t *>(src) + o);
+        }
     }
     lds_dma_wait();
     __syncthreads();
-    const int row = r0 + (lane >> 5);
     if (t < a.M) {
         const float *x = xl[wave];
-        const float *wr = wl[min(lane >> 5, nrows - 1)];
-        float acc = 0.0f;
+        // half-wave h takes rows rp + h, rp = 0, 2, ...
+#pragma unroll 1
+        for (int rp = 0; rp < kRouteRows; rp += 2) {
+            const int row = r0 + rp + (lane >> 5);
+            const float *wr = wl[min(rp + (lane >> 5), nrows - 1)];
+            float acc = 0.0f;
 #pragma unroll 16
-        for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l], acc);
-        acc = acc + __shfl_xor(acc, 16);
-        acc = acc + __shfl_xor(acc, 8);
-        acc = acc + __shfl_xor(acc, 4);
-        acc = acc + __shfl_xor(acc, 1);
-        acc = acc + __shfl_xor(acc, 2);
-        if (l == 0 && row < E)
-            __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else if (l == 0 && row == E && a.sh)
-            a.sgl[t] = acc;
+            for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l], acc);
+            acc = acc + __shfl_xor(acc, 16);
+            acc = acc + __shfl_xor(acc, 8);
+            acc = acc + __shfl_xor(acc, 4);
+            acc = acc + __shfl_xor(acc, 1);
+            acc = acc + __shfl_xor(acc, 2);
+            if (l == 0 && row < E)
+                __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else if (l == 0 && row == E && a.sh)
+                a.sgl[t] = acc;
+        }
         // Q8_K of fx: workgroup i of a token group quantises blocks i, i + gridDim.x, ...
         // of its tokens, so every block is formed whatever the expert count (grid width)
         for (int b = blockIdx.x; b < nb; b += gridDim.x) wave_quantize_q8l(x + b * QK, q8(a.q8x) + (size_t)t * nb + b);
@@ -668,10 +673,19 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
 // -- Q8_K of h per (expert, token) ---------------------------------------------
 __global__ __launch_bounds__(64) void quant_h_kernel(BatchedArgs a) {
     const int u = blockIdx.z, c = blockIdx.y, b = blockIdx.x;
-    if (u >= a.n_unique[0] + a.sh || c >= min(a.ucount[u], kMaxTok)) return;
     const int nbh = a.n_ff / QK;
     const size_t uc = (size_t)u * kMaxTok + c;
-    wave_quantize_q8l(a.hbuf + uc * a.n_ff + (size_t)b * QK, q8(a.q8h) + uc * nbh + b);
+    // h is loaded with the group count and size, not after them (its place
+    // does not depend on them; a place past the groups is in the buffer and
+    // its values are dropped), all three as vector loads in flight together
+    // (u < the grid's umax keeps them in bounds)
+    const int nu = __hip_atomic_load(a.n_unique, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + a.sh;
+    const int cnt = __hip_atomic_load(a.ucount + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float4 v4 = *reinterpret_cast<const float4 *>(a.hbuf + uc * a.n_ff + (size_t)b * QK + 4 * (threadIdx.x & 63));
+    asm volatile("" ::"v"(v4.x), "v"(v4.y), "v"(v4.z), "v"(v4.w));  // the load is not moved past the test
+    if (u >= nu || c >= min(cnt, kMaxTok)) return;
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    wave_quantize_q8l_regs(v, q8(a.q8h) + uc * nbh + b);
 }
 
 // -- down: one 16-row tile of one expert; y to Y[token][slot] -------------------
@@ -749,16 +763,27 @@ __global__ __launch_bounds__(256) void combine_kernel(BatchedArgs a) {
         return;
     }
     const int kk = a.k + a.sh;
-    float acc = 0.0f;
-    for (int j = 0; j < a.k; ++j) {
-        const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
-        acc = acc + a.wsel[t * a.k + j] * a.ybuf[((size_t)t * kk + js) * a.n_embd + d];
+    // every load is issued before the first is used: one memory latency, not k
+    float w[kMaxK], y[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j < a.k) {
+            const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
+            w[j] = a.wsel[t * a.k + j];
+            y[j] = a.ybuf[((size_t)t * kk + js) * a.n_embd + d];
+        }
     }
+    const float ysh = a.sh ? a.ybuf[((size_t)t * kk + a.k) * a.n_embd + d] : 0.0f;
+    const float r = a.res[(size_t)t * a.n_embd + d];
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+        if (j < a.k) acc = acc + w[j] * y[j];
     if (a.sh) {  // + sigmoid(gate logit) * shared expert output
         const float sg = 1.0f / (1.0f + expf(-a.sgl[t]));
-        acc = acc + a.ybuf[((size_t)t * kk + a.k) * a.n_embd + d] * sg;
+        acc = acc + ysh * sg;
     }
-    a.out[(size_t)t * a.n_embd + d] = acc + a.res[(size_t)t * a.n_embd + d];
+    a.out[(size_t)t * a.n_embd + d] = acc + r;
 }
 
 }  // namespace

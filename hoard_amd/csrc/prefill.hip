@@ -25,6 +25,7 @@
 #include "mfma.h"
 #include "qblocks.h"
 #include "rowdot.h"
+#include "router_tail.h"
 
 namespace hoard {
 
@@ -467,25 +468,37 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(BatchedArgs a) {
         return;
     }
     const int kk = a.k + a.sh;
+    // every load is issued before the first is used: one memory latency, not k
+    float w[kMaxK];
+    float4 y[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j < a.k) {
+            const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
+            w[j] = a.wsel[t * a.k + j];
+            y[j] = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + js) * a.n_embd + d);
+        }
+    }
+    const float4 ysh = a.sh ? *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + a.k) * a.n_embd + d)
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 r = *reinterpret_cast<const float4 *>(a.res + (size_t)t * a.n_embd + d);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int j = 0; j < a.k; ++j) {
-        const int js = a.ysrc ? a.ysrc[t * a.k + j] : j;  // a repeated id takes its first output
-        const float w = a.wsel[t * a.k + j];
-        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + js) * a.n_embd + d);
-        acc.x = acc.x + w * y.x;
-        acc.y = acc.y + w * y.y;
-        acc.z = acc.z + w * y.z;
-        acc.w = acc.w + w * y.w;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j < a.k) {
+            acc.x = acc.x + w[j] * y[j].x;
+            acc.y = acc.y + w[j] * y[j].y;
+            acc.z = acc.z + w[j] * y[j].z;
+            acc.w = acc.w + w[j] * y[j].w;
+        }
     }
     if (a.sh) {  // + sigmoid(gate logit) * shared expert output
         const float sg = 1.0f / (1.0f + expf(-a.sgl[t]));
-        const float4 y = *reinterpret_cast<const float4 *>(a.ybuf + ((size_t)t * kk + a.k) * a.n_embd + d);
-        acc.x = acc.x + y.x * sg;
-        acc.y = acc.y + y.y * sg;
-        acc.z = acc.z + y.z * sg;
-        acc.w = acc.w + y.w * sg;
+        acc.x = acc.x + ysh.x * sg;
+        acc.y = acc.y + ysh.y * sg;
+        acc.z = acc.z + ysh.z * sg;
+        acc.w = acc.w + ysh.w * sg;
     }
-    const float4 r = *reinterpret_cast<const float4 *>(a.res + (size_t)t * a.n_embd + d);
     *o = make_float4(acc.x + r.x, acc.y + r.y, acc.z + r.z, acc.w + r.w);
 }
 
