@@ -657,7 +657,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
             __syncthreads();
 #pragma unroll 1
             for (int c = 0; c < mc; ++c) {
-                const float v = lpb_row_q4k_mem<NB>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
+                const float v = lpb_row_q4k_mem<NB, true>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
                 if (t8 == NB - 1) gu[wave][grp][c0 + c] = v;
             }
         }
