@@ -425,9 +425,9 @@ def run_batched(args, shape, n_layer):
     sh_pairs = M * n_layer if shape.n_ff_shexp else 0  # the shared expert's group: all M tokens
     int8_ops = 2 * macs_per_pair * (int(hist.sum()) + sh_pairs)
     # verify-sized batches run groups of MFMA_MIN_TOKENS or more on MFMA; prefill-sized
-    # ones (more than 16 tokens) run every group on MFMA
-    mfma_groups = hist >= (MFMA_MIN_TOKENS if M <= 16 else 1)
-    sh_mfma = sh_pairs if (M > 16 or M >= MFMA_MIN_TOKENS) else 0
+    # ones (more than 32 tokens) run every group on MFMA
+    mfma_groups = hist >= (MFMA_MIN_TOKENS if M <= 32 else 1)
+    sh_mfma = sh_pairs if (M > 32 or M >= MFMA_MIN_TOKENS) else 0
     mfma_ops = 2 * macs_per_pair * (int(hist[mfma_groups].sum()) + sh_mfma)
     result = {
         "metric": f"batched MoE-layer us per step of {M} tokens + HBM GB/s, "
@@ -438,7 +438,7 @@ def run_batched(args, shape, n_layer):
         "data": "synthetic weights and N(0,1) hiddens, every token routed independently",
         "config": {"workload": f"{shape.name}: {n_layer} layers, {M} tokens per step, all experts resident",
                    "tokens_per_step": M, "layers": n_layer,
-                   "path": "verify-sized: expert groups of 16 token places" if M <= 16 else
+                   "path": "verify-sized: expert groups of 32 token places" if M <= 32 else
                            "prefill-sized: pairs sorted by expert, 64-pair units on MFMA"},
         "tokens_per_s": round(M * 1000.0 / ms, 2),
         "unique_experts_per_layer": round(float(uniq.mean()), 2),

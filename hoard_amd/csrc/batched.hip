@@ -7,7 +7,7 @@
 // followed by the weighted sum over the selected experts.
 //
 // The MFMA tiles and why they give the per-token path's bits are in mfma.h.
-// Batches of more than 16 tokens take the sorted-pair path of prefill.hip after
+// Batches of more than 32 tokens take the sorted-pair path of prefill.hip after
 // the routing and grouping here.
 #include "kernels.h"
 #include "lds_dma.h"
@@ -21,7 +21,8 @@ namespace hoard {
 namespace {
 
 constexpr int kTile = 16;                   // weight rows per MFMA tile
-constexpr int kMaxTok = kBatchedMaxTokens;  // token columns per MFMA tile
+constexpr int kMaxTok = kBatchedMaxTokens;  // token places per expert group
+constexpr int kCols = 16;                   // token columns per MFMA tile
 constexpr int kMfmaMinTokens = 12;          // smallest expert group computed on MFMA
 constexpr int kXChunk = 1;                  // tokens of Q8_K x staged in LDS at a time
 constexpr int kMaxExperts = 1024;
@@ -575,7 +576,8 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
 // Expert groups are computed two ways.  A group of fewer than kMfmaMinTokens
 // tokens runs token by token with the per-token row dot, whose cost grows with
 // the group; a larger group runs on MFMA, whose cost is that of 16 token
-// columns whatever the group's size.  Both give the per-token path's bits.
+// columns whatever the group's size (two passes over the LDS tile above 16
+// tokens).  Both give the per-token path's bits.
 // Weight tiles are contiguous rows of the expert and are copied into LDS in
 // one burst.
 
@@ -627,47 +629,57 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     if (!load_group(a, u, e, m)) return;
     __shared__ __align__(16) uint8_t wt[2][kTileBytes];
     __shared__ __align__(16) uint8_t xs[kXChunk * NB * sizeof(Q8L)];
-    __shared__ float gu[2][kRows][kMaxTok];
+    __shared__ float gu[2][kRows][kCols];  // gate and up values of 16 token columns
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kRows;
     const int *tok = a.utok + u * kMaxTok;
     const uint8_t *W = (wave ? batched_up(a, e) : batched_gate(a, e)) + (size_t)row0 * kRowBytes;
+    // h = silu(gate) * up of columns c0 .. c0 + 15 from gu (128 threads: 8 rows x 16 columns)
+    auto store_h = [&](int c0) {
+        __syncthreads();
+        const int r = threadIdx.x / kCols, cc = threadIdx.x % kCols;
+        if (c0 + cc < m) {
+            const float g = gu[0][r][cc], uu = gu[1][r][cc];
+            a.hbuf[((size_t)u * kMaxTok + c0 + cc) * a.n_ff + row0 + r] = g / (1.0f + expf(-g)) * uu;
+        }
+    };
     if (m >= kMfmaMinTokens) {
         dma_wave_copy_nt(wt[wave], W, kTileBytes);
-        const int c = lane & 15;
-        const Q8L *xq = q8(a.q8x) + (size_t)tok[c < m ? c : 0] * NB;
         lds_dma_wait();
-        float v[4];
-        tile_q4k<NB, 7>(wt[wave], kRowBytes, xq, v);
-        if (lane < 32) {
+        // 16 token columns at a time over the LDS tile
+        for (int c0 = 0; c0 < m; c0 += kCols) {
+            if (c0 > 0) __syncthreads();  // the previous columns' h is formed
+            const int c = c0 + (lane & 15);
+            const Q8L *xq = q8(a.q8x) + (size_t)tok[c < m ? c : 0] * NB;
+            float v[4];
+            tile_q4k<NB, 7>(wt[wave], kRowBytes, xq, v);
+            if (lane < 32) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) gu[wave][4 * (lane >> 4) + i][c] = v[i];
-        }
-    } else {
-        // x goes into LDS with the tile, kXChunk tokens at a time: a vector
-        // load issued during the compute would queue behind the tile copies
-        // of the other workgroups on this CU
-        const Q8L *xl = reinterpret_cast<const Q8L *>(xs);
-        for (int c0 = 0; c0 < m; c0 += kXChunk) {
-            const int mc = min(m - c0, kXChunk);
-            if (c0 > 0) __syncthreads();  // both waves are done with the previous chunk
-            gather_tokens<NB>(xs, a.q8x, tok, c0, mc, m, wave, 2);
-            if (c0 == 0) dma_wave_copy_nt(wt[wave], W, kTileBytes);
-            lds_dma_wait();
-            __syncthreads();
-#pragma unroll 1
-            for (int c = 0; c < mc; ++c) {
-                const float v = lpb_row_q4k_mem<NB, true>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
-                if (t8 == NB - 1) gu[wave][grp][c0 + c] = v;
+                for (int i = 0; i < 4; ++i) gu[wave][4 * (lane >> 4) + i][lane & 15] = v[i];
             }
+            store_h(c0);
+        }
+        return;
+    }
+    // fewer than kMfmaMinTokens <= 16 tokens: x goes into LDS with the tile,
+    // kXChunk tokens at a time (a vector load issued during the compute would
+    // queue behind the tile copies of the other workgroups on this CU)
+    static_assert(kMfmaMinTokens <= kCols, "a per-token group fits the 16 columns of gu");
+    const Q8L *xl = reinterpret_cast<const Q8L *>(xs);
+    for (int c0 = 0; c0 < m; c0 += kXChunk) {
+        const int mc = min(m - c0, kXChunk);
+        if (c0 > 0) __syncthreads();  // both waves are done with the previous chunk
+        gather_tokens<NB>(xs, a.q8x, tok, c0, mc, m, wave, 2);
+        if (c0 == 0) dma_wave_copy_nt(wt[wave], W, kTileBytes);
+        lds_dma_wait();
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < mc; ++c) {
+            const float v = lpb_row_q4k_mem<NB, true>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
+            if (t8 == NB - 1) gu[wave][grp][c0 + c] = v;
         }
     }
-    __syncthreads();
-    const int r = threadIdx.x / kMaxTok, cc = threadIdx.x % kMaxTok;  // 128 threads: 8 rows x 16 columns
-    if (cc < m) {
-        const float g = gu[0][r][cc], uu = gu[1][r][cc];
-        a.hbuf[((size_t)u * kMaxTok + cc) * a.n_ff + row0 + r] = g / (1.0f + expf(-g)) * uu;
-    }
+    store_h(0);
 }
 
 // -- Q8_K of h per (expert, token) ---------------------------------------------
@@ -708,18 +720,21 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
     const int kk = a.k + a.sh;  // output slots per token
     if (m >= kMfmaMinTokens) {
         dma_wave_copy_nt(tile, src, kTileBytes);
-        const int c = lane & 15;
-        const Q8L *xq = q8(a.q8h) + ((size_t)u * kMaxTok + (c < m ? c : 0)) * NBH;
         lds_dma_wait();
-        float v[4];
-        if constexpr (TD == kTypeQ4K)
-            tile_q4k<NBH>(tile, kRowBytes, xq, v);
-        else
-            tile_q6k<NBH>(tile, kRowBytes, xq, v);
-        if (c < m) {
-            float *y = a.ybuf + ((size_t)tok[c] * kk + slot[c]) * a.n_embd + row0;
+        // 16 token columns at a time over the LDS tile
+        for (int c0 = 0; c0 < m; c0 += kCols) {
+            const int c = c0 + (lane & 15);
+            const Q8L *xq = q8(a.q8h) + ((size_t)u * kMaxTok + (c < m ? c : 0)) * NBH;
+            float v[4];
+            if constexpr (TD == kTypeQ4K)
+                tile_q4k<NBH>(tile, kRowBytes, xq, v);
+            else
+                tile_q6k<NBH>(tile, kRowBytes, xq, v);
+            if (c < m) {
+                float *y = a.ybuf + ((size_t)tok[c] * kk + slot[c]) * a.n_embd + row0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) y[4 * (lane >> 4) + i] = v[i];
+                for (int i = 0; i < 4; ++i) y[4 * (lane >> 4) + i] = v[i];
+            }
         }
         return;
     }
@@ -800,7 +815,8 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
     const int nbh = a.n_ff / QK;
     const int umax = (a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k) + a.sh;
     hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
-    hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, kMaxTok, umax), dim3(64), 0, s, a);
+    // a group holds at most M (<= kMaxTok) tokens
+    hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, a.M, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
 #define HOARD_DOWN(T, N)                                                  \
     if (a.d_type == T && nbh == N) {                                      \
@@ -822,7 +838,7 @@ bool args_ok(const BatchedArgs &a) {
 
 }  // namespace
 
-// Batches of up to 16 tokens group by expert with 16 token places per group;
+// Batches of up to 32 tokens group by expert with 32 token places per group;
 // larger ones sort the pairs and run the prefill units (prefill.hip).
 hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)

@@ -63,7 +63,7 @@ struct DownArgs {
 };
 hipError_t launch_down_combine(const DownArgs &a, hipStream_t s);
 
-// Batched expert stage for M <= 16 tokens: grouping by expert, int8-MFMA
+// Batched expert stage for M tokens: grouping by expert, int8-MFMA
 // gate/up (+SwiGLU) and down tiles, ordered combine.
 struct BatchedArgs {
     int M, n_embd, n_ff, E, k;
@@ -80,13 +80,13 @@ struct BatchedArgs {
     const uint8_t *gate, *up, *down;
     size_t gstride, ustride, dstride;
     uint8_t *q8x;           // Q8_K(fx): [M][n_embd/256] blocks of 304 bytes
-    uint8_t *q8h;           // Q8_K(h):  [umax][16][n_ff/256] blocks
-    float *hbuf;            // [umax][16][n_ff]
+    uint8_t *q8h;           // Q8_K(h):  [umax][kBatchedMaxTokens][n_ff/256] blocks
+    float *hbuf;            // [umax][kBatchedMaxTokens][n_ff]
     float *ybuf;            // [M][k + sh][n_embd]: slot k holds the shared expert's output
     int *n_unique;          // [1]
     int *slot_of;           // [E] scratch
     int *uexp, *ucount;     // [umax] expert of each group, tokens in it
-    int *utok, *uslot;      // [umax][16] token and slot of each member
+    int *utok, *uslot;      // [umax][kBatchedMaxTokens] token and slot of each member
     unsigned *hist;         // [n_ids] tokens per expert (or slot) in the call
     int n_ids;              // id space the groups are formed over: E, or the slots of a pool
     int *ysrc;              // [M][k] caller ids only: the slot j' <= j whose output pair (t, j) takes
@@ -118,7 +118,7 @@ __device__ __forceinline__ const uint8_t *batched_up(const BatchedArgs &a, int e
 __device__ __forceinline__ const uint8_t *batched_down(const BatchedArgs &a, int e) {
     return a.sh && e == a.n_ids ? a.sh_down : a.down + (size_t)e * a.dstride;
 }
-constexpr int kBatchedMaxTokens = 16;         // the verify-sized path: per-token dots or MFMA per group
+constexpr int kBatchedMaxTokens = 32;         // the verify-sized path: per-token dots or MFMA per group
 constexpr int kBatchedMaxTokensLarge = 512;   // the prefill-sized path: sorted pairs, MFMA units
 constexpr int kUnitTokens = 64;               // pairs of one expert per prefill work unit
 constexpr int kBatchedCounters = 160;         // route completion counters: one per 4 tokens, and the tails'

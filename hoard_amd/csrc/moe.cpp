@@ -1140,7 +1140,7 @@ namespace {
 
 // Scratch of the batched entry points for batches of up to T tokens: the
 // byte size of every buffer and the layout of the int arrays.  The verify-sized
-// path (M <= 16) keeps 16 token places per expert group; the prefill-sized one
+// path (M <= 32) keeps 32 token places per expert group; the prefill-sized one
 // keeps the pairs sorted by expert.
 struct BatchedLayout {
     int T, Ts, umax, umax_s, max_units;

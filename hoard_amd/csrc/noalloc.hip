@@ -14,7 +14,7 @@
 
 namespace hoard {
 
-constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr size_t kScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {

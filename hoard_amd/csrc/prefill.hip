@@ -1,4 +1,4 @@
-// Expert products of a prefill-sized batch (more than 16 tokens): the
+// Expert products of a prefill-sized batch (more than 32 tokens): the
 // counterpart of ggml_mul_mat_id over all T prompt tokens
 // (src/run_m1.cpp:93-108) and of the verify step's mul_mat_id with per-token
 // ids (src/run_specloop.cpp:126-139), followed by the weighted sum over the

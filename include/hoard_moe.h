@@ -136,7 +136,7 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
    experts with per-token ids and the weighted sum over them
    (src/run_specloop.cpp:126-139, src/run_m1.cpp:97-108).  The (token, slot)
    pairs are grouped by expert so each selected expert's weights are read once
-   per call (per 64 pairs above 16 tokens, where the pairs are sorted by
+   per call (per 64 pairs above 32 tokens, where the pairs are sorted by
    expert into 64-pair units), and the expert products run on per-token int8
    dots or int8 MFMA; each token's result is the single-token
    hoard_moe_layer's bit for bit.  M > 512 returns HOARD_ERR_INVALID.  fx_dev, res_dev, out_dev:
@@ -153,10 +153,10 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
    that cannot allocate device memory (code under HIP graph capture, tight
    serving loops, harnesses that forbid hipMalloc).  No counterpart in the
    reference.  The per-call scratch lives in one fixed device array per GPU,
-   16 MiB, looked up when a handle is created and held until the process ends;
+   32 MiB, looked up when a handle is created and held until the process ends;
    1 <= M <= min(max_tokens, 16), and a shape whose scratch for M tokens exceeds
    the array is refused with HOARD_ERR_INVALID (the Qwen3-30B shape needs about
-   9 MiB at M = 16).  Results are hoard_moe_forward_batched's bit for bit.  Every
+   17 MiB at M = 16, the Qwen3-Next shape about 16.5 MiB).  Results are hoard_moe_forward_batched's bit for bit.  Every
    call on a GPU shares that GPU's array: calls that overlap on one GPU (any
    handle, any stream) race. */
 int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,

@@ -1,4 +1,5 @@
-"""Prefill-sized batches (17..512 tokens): the sorted-pair expert GEMM on int8 MFMA.
+"""Batches of 17..512 tokens: up to 32 the verify-sized path's expert groups (per-token
+dots, or int8 MFMA in 16-column passes), above 32 the sorted-pair expert GEMM on int8 MFMA.
 
 The counterpart of ggml_mul_mat_id over all T prompt tokens (src/run_m1.cpp:93-108).
 Each token's result must be the single-token path's bit for bit (the folded MFMA
@@ -50,7 +51,7 @@ def _check(orc, st, shape, hl, fx, res, out, sel, w, what, every=1):
     return worst
 
 
-@pytest.mark.parametrize("M", [17, 32, 128, 512])
+@pytest.mark.parametrize("M", [17, 32, 33, 128, 512])
 def test_prefill_matches_single_token_and_oracle(orc, stage, M):
     shape, hl, st = stage
     fx, res = _tokens(shape, M, 1000 + M)
@@ -65,10 +66,12 @@ def test_prefill_matches_single_token_and_oracle(orc, stage, M):
     assert stats.last_unique == int((counts > 0).sum())
 
 
-@pytest.mark.parametrize("M,same", [(200, 1), (300, 3)], ids=["200x1", "300x3"])
+@pytest.mark.parametrize("M,same", [(20, 1), (30, 2), (32, 1), (200, 1), (300, 3)],
+                         ids=["20x1", "30x2", "32x1", "200x1", "300x3"])
 def test_prefill_large_expert_groups(orc, stage, M, same):
-    """Tokens sharing a few hiddens: groups of 100-300 tokens, cut into several
-    64-pair units each."""
+    """Tokens sharing a few hiddens.  Up to 32 tokens the groups (15, 20 or 32
+    tokens) run on MFMA in one or two 16-column passes over each weight tile;
+    above, groups of 100-300 tokens are cut into several 64-pair units each."""
     shape, hl, st = stage
     fx, res = _tokens(shape, M, 3000 + M, same=same)
     print(f"prefill {shape.name} M={M}, {same} distinct hiddens", flush=True)

@@ -33,15 +33,16 @@ def _noalloc(st, layer, fx, res):
     return rc, (fx_d, res_d, out, sel, w)
 
 
-def test_noalloc_matches_forward_batched(orc):
+@pytest.mark.parametrize("shape", [W.QWEN3_30B, W.QWEN3_NEXT], ids=lambda s: s.name)
+def test_noalloc_matches_forward_batched(orc, shape):
+    """Qwen3-Next adds the shared expert's group and output slot to the layout."""
     from hoard_amd.runtime import MoEStage
-    shape = W.QWEN3_30B
     layers = {l: W.make_layer(shape, 13, l) for l in range(2)}
     st = MoEStage(shape, n_layer=2, layers=layers, max_tokens=16)
     try:
         calls = [(0, _tokens(shape, 16, 0)), (1, _tokens(shape, 5, 100))]
         refs = [st.forward_batched(l, fx, res) for l, (fx, res) in calls]
-        print("no-alloc: two calls in a row, M = 16 then M = 5", flush=True)
+        print(f"no-alloc {shape.name}: two calls in a row, M = 16 then M = 5", flush=True)
         got = []
         for l, (fx, res) in calls:
             rc, bufs = _noalloc(st, l, fx, res)
