@@ -307,21 +307,24 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 // Logits of 16 experts x 16 tokens per workgroup of 256 threads.  Thread
 // (group q = tid / 32, lane l = tid % 32) holds accumulator l of ggml's x86 f32
 // dot (elements 32 i + l, i ascending) for 4 experts x 8 tokens: the rows and
-// tokens pass through LDS 256 elements at a time, every element read once per
+// tokens pass through LDS 512 elements at a time, every element read once per
 // 32 dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
 // which fold them in ggml's order, so every logit is the single-token router's.
-constexpr int kTileE = 16, kTileT = 16, kTileK = 256;
+// Each K step costs a wait and a barrier besides its dots: 512-element steps
+// (4 of them) took 3.5 us less per launch than 256-element ones (8), and
+// 1024-element ones without a second buffer 1.6 us more than 512 at M = 512.
+constexpr int kTileE = 16, kTileT = 16, kTileK = 512;
 
-// K steps in LDS: the current one and the next in flight (four, three in
-// flight, measured the same: with one wave per SIMD the dots' own chains, not
-// the copies, set the pace once one step is prefetched)
+// K steps in LDS: the current one and the next in flight (four buffers, three
+// steps in flight, measured the same: once one step is prefetched the dots and
+// the per-step barrier set the pace).  128 KB of LDS: one workgroup per CU.
 constexpr int kGemmBufs = 2;
 __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
     __shared__ __align__(16) float wl[kGemmBufs][kTileE][kTileK];
     __shared__ __align__(16) float xl[kGemmBufs][kTileT][kTileK];
     constexpr int n = kRouteN, kSteps = n / kTileK;
     static_assert(kSteps >= kGemmBufs, "the ring is filled before the first step");
-    constexpr int kRowsPerWave = (kTileE + kTileT) / 4;  // copies each wave issues per step
+    constexpr int kRowsPerWave = (kTileE + kTileT) / 4 * (kTileK / 256);  // 1 KB copies each wave issues per step
     const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = tid >> 6, lane = tid & 63;
     const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
     const int re = (q & 3) * 4, rt = (q >> 2) * 8;  // this group's 4 experts and 8 tokens within the tile
@@ -341,7 +344,9 @@ __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
             const float *src = r < kTileE ? (row < a.E ? a.router + (size_t)row * n : a.sh_gate_inp)
                                           : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
             float *dst = r < kTileE ? wl[buf][r] : xl[buf][r - kTileE];
-            dma_chunk(reinterpret_cast<uint8_t *>(dst), reinterpret_cast<const uint8_t *>(src + k0));
+#pragma unroll
+            for (int ck = 0; ck < kTileK / 256; ++ck)
+                dma_chunk(reinterpret_cast<uint8_t *>(dst + 256 * ck), reinterpret_cast<const uint8_t *>(src + k0 + 256 * ck));
         }
     };
 #pragma unroll
