@@ -32,15 +32,17 @@ __device__ __forceinline__ Q8L *q8(uint8_t *p) { return reinterpret_cast<Q8L *>(
 
 // -- route: router logits, softmax / top-k, Q8_K of fx, grouping by expert ----
 // One launch replaces the router kernels and the grouping pass.  A workgroup
-// (4 waves) takes kRouteRows router rows against kRouteTok tokens, a wave per
-// token and a half-wave per row at a time, with the single-token router's
-// per-row accumulation order (lane l of 32 owns elements l, l+32, ...; ggml's
-// f32 dot fold).  Two rows per workgroup measured best at 4 and 16 tokens
-// (four: -0.5 us at 16 tokens, +1.2 us at 4; eight: slower at both).  The last
+// (4 waves) takes R router rows against kRouteTok tokens, a wave per token and
+// a half-wave per row at a time, with the single-token router's per-row
+// accumulation order (lane l of 32 owns elements l, l+32, ...; ggml's f32 dot
+// fold).  Up to 8 tokens two rows per workgroup, above that four (fewer
+// copies of the tokens' fx): measured per layer, four rows against two took
+// 0.5 us off at 16 tokens and 2.8 at 32 (Qwen3-30B shape), 3.3 and 7.5 with
+// 512 experts (Qwen3-Next), and added 1.2 us at 4 tokens; eight rows were
+// slower than four everywhere.  The last
 // workgroup of a token group (device-scope counter) runs the tails of its
 // tokens; the last token group's tail workgroup then groups the (token, slot)
 // pairs by expert.  Waves with a spare slot quantise fx to Q8_K.
-constexpr int kRouteRows = 2;
 constexpr int kRouteTok = 4;
 constexpr int kRouteN = 2048;  // n_embd of the batched path
 
@@ -219,6 +221,7 @@ __device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
     }
 }
 
+template <int R>
 __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     constexpr int n = kRouteN, nb = kRouteN / QK;
     const int E = a.E;
@@ -226,13 +229,13 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     const int tg = blockIdx.y;
     const int t = tg * kRouteTok + wave;  // this wave's token; its half-waves take one row each
     // rows 0..E-1 are the router's; row E (with a shared expert) is its gate row
-    const int r0 = blockIdx.x * kRouteRows;
-    const int nrows = min(kRouteRows, E + a.sh - r0);
+    const int r0 = blockIdx.x * R;
+    const int nrows = min(R, E + a.sh - r0);
     // the workgroup's token rows and router rows go to LDS in one burst, so
     // that every load is in flight at once; the dot then reads them in the
     // per-lane order the accumulation needs
     __shared__ __align__(16) float xl[kRouteTok][kRouteN];
-    __shared__ __align__(16) float wl[kRouteRows][kRouteN];
+    __shared__ __align__(16) float wl[R][kRouteN];
     if (t < a.M) dma_wave_copy(reinterpret_cast<uint8_t *>(xl[wave]), reinterpret_cast<const uint8_t *>(a.fx + (size_t)t * n),
                                n * (int)sizeof(float));
     {
@@ -250,7 +253,7 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
         const float *x = xl[wave];
         // half-wave h takes rows rp + h, rp = 0, 2, ...
 #pragma unroll 1
-        for (int rp = 0; rp < kRouteRows; rp += 2) {
+        for (int rp = 0; rp < R; rp += 2) {
             const int row = r0 + rp + (lane >> 5);
             const float *wr = wl[min(rp + (lane >> 5), nrows - 1)];
             float acc = 0.0f;
@@ -855,8 +858,11 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
     }
-    hipLaunchKernelGGL(route_kernel, dim3((a.E + a.sh + kRouteRows - 1) / kRouteRows, (a.M + kRouteTok - 1) / kRouteTok),
-                       dim3(256), 0, s, a);
+    const int nr = a.E + a.sh, ntg = (a.M + kRouteTok - 1) / kRouteTok;
+    if (a.M > 8)
+        hipLaunchKernelGGL(route_kernel<4>, dim3((nr + 3) / 4, ntg), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(route_kernel<2>, dim3((nr + 1) / 2, ntg), dim3(256), 0, s, a);
     return launch_groups(a, s);
 }
 
