@@ -713,20 +713,15 @@ __global__ __launch_bounds__(64) void quant_h_kernel(BatchedArgs a) {
 // the per-token Q6_K dot wants one alignment per wave, so each pass takes the
 // rows of one parity (the row size is 2 mod 4).
 template <int TD, int NBH>
-__global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
-    constexpr int kRowBytes = NBH * (TD == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
+__device__ __forceinline__ void down_group(const BatchedArgs &a, int u, int e, int m, uint8_t *tile, uint8_t *xs) {
+    constexpr int kRowBytes = NBH * QType<TD>::bytes;
     constexpr int kTileBytes = kTile * kRowBytes;
-    const int u = blockIdx.y;
-    int e, m;
-    if (!load_group(a, u, e, m)) return;
-    __shared__ __align__(16) uint8_t tile[kTileBytes];
-    __shared__ __align__(16) uint8_t xs[kXChunk * NBH * sizeof(Q8L)];
     const int lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kTile;
     const int *tok = a.utok + u * kMaxTok, *slot = a.uslot + u * kMaxTok;
     const uint8_t *src = batched_down(a, e) + (size_t)row0 * kRowBytes;
     const int kk = a.k + a.sh;  // output slots per token
-    if (m >= kMfmaMinTokens) {
+    if (TD != kTypeQ5K && m >= kMfmaMinTokens) {  // Q5_K groups of any size run token by token
         dma_wave_copy_nt(tile, src, kTileBytes);
         lds_dma_wait();
         // 16 token columns at a time over the LDS tile
@@ -736,7 +731,7 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
             float v[4];
             if constexpr (TD == kTypeQ4K)
                 tile_q4k<NBH>(tile, kRowBytes, xq, v);
-            else
+            else if constexpr (TD == kTypeQ6K)
                 tile_q6k<NBH>(tile, kRowBytes, xq, v);
             if (c < m) {
                 float *y = a.ybuf + ((size_t)tok[c] * kk + slot[c]) * a.n_embd + row0;
@@ -763,6 +758,13 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
                     const float v = g8_row_q6k_u<NBH>(tile + row * kRowBytes, xl + c * NBH, t8);
                     if (t8 == 0) y[row] = v;
                 }
+            } else if constexpr (TD == kTypeQ5K) {
+#pragma unroll 1
+                for (int p = 0; p < 2; ++p) {  // the single-token down kernel's Q5_K row dot
+                    const int row = 8 * p + grp;
+                    const float v = g8_row_q5k(tile + row * kRowBytes, xl + c * NBH, NBH, t8);
+                    if (t8 == 0) y[row] = v;
+                }
             } else {
 #pragma unroll 1
                 for (int p = 0; p < 2; ++p) {
@@ -774,6 +776,22 @@ __global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's LDS reads precede the next copy
     }
+}
+
+// TD: the routed experts' down type; TS: the shared expert's (Q6_K beside
+// Q5_K routed rows, as Qwen3.5 has them), run by the same launch.
+template <int TD, int NBH, int TS = TD>
+__global__ __launch_bounds__(64, 4) void down_kernel(BatchedArgs a) {
+    constexpr int kTileBytes = kTile * NBH * (QType<TD>::bytes > QType<TS>::bytes ? QType<TD>::bytes : QType<TS>::bytes);
+    const int u = blockIdx.y;
+    int e, m;
+    if (!load_group(a, u, e, m)) return;
+    __shared__ __align__(16) uint8_t tile[kTileBytes];
+    __shared__ __align__(16) uint8_t xs[kXChunk * NBH * sizeof(Q8L)];
+    if (TS != TD && a.sh && e == a.n_ids)
+        down_group<TS, NBH>(a, u, e, m, tile, xs);
+    else
+        down_group<TD, NBH>(a, u, e, m, tile, xs);
 }
 
 // -- combine: out[t][d] = (sum_j w[t][j] * y[t][j][d]) + res[t][d], j ascending --
@@ -813,7 +831,7 @@ __global__ __launch_bounds__(256) void combine_kernel(BatchedArgs a) {
 
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff) {
     return gu_type == kTypeQ4K && n_embd == 2048 && (n_ff == 768 || n_ff == 1024 || n_ff == 512) &&
-           (d_type == kTypeQ4K || d_type == kTypeQ6K);
+           (d_type == kTypeQ4K || d_type == kTypeQ6K || (d_type == kTypeQ5K && n_ff != 768));
 }
 
 namespace {
@@ -826,12 +844,16 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
     // a group holds at most M (<= kMaxTok) tokens
     hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, a.M, umax), dim3(64), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
-#define HOARD_DOWN(T, N)                                                  \
-    if (a.d_type == T && nbh == N) {                                      \
-        hipLaunchKernelGGL((down_kernel<T, N>), dg, dim3(64), 0, s, a);    \
+#define HOARD_DOWN(T, N, TS)                                                    \
+    if (a.d_type == T && nbh == N && sd == TS) {                                \
+        hipLaunchKernelGGL((down_kernel<T, N, TS>), dg, dim3(64), 0, s, a);     \
     } else
-    HOARD_DOWN(kTypeQ6K, 3) HOARD_DOWN(kTypeQ6K, 2) HOARD_DOWN(kTypeQ6K, 4) HOARD_DOWN(kTypeQ4K, 4)
-    HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
+    const int sd = a.sh ? a.sh_d_type : a.d_type;
+    HOARD_DOWN(kTypeQ6K, 3, kTypeQ6K) HOARD_DOWN(kTypeQ6K, 2, kTypeQ6K) HOARD_DOWN(kTypeQ6K, 4, kTypeQ6K)
+    HOARD_DOWN(kTypeQ4K, 4, kTypeQ4K) HOARD_DOWN(kTypeQ4K, 3, kTypeQ4K) HOARD_DOWN(kTypeQ4K, 2, kTypeQ4K)
+    HOARD_DOWN(kTypeQ5K, 2, kTypeQ5K) HOARD_DOWN(kTypeQ5K, 4, kTypeQ5K) HOARD_DOWN(kTypeQ5K, 2, kTypeQ6K) {
+        return hipErrorInvalidValue;
+    }
 #undef HOARD_DOWN
     hipLaunchKernelGGL(combine_kernel, dim3((a.n_embd + 255) / 256, a.M), dim3(256), 0, s, a);
     return hipGetLastError();

@@ -104,6 +104,7 @@ struct BatchedArgs {
     // expert id n_ids, whose weights are these tensors (n_ff rows, the routed
     // experts' types), and out = (sum_j w_j y_j + sigmoid(sgl[t]) * y_k) + res.
     int sh;                       // 1 with a shared expert, else 0
+    int sh_d_type;                // its down type: d_type, or Q6_K beside Q5_K routed rows
     const uint8_t *sh_gate, *sh_up, *sh_down;
     const float *sh_gate_inp;     // [n_embd] f32 gate row of the shared expert
     float *sgl;                   // [M] sh_gate_inp . fx[t] (the logit, before the sigmoid)

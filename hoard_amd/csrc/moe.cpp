@@ -1234,8 +1234,11 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     const bool sh = c.n_ff_shexp > 0;
     if (sh) {
         // the shared expert runs as one more expert of the routed experts' kernels
+        // (a Q6_K shared down beside Q5_K routed rows, Qwen3.5's types, runs in the
+        // same down launch)
+        const bool q5q6 = L.down_type == HOARD_TYPE_Q5_K && L.sh_down_type == HOARD_TYPE_Q6_K;
         if (c.n_ff_shexp != c.n_ff || L.sh_gate_type != L.gate_type || L.sh_up_type != L.up_type ||
-            L.sh_down_type != L.down_type)
+            (L.sh_down_type != L.down_type && !(q5q6 && c.n_ff == 512)))
             return fail(HOARD_ERR_UNSUPPORTED,
                         "batched path: the shared expert (n_ff %d, types %d/%d/%d) must match the routed experts'",
                         c.n_ff_shexp, L.sh_gate_type, L.sh_up_type, L.sh_down_type);
@@ -1247,6 +1250,10 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
+    // the prefill units (above kBatchedMaxTokens tokens) have Q4_K and Q6_K down tiles only
+    if (M > hoard::kBatchedMaxTokens && (L.down_type == HOARD_TYPE_Q5_K || (c.n_ff_shexp > 0 && L.sh_down_type != L.down_type)))
+        return fail(HOARD_ERR_UNSUPPORTED, "batched path: Q5_K down rows take at most %d tokens per call",
+                    hoard::kBatchedMaxTokens);
     if ((((uintptr_t)fx_dev | (uintptr_t)res_dev | (uintptr_t)out_dev) & 15) != 0)
         return fail(HOARD_ERR_INVALID, "fx, res and out must be 16-byte aligned");
     // the weight tiles are copied to LDS in 16-byte units
@@ -1275,6 +1282,7 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     a.ustride = L.ustride;
     a.dstride = L.dstride;
     a.sh = sh ? 1 : 0;
+    a.sh_d_type = sh ? L.sh_down_type : L.down_type;
     a.sh_gate = L.sh_gate;
     a.sh_up = L.sh_up;
     a.sh_down = L.sh_down;
