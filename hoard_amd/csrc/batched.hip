@@ -691,14 +691,15 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
 }
 
 // -- Q8_K of h per (expert, token) ---------------------------------------------
-__global__ __launch_bounds__(64) void quant_h_kernel(BatchedArgs a) {
-    const int u = blockIdx.z, c = blockIdx.y, b = blockIdx.x;
+// One workgroup per (group, token), a wave per 256-element block of h.
+__global__ __launch_bounds__(256) void quant_h_kernel(BatchedArgs a) {
+    const int u = blockIdx.y, c = blockIdx.x, b = threadIdx.x >> 6;
     const int nbh = a.n_ff / QK;
     const size_t uc = (size_t)u * kMaxTok + c;
     // h is loaded with the group count and size, not after them (its place
     // does not depend on them; a place past the groups is in the buffer and
     // its values are dropped), all three as vector loads in flight together
-    // (u < the grid's umax keeps them in bounds)
+    // (u < the grid's umax and b < nbh keep them in bounds)
     const int nu = __hip_atomic_load(a.n_unique, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + a.sh;
     const int cnt = __hip_atomic_load(a.ucount + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float4 v4 = *reinterpret_cast<const float4 *>(a.hbuf + uc * a.n_ff + (size_t)b * QK + 4 * (threadIdx.x & 63));
@@ -842,7 +843,7 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
     const int umax = (a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k) + a.sh;
     hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     // a group holds at most M (<= kMaxTok) tokens
-    hipLaunchKernelGGL(quant_h_kernel, dim3(nbh, a.M, umax), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(quant_h_kernel, dim3(a.M, umax), dim3(64 * nbh), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
 #define HOARD_DOWN(T, N, TS)                                                    \
     if (a.d_type == T && nbh == N && sd == TS) {                                \
