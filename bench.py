@@ -85,6 +85,9 @@ def parse():
     ap.add_argument("--batch-same", action="store_true",
                     help="with --batch: the M tokens of a step share one hidden, so every expert group holds "
                          "M tokens and runs on MFMA (the skewed end of the verify workload)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="headline run only: skip the other workloads carried on its line (Qwen3-Next decode, "
+                         "16-token verify batch, 512-token prefill)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -356,32 +359,47 @@ MFMA_MIN_TOKENS = 12  # smallest expert group the batched kernels run on MFMA (k
 MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA ops/s
 
 
-def run_batched(args, shape, n_layer):
-    """Batched workload: one step = M tokens through every layer, each layer one
-    hoard_moe_forward_batched (router for M tokens, grouping by expert, gate/up
-    and down per expert group, ordered combine).  Each token keeps its own
-    normalised hidden as the layer input (fx); the residual chain is in place."""
-    import torch
-
+def load_layers(lib, h, shape, n_layer, seed):
+    """Every layer's synthetic weights into the handle (one host layer regenerated in place)."""
     import hoard_amd as H
     from hoard_amd import workloads as W
+    hl = W.make_layer(shape, seed, 0)
+    for l in range(n_layer):
+        if l:
+            W.fill_layer(hl, seed, l)
+        H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(hl.weights())))
+    del hl
+
+
+def run_batched(args, shape, n_layer):
+    """Batched workload on a handle of its own (see batched_measure)."""
+    import hoard_amd as H
     lib = H.load_library()
     M = args.batch
     cfg = shape.cfg(n_layer, 0, M)
     h = ctypes.c_void_p()
     H.check(lib.hoard_moe_create(ctypes.byref(cfg), ctypes.byref(h)))
-    hl = W.make_layer(shape, args.seed, 0)
-    for l in range(n_layer):
-        if l:
-            W.fill_layer(hl, args.seed, l)
-        H.check(lib.hoard_moe_set_layer_weights(h, l, ctypes.byref(hl.weights())))
-    del hl
+    load_layers(lib, h, shape, n_layer, args.seed)
+    result = batched_measure(lib, h, shape, n_layer, M, args.steps, args.warmup, args.seed, args.batch_same)
+    lib.hoard_moe_destroy(h)
+    print(json.dumps(result), flush=True)
+
+
+def batched_measure(lib, h, shape, n_layer, M, steps, warm, seed, same=False):
+    """Batched workload: one step = M tokens through every layer, each layer one
+    hoard_moe_forward_batched (router for M tokens, grouping by expert, gate/up
+    and down per expert group, ordered combine).  Each token keeps its own
+    normalised hidden as the layer input (fx); the residual chain is in place.
+    The handle holds n_layer layers of `shape` and takes M tokens."""
+    import torch
+
+    import hoard_amd as H
+    from hoard_amd import workloads as W
     dev = torch.device("cuda:0")
-    steps, warm = args.steps, args.warmup
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     n_groups = 8
-    toks = [[W.make_hidden(shape, args.seed, 0, g * M + (0 if args.batch_same else t)) for t in range(M)]
+    toks = [[W.make_hidden(shape, seed, 0, g * M + (0 if same else t)) for t in range(M)]
             for g in range(n_groups)]
     fx_d = torch.stack([torch.stack([torch.from_numpy(f) for f, _ in grp]) for grp in toks]).to(dev)
     x_d = torch.stack([torch.stack([torch.from_numpy(r) for _, r in grp]) for grp in toks]).to(dev)
@@ -413,7 +431,7 @@ def run_batched(args, shape, n_layer):
     step(warm + steps)
     kt = H.KernelTimes()
     H.check(lib.hoard_moe_profile_read(h, ctypes.byref(kt)))
-    lib.hoard_moe_destroy(h)
+    H.check(lib.hoard_moe_profile(h, 0))
     # a shared expert (and its gate row) is read once per layer and taken by every token
     eb, sb = shape.expert_bytes(), shape.shared_bytes() + (4 * shape.n_embd if shape.n_ff_shexp else 0)
     layer_bytes = float(uniq.mean()) * eb + sb + 4 * shape.n_expert * shape.n_embd + M * 4 * shape.n_embd * 2
@@ -460,10 +478,73 @@ def run_batched(args, shape, n_layer):
                  "mfma_tops": round(mfma_ops / (ms * 1e-3) / 1e12, 2),
                  "utilization": round(mfma_ops / (ms * 1e-3) / MFMA_INT8_PEAK, 5), "peak_tops": MFMA_INT8_PEAK / 1e12},
     }
-    if args.batch_same:
+    if same:
         result["data"] = "synthetic weights; the M tokens of a step share one N(0,1) hidden (every group M tokens)"
         result["config"]["workload"] += ", tokens sharing one hidden"
-    print(json.dumps(result), flush=True)
+    return result
+
+
+
+
+def decode_measure(lib, h, shape, n_layer, steps, warm, seed):
+    """One-launch decode of one token through n_layer layers (plain launch),
+    timed as the headline: an event pair around `steps` steps, and an event pair
+    around each launch for the kernel's own duration."""
+    import torch
+
+    import hoard_amd as H
+    from hoard_amd import workloads as W
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    eps = ctypes.c_float(W.RMS_EPS)
+    H.check(lib.hoard_moe_set_option(h, H.OPT_DECODE_LAUNCH, 1))
+    xs = torch.stack([torch.from_numpy(W.make_hidden(shape, seed, 0, t)[1]) for t in range(steps + warm)]).to(dev)
+
+    def step(i):
+        H.check(lib.hoard_moe_decode(h, 0, n_layer, ctypes.c_void_p(xs[i].data_ptr()), eps, sp))
+
+    for i in range(warm):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(warm, warm + steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    assert torch.isfinite(xs).all().item(), f"non-finite {shape.name} decode output"
+    H.check(lib.hoard_moe_profile(h, 1))
+    for i in range(warm, warm + steps):
+        step(i)
+    kt = H.KernelTimes()
+    H.check(lib.hoard_moe_profile_read(h, ctypes.byref(kt)))
+    H.check(lib.hoard_moe_profile(h, 0))
+    kd = H.KERNEL_DECODE
+    us = ms * 1000.0 / n_layer
+    lb = shape.bytes_per_token_layer()
+    out = {"us_per_layer": round(us, 3), "tokens_per_s": round(1000.0 / ms, 2), "layer_bytes": lb,
+           "layer_hbm_gbps": round(lb / (us * 1e3), 1), "layer_hbm_frac": round(lb / (us * 1e3) / HBM_PEAK_GBPS, 4)}
+    if kt.launches[kd]:
+        kus = kt.total_ms[kd] / kt.launches[kd] * 1000.0
+        out["kernel"] = {"name": "decode_persistent", "avg_us_per_launch": round(kus, 3),
+                         "us_per_layer": round(kus / n_layer, 3),
+                         "gbps": round(n_layer * lb / kus / 1e3, 1),
+                         "frac": round(n_layer * lb / kus / 1e3 / HBM_PEAK_GBPS, 4)}
+    del xs
+    return out
+
+
+def extra_summary(r):
+    """The keys of a batched_measure result carried on the headline line."""
+    return {"us_per_layer": r["value"], "tokens_per_step": r["config"]["tokens_per_step"],
+            "tokens_per_s": r["tokens_per_s"], "layer_hbm_gbps": r["layer_hbm_gbps"],
+            "layer_hbm_frac": round(r["layer_hbm_gbps"] / HBM_PEAK_GBPS, 4),
+            "batched_call_hbm_frac": r["roofline"]["frac"],
+            "unique_experts_per_layer": r["unique_experts_per_layer"], "tokens_per_expert_max": r["tokens_per_expert_max"],
+            "expert_groups": r["expert_groups"], "mfma_utilization": r["mfma"]["utilization"],
+            "mfma_tops": r["mfma"]["mfma_tops"], "path": r["config"]["path"]}
 
 
 def measured_traffic(shape, kernel: str, n_layer: int):
@@ -574,7 +655,9 @@ def main():
 
     # ---- resident weights: 48 independent synthetic layers -------------------
     t0 = time.perf_counter()
-    cfg = shape.cfg(n_layer)
+    # the default run also measures the batched workloads on the same weights
+    extras = not args.no_extra and args.shape == "qwen3_30b" and args.layers is None and args.decode_kernel == "auto"
+    cfg = shape.cfg(n_layer, 0, 512 if extras else 1)
     h = ctypes.c_void_p()
     H.check(lib.hoard_moe_create(ctypes.byref(cfg), ctypes.byref(h)))
     if args.decode_kernel == "launches":
@@ -719,11 +802,40 @@ def main():
             result["phases_us"] = ph
             for k_, v_ in ph.items():
                 log(f"[phase] {k_:40s} {v_:8.3f} us")
-    # release every device object before the CPU leg: the handle, then torch's tensors
+    if extras:
+        # the verify-sized batch (16 tokens) and a prompt-sized one (512 tokens) on
+        # the same 48 resident layers, each token routed independently
+        xsteps, xwarm = max(1, min(steps, 20)), min(warm, 5)
+        for M, key in ((16, "batched_m16"), (512, "prefill_m512")):
+            r = batched_measure(lib, h, shape, n_layer, M, xsteps, xwarm, args.seed)
+            result[key] = extra_summary(r)
+            log(f"[bench] {key}: {r['value']:.2f} us/layer, {r['layer_hbm_gbps'] / 1e3:.2f} TB/s, "
+                f"{r['unique_experts_per_layer']:.1f} unique experts")
+    # release every device object before the next handle and the CPU leg: the
+    # handle, then torch's tensors
     lib.hoard_moe_destroy(h)
     del xs, xl, fxs
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    if extras:
+        # the Qwen3-Next-shaped decode: 48 layers of 512 experts, top-10 and a
+        # shared expert (50 GB resident), one plain launch of the rows-spread kernel
+        nx = W.QWEN3_NEXT
+        t1 = time.perf_counter()
+        cfg2 = nx.cfg(nx.n_layer)
+        h2 = ctypes.c_void_p()
+        H.check(lib.hoard_moe_create(ctypes.byref(cfg2), ctypes.byref(h2)))
+        load_layers(lib, h2, nx, nx.n_layer, args.seed)
+        log(f"[bench] {nx.n_layer} layers of {nx.name} resident in {time.perf_counter() - t1:.1f} s")
+        r2 = decode_measure(lib, h2, nx, nx.n_layer, max(1, min(steps, 20)), min(warm, 5), args.seed)
+        lib.hoard_moe_destroy(h2)
+        r2["workload"] = (f"{nx.name}: {nx.n_layer} stacked MoE layers, batch-1 decode, {nx.n_expert} experts "
+                          f"top-{nx.n_used} + a shared expert, ff {nx.n_ff}, all resident")
+        r2["decode_path"] = "one plain launch per token, expert rows spread over all CUs"
+        result["qwen3_next_decode"] = r2
+        log(f"[bench] qwen3_next_decode: {r2['us_per_layer']:.2f} us/layer ({r2['layer_hbm_frac']:.3f} of peak)")
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(shape, args.seed, args.cpu_seconds, n_layer)
     print(json.dumps(result), flush=True)

@@ -130,6 +130,11 @@ struct hoard_moe {
     // expert slot pool (pool_k > 0)
     hoard::SlotLru lru;
     bool pool_naive = false;
+    int pool_ids_cap = 0;             // ids one pool step takes: min(max_tokens, 512) x n_used
+    std::vector<int32_t> pool_slots;  // host scratch of a pool step, pool_ids_cap entries each
+    std::vector<uint8_t> pool_miss;
+    std::vector<int32_t> pool_mids;
+    std::vector<int> pool_mj;
     int32_t *pin_sel = nullptr;     // pinned [n_used]: device-routed ids read back on the on-demand path
     int32_t *slot_ids = nullptr;    // device [n_used]: slots of the on-demand path
     hipStream_t copy_x[kUpStreams - 1] = {};  // upload streams besides the caller's: copies in flight
@@ -147,6 +152,8 @@ struct hoard_moe {
     bool hist_pending = false;      // a batched call ran since the histogram was last read
     const unsigned *hist_src = nullptr;  // the last batched call's histogram and group count
     const int *nu_src = nullptr;
+    unsigned *nab_stats = nullptr;  // the allocation-free call's histogram [n_expert] and group count,
+                                    // copied out of the shared fixed array (allocated at creation)
     size_t trace_layers = 0;
     bool tracing = false;
     int trace_last = 0;  // layers covered by the last traced decode
@@ -197,6 +204,7 @@ struct hoard_moe {
         hipFree(b_ints);
         hipFree(b_hist);
         hipFree(b_counters);
+        hipFree(nab_stats);
     }
     static void free_layer(Layer &L) {
         for (auto ev : L.copied)
@@ -405,6 +413,11 @@ int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, flo
     a.wait_ticks = h->wait_ticks;
     if (!hoard::fused_layer_ok(a)) return HOARD_OK;
     if (h->tracing) {
+        // the stamp buffer may be (re)allocated here, which a capturing stream must not see
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(s, &capture));
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(HOARD_ERR_UNSUPPORTED, "one-launch layer: phase tracing is not captured");
         // phase stamps of this launch: [workgroup][kFusedStamps] (read with hoard_moe_fused_trace_read)
         const size_t words = (size_t)hoard::fused_layer_groups(a) * hoard::kFusedStamps;
         if (h->ftrace_words < words) {
@@ -428,7 +441,11 @@ int run_layer_fused(hoard_moe *h, const Layer &L, const float *xin, int rms, flo
 // missed experts on copy_stream (after the previous FFN that read this layer's
 // slots), and `stream` made to wait for them.  slot_dev (optional) receives
 // the slot ids through a pinned staging copy on `stream`.
-constexpr int kMaxPoolIds = 16 * 16;  // ids one pool step takes: up to 16 tokens x 16 experts
+// ids one pool step takes: a batch of up to 512 tokens (the batched entry
+// points' limit) times n_used
+int pool_ids_cap(const hoard_moe_cfg &c) {
+    return std::min(c.max_tokens, hoard::kBatchedMaxTokensLarge) * c.n_used;
+}
 
 // One slot upload.  HOARD_OPT_FAIL_UPLOAD counts down to an upload that fails
 // as a refused hipMemcpyAsync would, before anything is issued.
@@ -452,8 +469,9 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
     Layer &L = h->layers[layer];
     for (int j = 0; j < n; ++j)
         if (sel[j] < 0 || sel[j] >= c.n_expert) return fail(HOARD_ERR_INVALID, "expert id %d out of range", sel[j]);
-    int32_t slots[kMaxPoolIds];
-    uint8_t miss[kMaxPoolIds];
+    if (n > h->pool_ids_cap) return fail(HOARD_ERR_INVALID, "%d ids in one pool step (at most %d)", n, h->pool_ids_cap);
+    int32_t *slots = h->pool_slots.data();
+    uint8_t *miss = h->pool_miss.data();
     if (sequential)
         h->lru.access_sequential(layer, sel, n, slots, miss);
     else
@@ -486,8 +504,8 @@ int pool_ensure(hoard_moe *h, int layer, const int32_t *sel, int n, bool sequent
         // storage tier: the RAM tier serves or reads the missed experts (reads in
         // parallel, on the host), then each is uploaded from its RAM entry,
         // which is fenced until the upload is done
-        int32_t mids[kMaxPoolIds];
-        int mj[kMaxPoolIds], nm = 0;
+        int32_t *mids = h->pool_mids.data();
+        int *mj = h->pool_mj.data(), nm = 0;
         for (int j = 0; j < n; ++j)
             if (miss[j]) {
                 mj[nm] = j;
@@ -901,6 +919,11 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
         rc = fail(HOARD_ERR_HIP, "hipMemset counters");
     if (!rc && c.pool_k > 0) {
         h->lru.reset(c.n_layer, c.n_expert, c.pool_k);
+        h->pool_ids_cap = std::max(pool_ids_cap(c), c.n_used);
+        h->pool_slots.assign(h->pool_ids_cap, 0);
+        h->pool_miss.assign(h->pool_ids_cap, 0);
+        h->pool_mids.assign(h->pool_ids_cap, 0);
+        h->pool_mj.assign(h->pool_ids_cap, 0);
         if (hipHostMalloc((void **)&h->pin_sel, sizeof(int32_t) * c.n_used, hipHostMallocDefault) != hipSuccess)
             rc = fail(HOARD_ERR_OOM, "pinned selection buffer");
         rc = rc ? rc : dev_alloc((void **)&h->slot_ids, sizeof(int32_t) * c.n_used);
@@ -909,6 +932,7 @@ int hoard_moe_create(const hoard_moe_cfg *cfg, hoard_moe **out) {
                 rc = fail(HOARD_ERR_HIP, "upload stream");
     }
     if (!rc) rc = persistent_setup(h);
+    rc = rc ? rc : dev_alloc((void **)&h->nab_stats, sizeof(unsigned) * (c.n_expert + 1));
     if (!rc) {
         // this device's copy of the allocation-free entry point's fixed scratch
         const hipError_t e = hoard::noalloc_setup(h->device);
@@ -998,7 +1022,7 @@ int hoard_moe_set_layer_weights(hoard_moe *h, int layer, const hoard_layer_weigh
                 std::memcpy(r + L.gbytes + L.ubytes, d + e * L.dbytes, L.dbytes);
             }
         }
-        if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * kMaxPoolIds, hipHostMallocDefault) != hipSuccess)
+        if (!rc && hipHostMalloc((void **)&L.slot_stage, sizeof(int32_t) * h->pool_ids_cap, hipHostMallocDefault) != hipSuccess)
             rc = fail(HOARD_ERR_OOM, "pinned slot staging");
         for (int i = 0; !rc && i < kUpStreams; ++i)
             if (hipEventCreateWithFlags(&L.copied[i], hipEventDisableTiming) != hipSuccess) rc = fail(HOARD_ERR_HIP, "pool events");
@@ -1383,10 +1407,16 @@ int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const floa
         e = hoard::launch_batched(a, s);
     }
     if (e != hipSuccess) return fail(HOARD_ERR_HIP, "batched launch: %s", hipGetErrorString(e));
+    // the histogram and group count move out of the array every call on this GPU
+    // shares into the handle's own words, so hoard_moe_get_stats reports this call
+    // whatever later calls of other handles leave in the array
+    const int E = c.n_expert;
+    HIP_TRY(hipMemcpyAsync(h->nab_stats, a.hist, sizeof(unsigned) * E, hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(h->nab_stats + E, a.n_unique, sizeof(int), hipMemcpyDeviceToDevice, s));
     h->stats.tokens += (uint64_t)M;
     h->hist_pending = true;
-    h->hist_src = a.hist;
-    h->nu_src = a.n_unique;
+    h->hist_src = h->nab_stats;
+    h->nu_src = reinterpret_cast<const int *>(h->nab_stats + E);
     return HOARD_OK;
 }
 
@@ -1418,8 +1448,9 @@ int hoard_moe_pool_ensure_batched(hoard_moe *h, int layer, int n, const int32_t 
     if (c.pool_k == 0) return fail(HOARD_ERR_STATE, "handle has no slot pool (pool_k == 0)");
     if (h->pool_naive) return fail(HOARD_ERR_STATE, "naive pool mode places one token's experts; not a batch");
     if (!sel_host || (!slot_host && !slot_dev)) return fail(HOARD_ERR_INVALID, "null argument");
-    if (n < 1 || n > kMaxPoolIds || n > c.max_tokens * c.n_used)
-        return fail(HOARD_ERR_INVALID, "%d ids outside 1..max_tokens * n_used (%d)", n, c.max_tokens * c.n_used);
+    if (n < 1 || n > h->pool_ids_cap)
+        return fail(HOARD_ERR_INVALID, "%d ids outside 1..min(max_tokens, %d) * n_used (%d)", n,
+                    hoard::kBatchedMaxTokensLarge, h->pool_ids_cap);
     // every distinct expert of the batch must hold a slot at once
     std::vector<int32_t> u(sel_host, sel_host + n);
     std::sort(u.begin(), u.end());

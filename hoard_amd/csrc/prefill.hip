@@ -199,6 +199,10 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     stage_x(0, 0);
 #pragma unroll 1
     for (int b = 0; b < NB; ++b) {
+        // Other waves read the x chunks this wave copied: the compiler does not
+        // see the copies, so the wave waits for its own before the barrier (it
+        // waits for the raw weight loads of block b there anyway).
+        lds_dma_wait();
         __syncthreads();  // every wave's copies of x(b) landed, and x(b - 1) is read
         Q4Fold t;
         q4_fold(raw, t);

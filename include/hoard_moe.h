@@ -160,7 +160,10 @@ int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_de
    the array is refused with HOARD_ERR_INVALID (the Qwen3-30B shape needs about
    17 MiB at M = 16, the Qwen3-Next shape about 16.5 MiB).  Results are hoard_moe_forward_batched's bit for bit.  Every
    call on a GPU shares that GPU's array: calls that overlap on one GPU (any
-   handle, any stream) race. */
+   handle, any stream) race.  The call's histogram and unique-expert count are
+   copied into the handle's own memory on `stream` (allocated by
+   hoard_moe_create), so hoard_moe_get_stats reports them whatever later calls
+   on the GPU leave in the array. */
 int hoard_moe_forward_batched_noalloc(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
                                       float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 
@@ -179,10 +182,12 @@ int hoard_moe_ffn_combine_batched(hoard_moe *h, int layer, int M, const float *f
                                   const float *w_dev, const float *res_dev, float *out_dev, void *stream);
 
 /* Slot-pool step for a batch (pool_k > 0): the n ids sel_host[] of up to
-   max_tokens tokens (token-major, n_used per token), taken one after the other
-   as the verify loop's ensure does (src/run_specloop.cpp:59-67; no hits-first
-   pass), uploads as hoard_moe_pool_ensure.  The distinct experts must fit the
-   K slots.  slot_host / slot_dev (either optional) receive n slots. */
+   min(max_tokens, 512) tokens (token-major, n_used per token, so
+   1 <= n <= min(max_tokens, 512) * n_used: the batch hoard_moe_ffn_combine_batched
+   takes), taken one after the other as the verify loop's ensure does
+   (src/run_specloop.cpp:59-67; no hits-first pass), uploads as
+   hoard_moe_pool_ensure.  The distinct experts must fit the K slots.
+   slot_host / slot_dev (either optional) receive n slots. */
 int hoard_moe_pool_ensure_batched(hoard_moe *h, int layer, int n, const int32_t *sel_host, int32_t *slot_host,
                                   int32_t *slot_dev, void *stream, void *copy_stream);
 

@@ -12,11 +12,15 @@
  *   orc_dequant_q{3,4,5,6}_K             pinned: independent encoder + known-answer blocks
  *   orc_quantize_q8_K                    pinned: closed-form special cases + bounds
  *   orc_vec_dot_q{3,4,5,6}_K_q8_K        pinned: fp64 brute force over dequantised operands
- *   orc_vec_dot_f32                      pinned: fp64 within bound + order-sensitive vector
+ *   orc_vec_dot_f32                      pinned: fp64 within bound (the value only)
  *   orc_route                            pinned: fp64 softmax, brute-force top-k, clamp
  *   orc_expert_ffn / orc_moe_*           pinned: fp64 composition of the pinned parts
  *   fp32 summation ORDER of ggml's SIMD kernels: parity unpinned (ggml absent);
- *   the order used is stated at each function.
+ *   the order used is stated at each function.  The router dot's order in
+ *   particular is a choice, not a pin: it is the tree of ggml-cpu's AVX2 build;
+ *   the AVX-512 build of the same ggml (which an AVX-512 host loads) steps 64
+ *   elements as 4 vectors of 16 lanes and reduces another tree, so its logits
+ *   may differ in the last bits from these.
  */
 #include "moe_oracle.h"
 

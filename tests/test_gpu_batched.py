@@ -220,3 +220,69 @@ def test_batched_few_experts(orc, E, k):
             parity.assert_parity(out[t], ref[t], f"E={E} token {t}")
     finally:
         st.close()
+
+
+def test_pooled_verify_step_above_256_ids(orc):
+    """A pooled verify step of 48 tokens at top-8 (384 ids in one ensure, the
+    prefill-sized kernels over slots): bit-identical to the all-resident handle,
+    and the pool's hits and misses are the host replay's.  The cap is
+    min(max_tokens, 512) * n_used ids; one more is refused."""
+    import ctypes
+
+    from hoard_amd.runtime import MoEStage
+    shape, M = W.QWEN3_30B, 48
+    K = shape.n_expert
+    hl = W.make_layer(shape, 9, 0)
+    ref = MoEStage(shape, n_layer=1, layers={0: hl}, max_tokens=M)
+    st = MoEStage(shape, n_layer=1, layers={0: hl}, pool_k=K, max_tokens=M)
+    lib = H.load_library()
+    rp = ctypes.c_void_p()
+    H.check(lib.hoard_slot_lru_create(1, shape.n_expert, K, 2, ctypes.byref(rp)))
+    try:
+        for step in range(2):
+            fx, res = _tokens(shape, M, 3000 + 17 * step)
+            ids, w = _routing(orc, shape, hl, fx)
+            print(f"pooled verify step {step}: {ids.size} ids, {len(np.unique(ids))} distinct", flush=True)
+            slots = st.pool_ensure_batched(0, ids)
+            rs = np.zeros(ids.size, np.int32)
+            rm = np.zeros(ids.size, np.uint8)
+            flat = np.ascontiguousarray(ids.ravel())
+            H.check(lib.hoard_slot_lru_access(rp, 0, flat.ctypes.data, flat.size, rs.ctypes.data, rm.ctypes.data))
+            assert np.array_equal(slots.ravel(), rs)
+            got = st.ffn_combine_batched(0, fx, slots, w, res)
+            exp = ref.ffn_combine_batched(0, fx, ids, w, res)
+            assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), step
+            parity.assert_parity(got[0], orc.moe_ffn_combine(hl, fx[0], ids[0], w[0], res[0]), "pooled token 0")
+        too_many = np.zeros(M * shape.n_used + 1, np.int32)
+        with pytest.raises(H.HoardError) as ei:
+            st.pool_ensure_batched(0, too_many)
+        assert ei.value.code == H.ERR_INVALID
+    finally:
+        lib.hoard_slot_lru_destroy(rp)
+        st.close()
+        ref.close()
+
+
+@pytest.mark.parametrize("M", [17, 32])
+def test_qwen35_verify_sizes_above_16(orc, M):
+    """Qwen3.5's Q5_K routed down rows beside its Q6_K shared down in one down
+    launch, for groups of more than 16 tokens (the shared group holds all M, so
+    its tile takes a second 16-column MFMA pass): every token the single-token
+    path's bits, and the batch against the oracle."""
+    from hoard_amd.runtime import MoEStage
+    shape = W.QWEN35
+    hl = W.make_layer(shape, 4, 0)
+    st = MoEStage(shape, n_layer=1, layers={0: hl}, max_tokens=32)
+    try:
+        fx, res = _tokens(shape, M, 40 * M)
+        print(f"batched {shape.name} M={M}", flush=True)
+        out, sel, _ = st.forward_batched(0, fx, res)
+        ref, sel_o, _ = orc.moe_layer_batched(hl, fx, res)
+        assert np.array_equal(sel, sel_o)
+        for t in range(M):
+            o1, s1, _ = st.layer(0, fx[t], res[t])
+            assert np.array_equal(s1, sel[t])
+            assert np.array_equal(o1.view(np.uint32), out[t].view(np.uint32)), f"token {t}"
+            parity.assert_parity(out[t], ref[t], f"batched {shape.name} M={M} token {t}")
+    finally:
+        st.close()

@@ -5,6 +5,7 @@
   that chain must match the oracle applied to the device's own input of the
   layer (top-k indices identical, output within the bar).  The per-layer launch
   path (hoard_moe_layer's kernels) over the same 48 layers is held to the bar.
+  The same for 48 Qwen3-Next-shaped layers through the rows-spread kernel.
 * The slot-pool workload as measured: K = 32 slots per layer over all 48 layers,
   routing from the seeded 512-token trace (Zipf(0.8) popularity per layer, 40 %
   reuse of the last 4 tokens' experts).  Every token's chained hidden through the
@@ -30,8 +31,8 @@ SHAPE = W.QWEN3_30B
 NL = 48
 
 
-def _fill(st_list, seed):
-    hl = W.make_layer(SHAPE, seed, 0)
+def _fill(st_list, seed, shape=SHAPE):
+    hl = W.make_layer(shape, seed, 0)
     for l in range(NL):
         if l:
             W.fill_layer(hl, seed, l)
@@ -40,18 +41,22 @@ def _fill(st_list, seed):
     del hl
 
 
-def test_headline_stack_48_layers(orc):
+def _stack_against_oracle(orc, shape, seed, kernel):
+    """48 layers of `shape` decoded in one launch of the one-launch kernel
+    `kernel` (1 expert per XCD, 2 rows spread), for 2 tokens: bit-identical to
+    the same kernel run one layer per launch, every layer of that chain against
+    the oracle applied to the device's own input of the layer (top-k identical,
+    output within the bar), and the per-layer launches within the bar."""
     from hoard_amd.runtime import MoEStage
-    seed = 31
-    st = MoEStage(SHAPE, n_layer=NL)
+    st = MoEStage(shape, n_layer=NL)
     try:
-        print("stack: uploading 48 layers", flush=True)
-        _fill([st], seed)
+        print(f"stack {shape.name}: uploading 48 layers", flush=True)
+        _fill([st], seed, shape)
         st.set_option(H.OPT_PERSISTENT_DECODE, 2)
-        assert st.get_option(H.OPT_DECODE_KERNEL) == 0 and st.get_option(H.OPT_DECODE_KERNELS_AVAILABLE) & 1
+        st.set_option(H.OPT_DECODE_KERNEL, kernel)
         for tok in range(2):
-            _, x = W.make_hidden(SHAPE, seed, 0, tok)
-            print(f"stack token {tok}: one launch over 48 layers", flush=True)
+            _, x = W.make_hidden(shape, seed, 0, tok)
+            print(f"stack {shape.name} token {tok}: one launch over 48 layers", flush=True)
             whole = st.decode(x, 0, NL, W.RMS_EPS)
             st.sync_check()
             xs = [x]
@@ -62,22 +67,34 @@ def test_headline_stack_48_layers(orc):
             worst = {"max_rel": 0.0, "cos": 1.0, "bit_identical": 1.0}
             for l in range(NL):
                 fx = orc.rms_norm(xs[l], W.RMS_EPS)
-                router = W.make_router(SHAPE, seed, l)
-                sel_o, _, _ = orc.route(router, fx, SHAPE.n_expert, SHAPE.n_used, SHAPE.renorm)
-                hl = W.make_layer(SHAPE, seed, l, experts=sel_o)
+                router = W.make_router(shape, seed, l)
+                sel_o, _, _ = orc.route(router, fx, shape.n_expert, shape.n_used, shape.renorm)
+                hl = W.make_layer(shape, seed, l, experts=sel_o)
                 ref, sel_r, _ = orc.moe_layer(hl, fx, xs[l])
                 assert np.array_equal(sel_r, sel_o)
-                m = parity.assert_parity(xs[l + 1], ref, f"stack token {tok} layer {l}")
+                m = parity.assert_parity(xs[l + 1], ref, f"stack {shape.name} token {tok} layer {l}")
                 worst = {"max_rel": max(worst["max_rel"], m["max_rel"]), "cos": min(worst["cos"], m["cos"]),
                          "bit_identical": min(worst["bit_identical"], m["bit_identical"])}
             print(f"   48 layers against the oracle, worst {worst}", flush=True)
             st.set_option(H.OPT_PERSISTENT_DECODE, 0)
             launched = st.decode(x, 0, NL, W.RMS_EPS)
             st.set_option(H.OPT_PERSISTENT_DECODE, 2)
-            m = parity.assert_parity(launched, whole, f"stack token {tok}: per-layer launches vs one launch")
+            m = parity.assert_parity(launched, whole, f"stack {shape.name} token {tok}: per-layer launches vs one launch")
             print(f"   per-layer launches vs one launch {m}", flush=True)
     finally:
         st.close()
+
+
+def test_headline_stack_48_layers(orc):
+    _stack_against_oracle(orc, SHAPE, 31, H.DECODE_XCD)
+
+
+def test_qwen3_next_stack_48_layers(orc):
+    """The Qwen3-Next-shaped decode at its stated depth: 48 layers of 512
+    experts, top-10 and the sigmoid-gated shared expert (50 GB resident),
+    through the rows-spread one-launch kernel, whose exchange tags and
+    mailboxes are carried across all 48 layers."""
+    _stack_against_oracle(orc, W.QWEN3_NEXT, 37, H.DECODE_SPREAD)
 
 
 def _replay(trace, k):

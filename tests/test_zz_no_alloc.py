@@ -86,3 +86,28 @@ def test_noalloc_refuses_sizes_past_its_limit():
         assert b"fixed array" in st.lib.hoard_last_error()
     finally:
         st.close()
+
+
+def test_noalloc_stats_belong_to_the_handle():
+    """Two handles on one GPU share the fixed array: each handle's statistics
+    still report its own last call after the other handle's call."""
+    from hoard_amd.runtime import MoEStage
+    shape = W.QWEN3_30B
+    mk = lambda: MoEStage(shape, n_layer=1, layers={0: W.make_layer(shape, 13, 0, experts=[])},  # noqa: E731
+                          max_tokens=16)
+    sa, sb = mk(), mk()
+    try:
+        rc, ba = _noalloc(sa, 0, *_tokens(shape, 16, 0))
+        H.check(rc)
+        rc, bb = _noalloc(sb, 0, *_tokens(shape, 5, 100))
+        H.check(rc)
+        torch.cuda.synchronize()
+        for st, bufs, M in ((sa, ba, 16), (sb, bb, 5)):
+            sel = bufs[3].cpu().numpy()
+            counts = np.bincount(sel.ravel(), minlength=shape.n_expert)
+            stats = st.stats()
+            assert np.array_equal(np.array(stats.expert_hist[:shape.n_expert]), counts), M
+            assert stats.last_unique == len(np.unique(sel)), M
+    finally:
+        sa.close()
+        sb.close()
