@@ -69,14 +69,25 @@ __device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
 // at once.  The min term sum_s m_s * (sum of sub-block s's activation quants)
 // is a third MFMA with m_s broadcast over its sub-block.  The three chains give
 // exactly the per-token path's integer sums isum = 8 D_hi + D_lo and
-// msum = D_min.
+// msum = D_min.  Each 16-bit half of a word of four nibbles multiplies at once
+// (v_pk_mul_lo_u16, full rate, where a 32-bit multiply is quarter rate).
 struct Q4Fold {
     v4i hi[4], lo[4];
     uint32_t mn;          // byte jc: the min of the lane's sub-block in chunk jc
     float d[4], dmin[4];  // factors of the four rows whose results the lane receives
 };
 
-__device__ __forceinline__ uint32_t splat_byte(uint32_t v) { return v * 0x01010101u; }
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+// Bytes of w (each <= 15) times f (<= 7), byte by byte: no product carries.
+__device__ __forceinline__ int nib_mul(uint32_t w, uint32_t f) {
+    const v2u16 m = {(unsigned short)f, (unsigned short)f};
+    return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, w) * m);
+}
+
+// Byte i of w in all four bytes (one v_perm_b32).
+__device__ __forceinline__ int splat_byte_of(uint32_t w, int i) {
+    return (int)__builtin_amdgcn_perm(w, w, 0x01010101u * (uint32_t)i);
+}
 
 // The lane's raw bytes of one super-block of a 16-row tile: its row's header
 // and quants (16 bytes of each 64-element chunk) and the fp16 factors of the
@@ -112,8 +123,8 @@ __device__ __forceinline__ void q4_fold(const Q4Raw &raw, Q4Fold &o) {
         const uint32_t w[4] = {(qv.x >> nsh) & 0x0f0f0f0fu, (qv.y >> nsh) & 0x0f0f0f0fu, (qv.z >> nsh) & 0x0f0f0f0fu,
                                (qv.w >> nsh) & 0x0f0f0f0fu};
         const uint32_t h = scs >> 3, lw = scs & 7u;
-        o.hi[jc] = v4i{(int)(w[0] * h), (int)(w[1] * h), (int)(w[2] * h), (int)(w[3] * h)};
-        o.lo[jc] = v4i{(int)(w[0] * lw), (int)(w[1] * lw), (int)(w[2] * lw), (int)(w[3] * lw)};
+        o.hi[jc] = v4i{nib_mul(w[0], h), nib_mul(w[1], h), nib_mul(w[2], h), nib_mul(w[3], h)};
+        o.lo[jc] = v4i{nib_mul(w[0], lw), nib_mul(w[1], lw), nib_mul(w[2], lw), nib_mul(w[3], lw)};
         o.mn |= mns << (8 * jc);
     }
 #pragma unroll
@@ -134,7 +145,7 @@ __device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const Q8L &x, floa
         const v4i xv = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
         dh = mfma_16x16x64(w.hi[jc], xv, dh);
         dl = mfma_16x16x64(w.lo[jc], xv, dl);
-        const int m4 = (int)splat_byte((w.mn >> (8 * jc)) & 0xffu);
+        const int m4 = splat_byte_of(w.mn, jc);
         dn = mfma_16x16x64(v4i{m4, m4, m4, m4}, xv, dn);
     }
     const float xd = x.d;
@@ -313,8 +324,8 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
 // bits 4 (jc % 2) + 2 (g / 2) .. + 1 of qh bytes 128 + 32 (jc / 2) + 16 (g % 2) ..
 // + 15 on top, and which share one group scale, sc = scales[4 jc + g].  The
 // per-token path forms isum = sum_g sc_g * sum_{e in g} (q_e - 32) x_e.  Here
-// w = sc * q (|w| <= 8128) is split as w = 64 hi + lo with lo in [-32, 31] and
-// hi in [-127, 127], both int8, and the zero point comes from a third MFMA with
+// w = sc * q (-8064 <= w <= 8001) is split as w = 64 hi + lo with lo = w & 63 in
+// [0, 63] and hi = w >> 6 in [-126, 125], both int8, and the zero point comes from a third MFMA with
 // sc broadcast over the lane's 16 elements (the token's group sums):
 // isum = 64 D_hi + D_lo - 32 D_sc, exactly.  A super-block of the tile is
 // folded once and used for every token chunk of the unit.
@@ -351,9 +362,9 @@ __device__ __forceinline__ void q6_fold(const uint8_t *T, size_t rb, int b, Q6Fo
             typedef short v2s __attribute__((ext_vector_type(2)));
             const v2s s2 = __builtin_bit_cast(v2s, sc16);
             const v2s a02 = __builtin_bit_cast(v2s, w02) * s2, a13 = __builtin_bit_cast(v2s, w13) * s2;
-            // hi = (w + 32) >> 6 (arithmetic), lo = w - 64 hi
-            const v2s h02 = (a02 + (v2s){32, 32}) >> (v2s){6, 6}, h13 = (a13 + (v2s){32, 32}) >> (v2s){6, 6};
-            const v2s l02 = a02 - (h02 << (v2s){6, 6}), l13 = a13 - (h13 << (v2s){6, 6});
+            // hi = w >> 6 (arithmetic: floor(w / 64)), lo = w & 63 = w - 64 hi
+            const v2s h02 = a02 >> (v2s){6, 6}, h13 = a13 >> (v2s){6, 6};
+            const v2s l02 = a02 & (v2s){63, 63}, l13 = a13 & (v2s){63, 63};
             // back to bytes: result byte 2i from the 02 half i, byte 2i + 1 from the 13 half i
             hw[k] = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h13), __builtin_bit_cast(uint32_t, h02),
                                                0x06020400u);
@@ -390,7 +401,7 @@ __device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, flo
     for (int jc = 0; jc < 4; ++jc) {
         dh = mfma_16x16x64(w.hi[jc], x.x[jc], dh);
         dl = mfma_16x16x64(w.lo[jc], x.x[jc], dl);
-        const int s4 = (int)splat_byte((w.sc >> (8 * jc)) & 0xffu);
+        const int s4 = splat_byte_of(w.sc, jc);
         ds = mfma_16x16x64(v4i{s4, s4, s4, s4}, x.x[jc], ds);
     }
 #pragma unroll
