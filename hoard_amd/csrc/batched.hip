@@ -625,13 +625,16 @@ __device__ __forceinline__ void gather_tokens(uint8_t *xs, const uint8_t *q8base
 
 // -- gate/up: 8 rows of gate (wave 0) and up (wave 1) of one expert ----------
 // Per-token dot: one 8-lane group per row, lane t holding the token's Q8_K
-// block t.  MFMA: the 8 rows fill a 16-row tile twice.
-template <int NB>
+// block t.  MFMA (Q4_K groups of kMfmaMinTokens or more): the 8 rows fill a
+// 16-row tile twice.  Q3_K groups of any size run token by token.
+template <int TGU, int NB>
 __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     static_assert(NB == 8, "one 8-lane group per row, one lane per super-block");
+    static_assert(TGU == kTypeQ4K || TGU == kTypeQ3K, "gate/up rows are Q4_K or Q3_K");
     constexpr int kRows = 8;
-    constexpr int kRowBytes = NB * kQ4KBytes;
+    constexpr int kRowBytes = NB * QType<TGU>::bytes;
     constexpr int kTileBytes = kRows * kRowBytes;
+    static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
     const int u = blockIdx.y;
     int e, m;
     if (!load_group(a, u, e, m)) return;
@@ -651,7 +654,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
             a.hbuf[((size_t)u * kMaxTok + c0 + cc) * a.n_ff + row0 + r] = g / (1.0f + expf(-g)) * uu;
         }
     };
-    if (m >= kMfmaMinTokens) {
+    if (TGU == kTypeQ4K && m >= kMfmaMinTokens) {
         dma_wave_copy_nt(wt[wave], W, kTileBytes);
         lds_dma_wait();
         // 16 token columns at a time over the LDS tile
@@ -669,10 +672,9 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
         }
         return;
     }
-    // fewer than kMfmaMinTokens <= 16 tokens: x goes into LDS with the tile,
-    // kXChunk tokens at a time (a vector load issued during the compute would
-    // queue behind the tile copies of the other workgroups on this CU)
-    static_assert(kMfmaMinTokens <= kCols, "a per-token group fits the 16 columns of gu");
+    // token by token: x goes into LDS with the tile, kXChunk tokens at a time (a
+    // vector load issued during the compute would queue behind the tile copies
+    // of the other workgroups on this CU); h is stored every 16 token columns
     const Q8L *xl = reinterpret_cast<const Q8L *>(xs);
     for (int c0 = 0; c0 < m; c0 += kXChunk) {
         const int mc = min(m - c0, kXChunk);
@@ -683,11 +685,18 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
         __syncthreads();
 #pragma unroll 1
         for (int c = 0; c < mc; ++c) {
-            const float v = lpb_row_q4k_mem<NB, true>(wt[wave] + grp * kRowBytes, xl[c * NB + t8], t8);
-            if (t8 == NB - 1) gu[wave][grp][c0 + c] = v;
+            const uint8_t *rp = wt[wave] + grp * kRowBytes;
+            float v;
+            if constexpr (TGU == kTypeQ3K)
+                v = lpb_row_q3k_mem<NB, true>(rp, xl[c * NB + t8], t8);
+            else
+                v = lpb_row_q4k_mem<NB, true>(rp, xl[c * NB + t8], t8);
+            if (t8 == NB - 1) gu[wave][grp][(c0 + c) % kCols] = v;
         }
+        static_assert(kCols % kXChunk == 0, "a chunk of tokens stays within 16 columns");
+        if ((c0 + mc) % kCols == 0 && c0 + mc < m) store_h(c0 + mc - kCols);  // a full 16 columns, more to come
     }
-    store_h(0);
+    store_h((m - 1) / kCols * kCols);
 }
 
 // -- Q8_K of h per (expert, token) ---------------------------------------------
@@ -831,7 +840,8 @@ __global__ __launch_bounds__(256) void combine_kernel(BatchedArgs a) {
 }  // namespace
 
 bool batched_shape_compiled(int gu_type, int n_embd, int d_type, int n_ff) {
-    return gu_type == kTypeQ4K && n_embd == 2048 && (n_ff == 768 || n_ff == 1024 || n_ff == 512) &&
+    return (gu_type == kTypeQ4K || gu_type == kTypeQ3K) && n_embd == 2048 &&
+           (n_ff == 768 || n_ff == 1024 || n_ff == 512) &&
            (d_type == kTypeQ4K || d_type == kTypeQ6K || (d_type == kTypeQ5K && n_ff != 768));
 }
 
@@ -841,7 +851,10 @@ namespace {
 hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
     const int nbh = a.n_ff / QK;
     const int umax = (a.n_ids < a.M * a.k ? a.n_ids : a.M * a.k) + a.sh;
-    hipLaunchKernelGGL(gateup_kernel<8>, dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
+    if (a.gu_type == kTypeQ3K)
+        hipLaunchKernelGGL((gateup_kernel<kTypeQ3K, 8>), dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
+    else
+        hipLaunchKernelGGL((gateup_kernel<kTypeQ4K, 8>), dim3(a.n_ff / 8, umax), dim3(128), 0, s, a);
     // a group holds at most M (<= kMaxTok) tokens
     hipLaunchKernelGGL(quant_h_kernel, dim3(a.M, umax), dim3(64 * nbh), 0, s, a);
     const dim3 dg(a.n_embd / kTile, umax);
@@ -861,7 +874,8 @@ hipError_t launch_groups(const BatchedArgs &a, hipStream_t s) {
 }
 
 bool args_ok(const BatchedArgs &a) {
-    return a.M >= 1 && a.M <= kBatchedMaxTokensLarge && a.n_embd == kRouteN && a.gu_type == kTypeQ4K &&
+    return a.M >= 1 && a.M <= kBatchedMaxTokensLarge && a.n_embd == kRouteN &&
+           (a.gu_type == kTypeQ4K || a.gu_type == kTypeQ3K) &&
            a.k + a.sh <= kMaxK && a.n_ids >= 1 && a.n_ids + a.sh <= kMaxExperts && a.E + a.sh <= kMaxExperts &&
            (!a.sh || (a.sh == 1 && a.sh_gate && a.sh_up && a.sh_down && a.sh_gate_inp && a.sgl)) &&
            (a.M <= kMaxTok || (a.goff && a.ptok && a.pslot && a.pexp && a.units && a.n_units && a.max_units >= 1));

@@ -1274,10 +1274,6 @@ int batched_check(hoard_moe *h, int layer, int M, const float *fx_dev, const flo
     if (L.up_type != L.gate_type || !hoard::batched_shape_compiled(L.gate_type, c.n_embd, L.down_type, c.n_ff))
         return fail(HOARD_ERR_UNSUPPORTED, "batched path: types %d/%d/%d with n_embd %d, n_ff %d not built",
                     L.gate_type, L.up_type, L.down_type, c.n_embd, c.n_ff);
-    // the prefill units (above kBatchedMaxTokens tokens) have Q4_K and Q6_K down tiles only
-    if (M > hoard::kBatchedMaxTokens && (L.down_type == HOARD_TYPE_Q5_K || (c.n_ff_shexp > 0 && L.sh_down_type != L.down_type)))
-        return fail(HOARD_ERR_UNSUPPORTED, "batched path: Q5_K down rows take at most %d tokens per call",
-                    hoard::kBatchedMaxTokens);
     if ((((uintptr_t)fx_dev | (uintptr_t)res_dev | (uintptr_t)out_dev) & 15) != 0)
         return fail(HOARD_ERR_INVALID, "fx, res and out must be 16-byte aligned");
     // the weight tiles are copied to LDS in 16-byte units

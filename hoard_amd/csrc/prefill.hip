@@ -15,6 +15,9 @@
 //   Q8_K(h)  per pair;
 //   down     64 rows per workgroup, the tile staged in LDS in one burst;
 //            y goes to its (token, slot) place;
+// Q3_K gate/up rows (pf_gateup_q3_kernel) and Q4_K / Q5_K down rows run one
+// MFMA per sub-block or scale group with the scales applied per (row, token)
+// (mfma.h); Q4_K gate/up and Q6_K down rows fold the scales into the operand.
 //   combine  per token, slots in order, plus the residual.
 // Every expert's weights are read once per unit (once per call for a group of
 // at most kUnitTokens tokens); each (row, token) value is formed from the
@@ -261,11 +264,11 @@ __global__ __launch_bounds__(256) void pf_quant_h_kernel(BatchedArgs a) {
 }
 
 // -- down: 64 rows of the unit's expert, y to its (token, slot) place -----------
-// grid (n_embd / 64, max units), block 256.  The 64-row tile is copied into LDS
-// in one burst; wave w takes rows [16 w, +16) of it.
-template <int TD, int NBH>
-__global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
-    constexpr int kRowBytes = NBH * QType<TD>::bytes;
+// grid (n_embd / 64, max units), block 256, for Q4_K down rows (OLMoE).  The
+// 64-row tile is copied into LDS in one burst; wave w takes rows [16 w, +16) of it.
+template <int NBH>
+__global__ __launch_bounds__(256) void pf_down_q4_kernel(BatchedArgs a) {
+    constexpr int kRowBytes = NBH * kQ4KBytes;
     constexpr int kTileBytes = kDnRows * kRowBytes;
     static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
     __shared__ __align__(16) uint8_t tile[kTileBytes];
@@ -296,17 +299,14 @@ __global__ __launch_bounds__(256) void pf_down_kernel(BatchedArgs a) {
     for (int st = 0; st < steps; ++st) {
         const int ch = st / NBH, b = st - ch * NBH;
         if (st + 1 < steps) q6_load_x(xq_of((st + 1) / NBH), (st + 1) % NBH, nxt);
-        if constexpr (TD == kTypeQ4K)
-            q4_tile_block(T, kRowBytes, b, cur, acc, accm);
-        else
-            q6_tile_block(T, kRowBytes, b, cur, acc);
+        q4_tile_block(T, kRowBytes, b, cur, acc, accm);
         if (b == NBH - 1) {
             const int idx = ch * 16 + c;
             if (idx < w.n) {
                 const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
                 float v[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = TD == kTypeQ4K ? acc[i] - accm[i] : acc[i];
+                for (int i = 0; i < 4; ++i) v[i] = acc[i] - accm[i];
                 *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows +
                                             4 * q) = make_float4(v[0], v[1], v[2], v[3]);
             }
@@ -411,6 +411,232 @@ __device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, flo
     }
 }
 
+typedef short v2s16 __attribute__((ext_vector_type(2)));
+typedef unsigned short v2u16b __attribute__((ext_vector_type(2)));
+
+// Bytes 0, 2 and 1, 3 of w in the 16-bit halves of two words, and back.
+__device__ __forceinline__ void bytes_to_halves(uint32_t w, uint32_t &w02, uint32_t &w13) {
+    w02 = __builtin_amdgcn_perm(0u, w, 0x0c020c00u);
+    w13 = __builtin_amdgcn_perm(0u, w, 0x0c030c01u);
+}
+__device__ __forceinline__ int halves_to_bytes(uint32_t w02, uint32_t w13) {
+    return (int)__builtin_amdgcn_perm(w13, w02, 0x06020400u);
+}
+
+// Q3_K super-block b of a 16-row tile in LDS (row r at T + r*rb; 110-byte
+// blocks, only 2-byte aligned), folded for v_mfma_i32_16x16x64_i8.  Lane group
+// g of chunk jc supplies elements 64 jc + 16 g .. + 15 of its row: 32-element
+// range 2 jc + g / 2 (half n = jc / 2, quarter j = 2 (jc & 1) + g / 2),
+// positions l = 16 (g & 1) .. + 15, one 16-element scale group G = 4 jc + g.
+// Its quants are q3 = q2 + 4 h - 4 (q2: bits 2 j .. 2 j + 1 of qs[32 n + l];
+// h: bit 4 n + j of hmask[l]) and w = (sc_G - 32) * q3 lies in [-124, 128]; it
+// is split as w = 64 hi + lo with lo = w & 63 and hi = w >> 6 in [-2, 2], both
+// int8, so isum = 64 D_hi + D_lo is the per-token path's integer sum exactly.
+struct Q3Fold {
+    v4i hi[4], lo[4];
+    float d[4];  // factors of the four rows whose results the lane receives
+};
+
+__device__ __forceinline__ void q3_fold(const uint8_t *T, size_t rb, int b, Q3Fold &o) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const uint8_t *blk = T + (size_t)r * rb + (size_t)b * kQ3KBytes;
+    const uint4 hm = lds_u128_a2(blk + 16 * (g & 1));  // hmask[l], l = 16 (g & 1) .. + 15
+    const uint2 s01 = lds_u64_a2(blk + 96);
+    const uint32_t s2 = lds_u32(blk + 104);
+    const uint32_t hmw[4] = {hm.x, hm.y, hm.z, hm.w};
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        const int n = jc >> 1, j = 2 * (jc & 1) + (g >> 1);
+        const uint4 qv = lds_u128_a2(blk + 32 + 32 * n + 16 * (g & 1));
+        const int sc = q3k_scale(4 * jc + g, s01.x, s01.y, s2);
+        const v2s16 scv = {(short)sc, (short)sc};
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        int hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = ((qw[k] >> (2 * j)) & 0x03030303u) | (((hmw[k] >> (4 * n + j)) & 0x01010101u) << 2);
+            uint32_t q02, q13;
+            bytes_to_halves(q, q02, q13);
+            const v2s16 w02 = (__builtin_bit_cast(v2s16, q02) - (v2s16){4, 4}) * scv;
+            const v2s16 w13 = (__builtin_bit_cast(v2s16, q13) - (v2s16){4, 4}) * scv;
+            hw[k] = halves_to_bytes(__builtin_bit_cast(uint32_t, w02 >> (v2s16){6, 6}),
+                                    __builtin_bit_cast(uint32_t, w13 >> (v2s16){6, 6}));
+            lw[k] = halves_to_bytes(__builtin_bit_cast(uint32_t, w02 & (v2s16){63, 63}),
+                                    __builtin_bit_cast(uint32_t, w13 & (v2s16){63, 63}));
+        }
+        o.hi[jc] = v4i{hw[0], hw[1], hw[2], hw[3]};
+        o.lo[jc] = v4i{lw[0], lw[1], lw[2], lw[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint8_t *blk_i = T + (size_t)(4 * g + i) * rb + (size_t)b * kQ3KBytes;
+        o.d[i] = half_bits_to_float((uint32_t)blk_i[108] | ((uint32_t)blk_i[109] << 8));
+    }
+}
+
+__device__ __forceinline__ void q3_fold_step(const Q3Fold &w, const Q6XB &x, float acc[4]) {
+    v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0};
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        dh = mfma_16x16x64(w.hi[jc], x.x[jc], dh);
+        dl = mfma_16x16x64(w.lo[jc], x.x[jc], dl);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int isum = 64 * dh[i] + dl[i];
+        acc[i] = acc[i] + (w.d[i] * x.xd) * (float)isum;
+    }
+}
+
+// Q5_K super-block b of a 16-row tile in LDS (16-byte aligned 176-byte blocks:
+// d, dmin, Q4_K-packed scales and mins, qh[32], qs[128]), folded as the Q4_K
+// gate/up tile is: lane group g of chunk jc takes nibble g / 2 of qs bytes
+// 32 jc + 16 (g & 1) .. + 15 with bit 2 jc + g / 2 of qh[l] on top (q5 in
+// [0, 31]), sub-block s = 2 jc + g / 2.  w = sc_s * q5 <= 1953 is split as
+// w = 64 hi + lo (lo = w & 63, hi = w >> 6 <= 30); the min term is a third MFMA
+// with m_s broadcast over its sub-block: isum = 64 D_hi + D_lo, msum = D_min.
+struct Q5Fold {
+    v4i hi[4], lo[4];
+    uint32_t mn;          // byte jc: the min of the lane's sub-block in chunk jc
+    float d[4], dmin[4];  // factors of the four rows whose results the lane receives
+};
+
+__device__ __forceinline__ void q5_fold(const uint8_t *T, size_t rb, int b, Q5Fold &o) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const uint8_t *blk = T + (size_t)r * rb + (size_t)b * kQ5KBytes;
+    const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+    const uint4 qh = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * (g & 1));  // qh[l], l = 16 (g & 1) .. + 15
+    uint32_t sc[2], mn[2];
+    q4k_scales_packed(hd, sc, mn);
+    const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+    const uint32_t nsh = 4u * (uint32_t)(g >> 1), bsh = 8u * (uint32_t)(g >> 1);
+    o.mn = 0u;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        const int s = 2 * jc + (g >> 1);
+        const uint32_t sh = 16u * (uint32_t)(jc & 1) + bsh;  // byte 2 (jc & 1) + g / 2 of word jc / 2
+        const uint32_t scs = (sc[jc >> 1] >> sh) & 0xffu, mns = (mn[jc >> 1] >> sh) & 0xffu;
+        const v2u16b scv = {(unsigned short)scs, (unsigned short)scs};
+        const uint4 qv = *reinterpret_cast<const uint4 *>(blk + 48 + 32 * jc + 16 * (g & 1));
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        int hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = ((qw[k] >> nsh) & 0x0f0f0f0fu) | (((qhw[k] >> s) & 0x01010101u) << 4);
+            uint32_t q02, q13;
+            bytes_to_halves(q, q02, q13);
+            const v2u16b w02 = __builtin_bit_cast(v2u16b, q02) * scv, w13 = __builtin_bit_cast(v2u16b, q13) * scv;
+            hw[k] = halves_to_bytes(__builtin_bit_cast(uint32_t, w02 >> (v2u16b){6, 6}),
+                                    __builtin_bit_cast(uint32_t, w13 >> (v2u16b){6, 6}));
+            lw[k] = halves_to_bytes(__builtin_bit_cast(uint32_t, w02 & (v2u16b){63, 63}),
+                                    __builtin_bit_cast(uint32_t, w13 & (v2u16b){63, 63}));
+        }
+        o.hi[jc] = v4i{hw[0], hw[1], hw[2], hw[3]};
+        o.lo[jc] = v4i{lw[0], lw[1], lw[2], lw[3]};
+        o.mn |= mns << (8 * jc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t dm = *reinterpret_cast<const uint32_t *>(T + (size_t)(4 * g + i) * rb + (size_t)b * kQ5KBytes);
+        o.d[i] = half_bits_to_float(dm & 0xffffu);
+        o.dmin[i] = half_bits_to_float(dm >> 16);
+    }
+}
+
+__device__ __forceinline__ void q5_fold_step(const Q5Fold &w, const Q6XB &x, float acc[4], float accm[4]) {
+    v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0}, dn = {0, 0, 0, 0};
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) {
+        dh = mfma_16x16x64(w.hi[jc], x.x[jc], dh);
+        dl = mfma_16x16x64(w.lo[jc], x.x[jc], dl);
+        const int m4 = splat_byte_of(w.mn, jc);
+        dn = mfma_16x16x64(v4i{m4, m4, m4, m4}, x.x[jc], dn);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int isum = 64 * dh[i] + dl[i];
+        const float dd = w.d[i] * x.xd;
+        const float dm = w.dmin[i] * x.xd;
+        acc[i] = acc[i] + dd * (float)isum;
+        accm[i] = accm[i] + dm * (float)dn[i];
+    }
+}
+
+// -- gate/up + SwiGLU for Q3_K rows (OLMoE in its Q3_K_M form) --------------------
+// grid (n_ff / 32, max units), block 256: wave w takes rows [32 x + 16 (w % 2), +16)
+// of gate (w < 2) or up (w >= 2).  The 32 rows of each matrix are copied into
+// LDS in one burst (110-byte blocks, 2-byte aligned, read with alignbyte); per
+// super-block each wave folds its rows once (q3_fold) and runs them against
+// every token chunk of the unit.  The gate waves hand their values to the up
+// waves through LDS, which form h.
+template <int NB>
+__global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
+    constexpr int kRowBytes = NB * kQ3KBytes;
+    constexpr int kTileBytes = 2 * kWaveRows * kRowBytes;  // 32 rows of one matrix
+    static_assert(kRowBytes % 16 == 0, "Q3_K rows of 8 blocks are 880 bytes: tiles start 16-byte aligned");
+    __shared__ __align__(16) uint8_t tile[2][kTileBytes];
+    __shared__ float gx[2][kChunks][4][64];  // gate values: [row tile][chunk][row i][lane]
+    Unit w;
+    if (!load_unit(a, blockIdx.y, w)) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int m = wave >> 1, rt = wave & 1;
+    const int row0 = blockIdx.x * 2 * kWaveRows;
+    {
+        // each matrix's 32 rows split over its two waves
+        const uint8_t *src = (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)row0 * kRowBytes;
+        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
+        for (int ck = rt; ck < kChunksTotal; ck += 2)
+            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile[m] + ck * 1024, src + (size_t)ck * 1024);
+        lds_dma_wait();
+    }
+    __syncthreads();
+    const uint8_t *T = tile[m] + rt * kWaveRows * kRowBytes;
+    const int nch = (w.n + 15) >> 4;
+    const Q8L *q8x = reinterpret_cast<const Q8L *>(a.q8x);
+    auto x_of = [&](int ch, int b) -> const Q8L & {
+        return q8x[(size_t)a.ptok[w.p0 + min(ch * 16 + c, w.n - 1)] * NB + b];
+    };
+    float acc[kChunks][4];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
+#pragma unroll 1
+    for (int b = 0; b < NB; ++b) {
+        Q3Fold f;
+        q3_fold(T, kRowBytes, b, f);
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch) {
+            if (ch >= nch) break;
+            Q6XB xc;
+            q6_load_xb(x_of(ch, b), xc);
+            q3_fold_step(f, xc, acc[ch]);
+        }
+    }
+    if (m == 0) {
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gx[rt][ch][i][lane] = acc[ch][i];
+    }
+    __syncthreads();
+    if (m == 0) return;
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+        const int idx = ch * 16 + c;
+        if (ch < nch && idx < w.n) {
+            float hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float g = gx[rt][ch][i][lane], uu = acc[ch][i];
+                hv[i] = g / (1.0f + expf(-g)) * uu;
+            }
+            *reinterpret_cast<float4 *>(a.hbuf + (size_t)(w.p0 + idx) * a.n_ff + row0 + rt * kWaveRows + 4 * q) =
+                make_float4(hv[0], hv[1], hv[2], hv[3]);
+        }
+    }
+}
+
 // grid (n_embd / 64, max units), block 256: as pf_down_kernel for Q6_K rows,
 // super-block major: each super-block of the wave's 16 rows is folded once,
 // then run against every token chunk of the unit.  Three workgroups per CU
@@ -464,6 +690,82 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
             const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
             *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
                 make_float4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
+        }
+    }
+}
+
+// grid (n_embd / 64, max units), block 256: Q5_K down rows folded as the Q6_K
+// ones are (each super-block of the wave's 16 rows folded once, then run against
+// every token chunk of the unit); TS = Q6_K: the shared expert's Q6_K rows
+// beside them (Qwen3.5), a unit of which takes the Q6_K fold.
+template <int NBH, int TS>
+__global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
+    constexpr int kRowBytesD = NBH * kQ5KBytes, kRowBytesS = NBH * QType<TS>::bytes;
+    constexpr int kTileBytes = kDnRows * (kRowBytesD > kRowBytesS ? kRowBytesD : kRowBytesS);
+    static_assert(TS == kTypeQ5K || TS == kTypeQ6K, "the shared expert's down rows are Q5_K or Q6_K");
+    __shared__ __align__(16) uint8_t tile[kTileBytes];
+    Unit w;
+    if (!load_unit(a, blockIdx.y, w)) return;
+    const bool shx = TS != kTypeQ5K && a.sh && w.e == a.n_ids;  // the shared expert's Q6_K rows
+    const int rbytes = shx ? kRowBytesS : kRowBytesD, tbytes = kDnRows * rbytes;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int rt0 = blockIdx.x * kDnRows;
+    {
+        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * rbytes;
+        const int nck = (tbytes + 1023) / 1024;
+        for (int ck = wave; ck < nck; ck += 4)
+            if (ck * 1024 + 16 * lane < tbytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
+        lds_dma_wait();
+    }
+    __syncthreads();
+    const uint8_t *T = tile + wave * kWaveRows * rbytes;
+    const int nch = (w.n + 15) >> 4;
+    const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
+    auto x_of = [&](int ch, int b) -> const Q8L & {
+        return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
+    };
+    float acc[kChunks][4], accm[kChunks][4];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ch][i] = accm[ch][i] = 0.0f;
+    if (shx) {
+        if constexpr (TS == kTypeQ6K) {
+#pragma unroll 1
+            for (int b = 0; b < NBH; ++b) {
+                Q6Fold f;
+                q6_fold(T, kRowBytesS, b, f);
+#pragma unroll
+                for (int ch = 0; ch < kChunks; ++ch) {
+                    if (ch >= nch) break;
+                    Q6XB xc;
+                    q6_load_xb(x_of(ch, b), xc);
+                    q6_fold_step(f, xc, acc[ch]);
+                }
+            }
+        }
+    } else {
+#pragma unroll 1
+        for (int b = 0; b < NBH; ++b) {
+            Q5Fold f;
+            q5_fold(T, kRowBytesD, b, f);
+#pragma unroll
+            for (int ch = 0; ch < kChunks; ++ch) {
+                if (ch >= nch) break;
+                Q6XB xc;
+                q6_load_xb(x_of(ch, b), xc);
+                q5_fold_step(f, xc, acc[ch], accm[ch]);
+            }
+        }
+    }
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+        const int idx = ch * 16 + c;
+        if (ch < nch && idx < w.n) {
+            const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
+            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
+                make_float4(acc[ch][0] - accm[ch][0], acc[ch][1] - accm[ch][1], acc[ch][2] - accm[ch][2],
+                            acc[ch][3] - accm[ch][3]);  // accm stays 0 for Q6_K rows
         }
     }
 }
@@ -523,21 +825,31 @@ hipError_t launch_prefill_groups(const BatchedArgs &a, hipStream_t s) {
     const int nbh = a.n_ff / QK;
     if (a.n_embd != 2048 || a.n_ff % kGuRows || a.n_embd % kDnRows || nbh > 4 || a.max_units < 1)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_gateup_kernel<8>, dim3(a.n_ff / kGuRows, a.max_units), dim3(256), 0, s, a);
+    if (a.gu_type == kTypeQ4K)
+        hipLaunchKernelGGL(pf_gateup_kernel<8>, dim3(a.n_ff / kGuRows, a.max_units), dim3(256), 0, s, a);
+    else if (a.gu_type == kTypeQ3K)
+        hipLaunchKernelGGL(pf_gateup_q3_kernel<8>, dim3(a.n_ff / kGuRows, a.max_units), dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(pf_quant_h_kernel, dim3(a.M * (a.k + a.sh)), dim3(64 * nbh), 0, s, a);
     const dim3 dg(a.n_embd / kDnRows, a.max_units);
-#define HOARD_DOWN(T, N)                                                         \
-    if (a.d_type == T && nbh == N) {                                             \
-        hipLaunchKernelGGL((pf_down_kernel<T, N>), dg, dim3(256), 0, s, a);     \
+    const int sd = a.sh ? a.sh_d_type : a.d_type;
+// one kernel instance per (routed down type, super-blocks per row, shared down type)
+#define HOARD_DOWN(T, N, TS, K)                                          \
+    if (a.d_type == T && nbh == N && sd == TS) {                         \
+        hipLaunchKernelGGL((K), dg, dim3(256), 0, s, a);                 \
     } else
-    if (a.d_type == kTypeQ6K && nbh == 3) {
-        hipLaunchKernelGGL((pf_down_q6_kernel<3>), dg, dim3(256), 0, s, a);
-    } else if (a.d_type == kTypeQ6K && nbh == 2) {
-        hipLaunchKernelGGL((pf_down_q6_kernel<2>), dg, dim3(256), 0, s, a);
-    } else if (a.d_type == kTypeQ6K && nbh == 4) {
-        hipLaunchKernelGGL((pf_down_q6_kernel<4>), dg, dim3(256), 0, s, a);
-    } else
-    HOARD_DOWN(kTypeQ4K, 4) HOARD_DOWN(kTypeQ4K, 3) HOARD_DOWN(kTypeQ4K, 2) { return hipErrorInvalidValue; }
+    HOARD_DOWN(kTypeQ6K, 3, kTypeQ6K, pf_down_q6_kernel<3>)
+    HOARD_DOWN(kTypeQ6K, 2, kTypeQ6K, pf_down_q6_kernel<2>)
+    HOARD_DOWN(kTypeQ6K, 4, kTypeQ6K, pf_down_q6_kernel<4>)
+    HOARD_DOWN(kTypeQ4K, 4, kTypeQ4K, pf_down_q4_kernel<4>)
+    HOARD_DOWN(kTypeQ4K, 3, kTypeQ4K, pf_down_q4_kernel<3>)
+    HOARD_DOWN(kTypeQ4K, 2, kTypeQ4K, pf_down_q4_kernel<2>)
+    HOARD_DOWN(kTypeQ5K, 4, kTypeQ5K, (pf_down_q5_kernel<4, kTypeQ5K>))
+    HOARD_DOWN(kTypeQ5K, 2, kTypeQ5K, (pf_down_q5_kernel<2, kTypeQ5K>))
+    HOARD_DOWN(kTypeQ5K, 2, kTypeQ6K, (pf_down_q5_kernel<2, kTypeQ6K>)) {
+        return hipErrorInvalidValue;
+    }
 #undef HOARD_DOWN
     hipLaunchKernelGGL(pf_combine_kernel, dim3((a.n_embd + 1023) / 1024, a.M), dim3(256), 0, s, a);
     return hipGetLastError();

@@ -146,8 +146,9 @@ int hoard_moe_decode(hoard_moe *h, int layer_begin, int layer_end, float *x_dev,
    shared expert (n_ff_shexp > 0) must have the routed experts' n_ff and types
    (or a Q6_K down beside Q5_K routed down rows, n_ff 512) and n_used <= 15: it
    runs as one more expert taken by every token, gated by
-   sigmoid(ffn_gate_inp_shexp . fx) as in hoard_moe_layer.  Q5_K down rows take
-   M <= 32 (more returns HOARD_ERR_UNSUPPORTED). */
+   sigmoid(ffn_gate_inp_shexp . fx) as in hoard_moe_layer.  Expert types: Q4_K
+   or Q3_K gate/up (both the same) with Q4_K, Q5_K or Q6_K down rows, n_ff of
+   512, 768 (not with Q5_K) or 1024, n_embd 2048. */
 int hoard_moe_forward_batched(hoard_moe *h, int layer, int M, const float *fx_dev, const float *res_dev,
                               float *out_dev, int32_t *sel_dev, float *w_dev, void *stream);
 

@@ -6,6 +6,10 @@ Each token's result must be the single-token path's bit for bit (the folded MFMA
 operands give the per-token integer sub-block sums exactly) and match the oracle's
 batched layer (every token routed and computed independently) to the parity bar;
 the per-expert histogram must count the call's (token, slot) pairs.
+
+Shapes: Qwen3-30B (Q4_K gate/up, Q6_K down), OLMoE (all Q4_K), Qwen3-Next (a
+shared expert), Qwen3.5 (Q5_K routed down rows beside a Q6_K shared expert) and
+OLMoE in its Q3_K_M form (Q3_K gate/up, Q5_K down).
 """
 import numpy as np
 import pytest
@@ -19,7 +23,8 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.OLMOE, W.QWEN3_NEXT], ids=lambda s: s.name)
+@pytest.fixture(scope="module", params=[W.QWEN3_30B, W.OLMOE, W.QWEN3_NEXT, W.QWEN35, W.OLMOE_Q3],
+                ids=lambda s: s.name)
 def stage(request):
     from hoard_amd.runtime import MoEStage
     shape = request.param
