@@ -603,15 +603,16 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
         for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
 #pragma unroll 1
     for (int b = 0; b < NB; ++b) {
+        // every chunk's activation operands in flight before the fold, which covers them
+        Q6XB xc[kChunks];
+#pragma unroll
+        for (int ch = 0; ch < kChunks; ++ch)
+            if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
         Q3Fold f;
         q3_fold(T, kRowBytes, b, f);
 #pragma unroll
-        for (int ch = 0; ch < kChunks; ++ch) {
-            if (ch >= nch) break;
-            Q6XB xc;
-            q6_load_xb(x_of(ch, b), xc);
-            q3_fold_step(f, xc, acc[ch]);
-        }
+        for (int ch = 0; ch < kChunks; ++ch)
+            if (ch < nch) q3_fold_step(f, xc[ch], acc[ch]);
     }
     if (m == 0) {
 #pragma unroll
@@ -733,29 +734,29 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
         if constexpr (TS == kTypeQ6K) {
 #pragma unroll 1
             for (int b = 0; b < NBH; ++b) {
+                Q6XB xc[kChunks];
+#pragma unroll
+                for (int ch = 0; ch < kChunks; ++ch)
+                    if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
                 Q6Fold f;
                 q6_fold(T, kRowBytesS, b, f);
 #pragma unroll
-                for (int ch = 0; ch < kChunks; ++ch) {
-                    if (ch >= nch) break;
-                    Q6XB xc;
-                    q6_load_xb(x_of(ch, b), xc);
-                    q6_fold_step(f, xc, acc[ch]);
-                }
+                for (int ch = 0; ch < kChunks; ++ch)
+                    if (ch < nch) q6_fold_step(f, xc[ch], acc[ch]);
             }
         }
     } else {
 #pragma unroll 1
         for (int b = 0; b < NBH; ++b) {
+            Q6XB xc[kChunks];
+#pragma unroll
+            for (int ch = 0; ch < kChunks; ++ch)
+                if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
             Q5Fold f;
             q5_fold(T, kRowBytesD, b, f);
 #pragma unroll
-            for (int ch = 0; ch < kChunks; ++ch) {
-                if (ch >= nch) break;
-                Q6XB xc;
-                q6_load_xb(x_of(ch, b), xc);
-                q5_fold_step(f, xc, acc[ch], accm[ch]);
-            }
+            for (int ch = 0; ch < kChunks; ++ch)
+                if (ch < nch) q5_fold_step(f, xc[ch], acc[ch], accm[ch]);
         }
     }
 #pragma unroll
