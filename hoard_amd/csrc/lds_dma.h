@@ -26,14 +26,6 @@ __device__ __forceinline__ void dma_lanes(uint8_t *dst, const uint8_t *g) {
                  : "memory", "m0");
 }
 
-// dma_lanes with the non-temporal (streaming) cache policy.
-__device__ __forceinline__ void dma_lanes_nt(uint8_t *dst, const uint8_t *g) {
-    const lds_void *lp = (const lds_void *)dst;
-    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lp);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds), "v"(g)
-                 : "memory", "m0");
-}
-
 // The contiguous form: lane l copies src[16 l, 16 l + 16).
 __device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src) {
     dma_lanes(dst, src + (threadIdx.x & 63) * 16);
