@@ -220,6 +220,10 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
         __syncthreads();  // every wave's copies of x(b) landed, and x(b - 1) is read
         Q4Fold t;
         q4_fold(raw, t);
+        // the fold is done before the next loads issue
+        asm volatile("" ::"v"(t.hi[0]), "v"(t.hi[1]), "v"(t.hi[2]), "v"(t.hi[3]), "v"(t.lo[0]), "v"(t.lo[1]),
+                     "v"(t.lo[2]), "v"(t.lo[3])
+                     : "memory");
         if (b + 1 < NB) {
             q4_raw_load(W, rb, b + 1, raw);
             stage_x(b + 1, (b + 1) & 1);
@@ -581,6 +585,10 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * 2 * kWaveRows;
+    // the lane's token of each chunk, read once, while the tile lands
+    int tok[kChunks];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) tok[ch] = a.ptok[w.p0 + min(ch * 16 + c, w.n - 1)];
     {
         // each matrix's 32 rows split over its two waves
         const uint8_t *src = (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)row0 * kRowBytes;
@@ -593,9 +601,7 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     const uint8_t *T = tile[m] + rt * kWaveRows * kRowBytes;
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8x = reinterpret_cast<const Q8L *>(a.q8x);
-    auto x_of = [&](int ch, int b) -> const Q8L & {
-        return q8x[(size_t)a.ptok[w.p0 + min(ch * 16 + c, w.n - 1)] * NB + b];
-    };
+    auto x_of = [&](int ch, int b) -> const Q8L & { return q8x[(size_t)tok[ch] * NB + b]; };
     float acc[kChunks][4];
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch)
@@ -638,21 +644,35 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     }
 }
 
-// grid (n_embd / 64, max units), block 256: as pf_down_kernel for Q6_K rows,
+// grid (n_embd / 64, max units), block 256: as pf_down_q4_kernel for Q6_K rows,
 // super-block major: each super-block of the wave's 16 rows is folded once,
-// then run against every token chunk of the unit.  Three workgroups per CU
-// (148 VGPRs, no prefetch of the next chunk's operands): 227 against 231 us
-// a layer at M = 512 for two workgroups with the prefetch.
+// then run against every token chunk of the unit, the next chunk's activation
+// operands in flight meanwhile.  Three workgroups per CU (166 VGPRs).
 template <int NBH>
 __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     constexpr int kRowBytes = NBH * kQ6KBytes;
     constexpr int kTileBytes = kDnRows * kRowBytes;
     static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
     __shared__ __align__(16) uint8_t tile[kTileBytes];
+    __shared__ int yrow[kUnitTokens];  // y row (token * slots + slot) of each of the unit's pairs
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
+    const int nch = (w.n + 15) >> 4;
+    const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
+    auto x_of = [&](int ch, int b) -> const Q8L & {
+        return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
+    };
+    // Chunk ch of a super-block takes its activation operands from x[ch % 2]:
+    // super-block 0's first two are issued ahead of the tile burst, a later
+    // super-block's chunk 0 before its fold, and each later chunk's while the
+    // one before it computes.
+    static_assert(kChunks == 4, "four chunks, two operand sets");
+    Q6XB x0, x1;
+    // the pairs' places, read while the tile lands
+    const int tid = threadIdx.x;
+    const int pt = tid < w.n ? a.ptok[w.p0 + tid] : 0, ps = tid < w.n ? a.pslot[w.p0 + tid] : 0;
     {
         const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * kRowBytes;
         constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
@@ -660,13 +680,9 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
             if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
         lds_dma_wait();
     }
+    if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
     __syncthreads();
     const uint8_t *T = tile + wave * kWaveRows * kRowBytes;
-    const int nch = (w.n + 15) >> 4;
-    const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
-    auto x_of = [&](int ch, int b) -> const Q8L & {
-        return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
-    };
     float acc[kChunks][4];
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch)
@@ -674,22 +690,26 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
         for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
 #pragma unroll 1
     for (int b = 0; b < NBH; ++b) {
+        q6_load_xb(x_of(0, b), x0);
         Q6Fold f;
         q6_fold(T, kRowBytes, b, f);
-#pragma unroll
-        for (int ch = 0; ch < kChunks; ++ch) {
-            if (ch >= nch) break;
-            Q6XB xc;
-            q6_load_xb(x_of(ch, b), xc);
-            q6_fold_step(f, xc, acc[ch]);
+        if (nch > 1) q6_load_xb(x_of(1, b), x1);
+        q6_fold_step(f, x0, acc[0]);
+        if (nch > 1) {
+            if (nch > 2) q6_load_xb(x_of(2, b), x0);
+            q6_fold_step(f, x1, acc[1]);
+            if (nch > 2) {
+                if (nch > 3) q6_load_xb(x_of(3, b), x1);
+                q6_fold_step(f, x0, acc[2]);
+                if (nch > 3) q6_fold_step(f, x1, acc[3]);
+            }
         }
     }
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch) {
         const int idx = ch * 16 + c;
         if (ch < nch && idx < w.n) {
-            const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
-            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
+            *reinterpret_cast<float4 *>(a.ybuf + (size_t)yrow[idx] * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
                 make_float4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
         }
     }
@@ -705,12 +725,16 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     constexpr int kTileBytes = kDnRows * (kRowBytesD > kRowBytesS ? kRowBytesD : kRowBytesS);
     static_assert(TS == kTypeQ5K || TS == kTypeQ6K, "the shared expert's down rows are Q5_K or Q6_K");
     __shared__ __align__(16) uint8_t tile[kTileBytes];
+    __shared__ int yrow[kUnitTokens];  // y row (token * slots + slot) of each of the unit's pairs
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const bool shx = TS != kTypeQ5K && a.sh && w.e == a.n_ids;  // the shared expert's Q6_K rows
     const int rbytes = shx ? kRowBytesS : kRowBytesD, tbytes = kDnRows * rbytes;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
+    // the pairs' places, read while the tile lands
+    const int tid = threadIdx.x;
+    const int pt = tid < w.n ? a.ptok[w.p0 + tid] : 0, ps = tid < w.n ? a.pslot[w.p0 + tid] : 0;
     {
         const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * rbytes;
         const int nck = (tbytes + 1023) / 1024;
@@ -718,6 +742,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
             if (ck * 1024 + 16 * lane < tbytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
         lds_dma_wait();
     }
+    if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
     __syncthreads();
     const uint8_t *T = tile + wave * kWaveRows * rbytes;
     const int nch = (w.n + 15) >> 4;
@@ -763,8 +788,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     for (int ch = 0; ch < kChunks; ++ch) {
         const int idx = ch * 16 + c;
         if (ch < nch && idx < w.n) {
-            const int pos = w.p0 + idx, t = a.ptok[pos], j = a.pslot[pos];
-            *reinterpret_cast<float4 *>(a.ybuf + ((size_t)t * (a.k + a.sh) + j) * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
+            *reinterpret_cast<float4 *>(a.ybuf + (size_t)yrow[idx] * a.n_embd + rt0 + wave * kWaveRows + 4 * q) =
                 make_float4(acc[ch][0] - accm[ch][0], acc[ch][1] - accm[ch][1], acc[ch][2] - accm[ch][2],
                             acc[ch][3] - accm[ch][3]);  // accm stays 0 for Q6_K rows
         }
