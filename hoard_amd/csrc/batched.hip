@@ -178,6 +178,7 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
         if (lane == 63) {
             a.n_unique[0] = ig - a.sh;  // routed experts used
             a.n_units[0] = iu;
+            g.total = ip;  // pairs in all groups
         }
     }
 }
@@ -190,7 +191,7 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
 // expert comes from chunks of at most 32 tokens taken in token order: a pair's
 // place is its expert's running base plus the tokens of its chunk before it
 // that select the same expert (a token joins a group at most once).
-__device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
+__device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe, int *sorted) {
     const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids + a.sh, k = a.k + a.sh, P = a.M * k;
     for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
     __syncthreads();
@@ -212,8 +213,7 @@ __device__ void group_large(const BatchedArgs &a, GroupLds &g, const int *pe) {
             if (e < 0) continue;
             const int t = p / k;
             const int pos = g.base[e] + __popc(g.mask[e] & ((1u << (t - t0)) - 1u));
-            a.ptok[pos] = t;
-            a.pslot[pos] = p - t * k;
+            sorted[pos] = t | (p - t * k) << 16;
         }
         __syncthreads();
         for (int e = tid; e < E; e += nt) g.base[e] += __popc(g.mask[e]);
@@ -307,42 +307,45 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 }
 
 // -- prefill-sized routing: tiled router GEMM, then tails, then the grouping -----
-// Logits of 16 experts x 16 tokens per workgroup of 256 threads.  Thread
+// Logits of 16 experts x 16 tokens per workgroup of 512 threads.  Thread
 // (group q = tid / 32, lane l = tid % 32) holds accumulator l of ggml's x86 f32
-// dot (elements 32 i + l, i ascending) for 4 experts x 8 tokens: the rows and
+// dot (elements 32 i + l, i ascending) for 4 experts x 4 tokens: the rows and
 // tokens pass through LDS 512 elements at a time, every element read once per
-// 32 dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
+// 16 dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
 // which fold them in ggml's order, so every logit is the single-token router's.
-// Each K step costs a wait and a barrier besides its dots: 512-element steps
-// (4 of them) took 3.5 us less per launch than 256-element ones (8), and
-// 1024-element ones without a second buffer 1.6 us more than 512 at M = 512.
+// One workgroup per CU: eight waves (two per SIMD) took 4 us less per launch
+// than four waves with 4 x 8 dots each, sixteen waves with 2 x 4 each 1 us
+// more than eight.  Each K step costs a wait and a barrier besides its dots:
+// 512-element steps (4 of them) took 3.5 us less per launch than 256-element
+// ones (8), and 1024-element ones without a second buffer 1.6 us more than
+// 512 at M = 512 (four waves).
 constexpr int kTileE = 16, kTileT = 16, kTileK = 512;
 
 // K steps in LDS: the current one and the next in flight (four buffers, three
 // steps in flight, measured the same: once one step is prefetched the dots and
 // the per-step barrier set the pace).  128 KB of LDS: one workgroup per CU.
 constexpr int kGemmBufs = 2;
-__global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
+__global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
     __shared__ __align__(16) float wl[kGemmBufs][kTileE][kTileK];
     __shared__ __align__(16) float xl[kGemmBufs][kTileT][kTileK];
     constexpr int n = kRouteN, kSteps = n / kTileK;
     static_assert(kSteps >= kGemmBufs, "the ring is filled before the first step");
-    constexpr int kRowsPerWave = (kTileE + kTileT) / 4 * (kTileK / 256);  // 1 KB copies each wave issues per step
+    constexpr int kRowsPerWave = (kTileE + kTileT) / 8 * (kTileK / 256);  // 1 KB copies each wave issues per step
     const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = tid >> 6, lane = tid & 63;
     const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
-    const int re = (q & 3) * 4, rt = (q >> 2) * 8;  // this group's 4 experts and 8 tokens within the tile
-    float acc[4][8];
+    const int re = (q & 3) * 4, rt = (q >> 2) * 4;  // this group's 4 experts and 4 tokens within the tile
+    float acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
     // 32 rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
     // rows past the end repeat the last one (their results are not stored).  The
     // next steps' rows are in flight while the current one is dotted.  Expert
     // row E (with a shared expert) is the shared expert's gate row.
     const int er = a.E + a.sh;
     auto issue = [&](int k0, int buf) {
-        for (int r = wave; r < kTileE + kTileT; r += 4) {
+        for (int r = wave; r < kTileE + kTileT; r += 8) {
             const int row = min(e0 + r, er - 1);
             const float *src = r < kTileE ? (row < a.E ? a.router + (size_t)row * n : a.sh_gate_inp)
                                           : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
@@ -372,22 +375,22 @@ __global__ __launch_bounds__(256) void route_gemm_kernel(BatchedArgs a) {
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < kTileK / 32; ++i) {
-            float wv[4], xv[8];
+            float wv[4], xv[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) wv[r] = wl[buf][re + r][32 * i + l];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) xv[t] = xl[buf][rt + t][32 * i + l];
+            for (int t = 0; t < 4; ++t) xv[t] = xl[buf][rt + t][32 * i + l];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
+                for (int t = 0; t < 4; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
         }
         __syncthreads();  // every wave is done with this buffer before it is refilled
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < 4; ++t) {
             float v = acc[r][t];
             v = v + __shfl_xor(v, 16);  // accumulators l and l + 16
             v = row16_ggml_fold(v);
@@ -490,8 +493,9 @@ __global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
 // within the expert's run, so a pair's place is its expert's first place, its
 // chunk's start and the tokens of its chunk before it that select the expert.
 // Three barriers in all, where the chunk loop takes four per chunk.
-constexpr int kGroupChunkWords = 4096;
-__device__ void group_large_chunks(const BatchedArgs &a, GroupLds &g, const int *pe, unsigned *cm, int *cb) {
+constexpr int kGroupChunkWords = 8448;  // 16 chunks of 32 tokens x 528 experts
+__device__ void group_large_chunks(const BatchedArgs &a, GroupLds &g, const int *pe, unsigned *cm, int *cb,
+                                   int *sorted) {
     const int tid = threadIdx.x, nt = blockDim.x, E = a.n_ids + a.sh, k = a.k + a.sh, P = a.M * k;
     const int nch = (a.M + 31) >> 5;
     for (int e = tid; e < E; e += nt) g.cnt[e] = 0u;
@@ -522,23 +526,32 @@ __device__ void group_large_chunks(const BatchedArgs &a, GroupLds &g, const int 
         if (e < 0) continue;
         const int t = p / k, c = t >> 5;
         const int pos = g.base[e] + cb[c * E + e] + __popc(cm[c * E + e] & ((1u << (t & 31)) - 1u));
-        a.ptok[pos] = t;
-        a.pslot[pos] = p - t * k;
+        sorted[pos] = t | (p - t * k) << 16;
     }
 }
 
+// The pairs are sorted into LDS (token | slot << 16 at each sorted place) and
+// copied out in order: scattered 4-byte stores from one CU took 3 us at 4,096
+// pairs, the copy a fraction of that.
 __global__ __launch_bounds__(1024) void group_kernel(BatchedArgs a) {
     __shared__ GroupLds g;
     __shared__ int pe[kBatchedMaxTokensLarge * kMaxK];
+    __shared__ int sorted[kBatchedMaxTokensLarge * kMaxK];
     __shared__ unsigned cm[kGroupChunkWords];
     __shared__ int cb[kGroupChunkWords];
     const int P = a.M * (a.k + a.sh);
     for (int p = threadIdx.x; p < P; p += blockDim.x) pe[p] = a.pexp[p];
     __syncthreads();
     if (((a.M + 31) >> 5) * (a.n_ids + a.sh) <= kGroupChunkWords)
-        group_large_chunks(a, g, pe, cm, cb);
+        group_large_chunks(a, g, pe, cm, cb, sorted);
     else
-        group_large(a, g, pe);
+        group_large(a, g, pe, sorted);
+    __syncthreads();
+    for (int i = threadIdx.x; i < g.total; i += blockDim.x) {
+        const int v = sorted[i];
+        a.ptok[i] = v & 0xffff;
+        a.pslot[i] = v >> 16;
+    }
 }
 
 // -- caller ids: Q8_K of fx (workgroups 0..M-1, a wave per block) and the
@@ -890,7 +903,7 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.M > kMaxTok) {
         hipLaunchKernelGGL(route_gemm_kernel, dim3((a.E + a.sh + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT),
-                           dim3(256), 0, s, a);
+                           dim3(512), 0, s, a);
         hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(512), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
