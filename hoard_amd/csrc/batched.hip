@@ -319,12 +319,15 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 // 512-element steps (4 of them) took 3.5 us less per launch than 256-element
 // ones (8), and 1024-element ones without a second buffer 1.6 us more than
 // 512 at M = 512 (four waves).
-constexpr int kTileE = 16, kTileT = 16, kTileK = 512;
+constexpr int kTileE = 16, kTileT = 16;
 
 // K steps in LDS: the current one and the next in flight (four buffers, three
 // steps in flight, measured the same: once one step is prefetched the dots and
-// the per-step barrier set the pace).  128 KB of LDS: one workgroup per CU.
+// the per-step barrier set the pace).  kTileK = 512: 128 KB of LDS, one
+// workgroup per CU; 256: 64 KB, two a CU, for grids of more tiles than CUs
+// (512 experts at 128 and 512 tokens: 49.5 against 2 x 12 us per launch).
 constexpr int kGemmBufs = 2;
+template <int kTileK>
 __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
     __shared__ __align__(16) float wl[kGemmBufs][kTileE][kTileK];
     __shared__ __align__(16) float xl[kGemmBufs][kTileT][kTileK];
@@ -902,8 +905,11 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
         return hipErrorInvalidValue;
     if (a.M > kMaxTok) {
-        hipLaunchKernelGGL(route_gemm_kernel, dim3((a.E + a.sh + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT),
-                           dim3(512), 0, s, a);
+        const dim3 rg((a.E + a.sh + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT);
+        if (rg.x * rg.y > 256)  // more tiles than CUs: two workgroups a CU
+            hipLaunchKernelGGL(route_gemm_kernel<256>, rg, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL(route_gemm_kernel<512>, rg, dim3(512), 0, s, a);
         hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(512), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
