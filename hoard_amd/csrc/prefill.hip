@@ -280,16 +280,12 @@ __global__ __launch_bounds__(256) void pf_down_q4_kernel(BatchedArgs a) {
     if (!load_unit(a, blockIdx.y, w)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
-    {
-        // the burst split over the four waves, 1 KB chunks each
-        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * kRowBytes;
-        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
-        for (int ck = wave; ck < kChunksTotal; ck += 4)
-            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
-        lds_dma_wait();
-    }
-    __syncthreads();
-    const uint8_t *T = tile + wave * kWaveRows * kRowBytes;
+    // each wave copies its own 16 rows and waits for them alone
+    constexpr int kWaveBytes = kWaveRows * kRowBytes;
+    static_assert(kWaveBytes % 16 == 0, "a wave's rows copy in 16-byte units");
+    uint8_t *T = tile + wave * kWaveBytes;
+    dma_wave_copy_nt(T, batched_down(a, w.e) + (size_t)(rt0 + wave * kWaveRows) * kRowBytes, kWaveBytes);
+    lds_dma_wait();
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
     // (chunk, block) steps with the next step's activation operands loaded
@@ -589,16 +585,12 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     int tok[kChunks];
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch) tok[ch] = a.ptok[w.p0 + min(ch * 16 + c, w.n - 1)];
-    {
-        // each matrix's 32 rows split over its two waves
-        const uint8_t *src = (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)row0 * kRowBytes;
-        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
-        for (int ck = rt; ck < kChunksTotal; ck += 2)
-            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile[m] + ck * 1024, src + (size_t)ck * 1024);
-        lds_dma_wait();
-    }
-    __syncthreads();
-    const uint8_t *T = tile[m] + rt * kWaveRows * kRowBytes;
+    // each wave copies its own 16 rows and waits for them alone
+    constexpr int kWaveBytes = kWaveRows * kRowBytes;
+    uint8_t *T = tile[m] + rt * kWaveBytes;
+    dma_wave_copy_nt(T, (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)(row0 + rt * kWaveRows) * kRowBytes,
+                     kWaveBytes);
+    lds_dma_wait();
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8x = reinterpret_cast<const Q8L *>(a.q8x);
     auto x_of = [&](int ch, int b) -> const Q8L & { return q8x[(size_t)tok[ch] * NB + b]; };
@@ -665,24 +657,21 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
         return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
     };
     // Chunk ch of a super-block takes its activation operands from x[ch % 2]:
-    // super-block 0's first two are issued ahead of the tile burst, a later
-    // super-block's chunk 0 before its fold, and each later chunk's while the
-    // one before it computes.
+    // chunk 0's are loaded before the fold, each later chunk's while the one
+    // before it computes.
     static_assert(kChunks == 4, "four chunks, two operand sets");
     Q6XB x0, x1;
     // the pairs' places, read while the tile lands
     const int tid = threadIdx.x;
     const int pt = tid < w.n ? a.ptok[w.p0 + tid] : 0, ps = tid < w.n ? a.pslot[w.p0 + tid] : 0;
-    {
-        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * kRowBytes;
-        constexpr int kChunksTotal = (kTileBytes + 1023) / 1024;
-        for (int ck = wave; ck < kChunksTotal; ck += 4)
-            if (ck * 1024 + 16 * lane < kTileBytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
-        lds_dma_wait();
-    }
+    // each wave copies its own 16 rows and waits for them alone: no barrier
+    // between the copies and the folds
+    constexpr int kWaveBytes = kWaveRows * kRowBytes;
+    static_assert(kWaveBytes % 16 == 0, "a wave's rows copy in 16-byte units");
+    uint8_t *T = tile + wave * kWaveBytes;
+    dma_wave_copy_nt(T, batched_down(a, w.e) + (size_t)(rt0 + wave * kWaveRows) * kRowBytes, kWaveBytes);
+    lds_dma_wait();
     if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
-    __syncthreads();
-    const uint8_t *T = tile + wave * kWaveRows * kRowBytes;
     float acc[kChunks][4];
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch)
@@ -705,6 +694,7 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
             }
         }
     }
+    __syncthreads();  // yrow is written
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch) {
         const int idx = ch * 16 + c;
@@ -729,22 +719,18 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const bool shx = TS != kTypeQ5K && a.sh && w.e == a.n_ids;  // the shared expert's Q6_K rows
-    const int rbytes = shx ? kRowBytesS : kRowBytesD, tbytes = kDnRows * rbytes;
+    const int rbytes = shx ? kRowBytesS : kRowBytesD;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
     // the pairs' places, read while the tile lands
     const int tid = threadIdx.x;
     const int pt = tid < w.n ? a.ptok[w.p0 + tid] : 0, ps = tid < w.n ? a.pslot[w.p0 + tid] : 0;
-    {
-        const uint8_t *src = batched_down(a, w.e) + (size_t)rt0 * rbytes;
-        const int nck = (tbytes + 1023) / 1024;
-        for (int ck = wave; ck < nck; ck += 4)
-            if (ck * 1024 + 16 * lane < tbytes) dma_chunk_nt(tile + ck * 1024, src + (size_t)ck * 1024);
-        lds_dma_wait();
-    }
+    // each wave copies its own 16 rows and waits for them alone
+    const int wbytes = kWaveRows * rbytes;  // a multiple of 16 for both row types
+    uint8_t *T = tile + wave * wbytes;
+    dma_wave_copy_nt(T, batched_down(a, w.e) + (size_t)(rt0 + wave * kWaveRows) * rbytes, wbytes);
+    lds_dma_wait();
     if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
-    __syncthreads();
-    const uint8_t *T = tile + wave * kWaveRows * rbytes;
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
     auto x_of = [&](int ch, int b) -> const Q8L & {
@@ -784,6 +770,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
                 if (ch < nch) q5_fold_step(f, xc[ch], acc[ch], accm[ch]);
         }
     }
+    __syncthreads();  // yrow is written
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch) {
         const int idx = ch * 16 + c;
