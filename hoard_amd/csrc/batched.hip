@@ -437,23 +437,23 @@ __device__ __forceinline__ int pair_expert(int id, int j, int k, int n_ids) {
     return first ? e : -1;
 }
 
-// One token per workgroup of 512 threads: wave 0 runs the router tail
+// One token per workgroup of 64 (nb + 1) threads: wave 0 runs the router tail
 // (softmax, top-k, renorm) on the token's logits and writes the pairs' experts
-// for the grouping; wave b forms Q8_K of block b of its fx.
-__global__ __launch_bounds__(512) void route_tails_kernel(BatchedArgs a) {
+// for the grouping from the selection it holds; wave b + 1 forms Q8_K of block
+// b of its fx.
+__global__ __launch_bounds__(576) void route_tails_kernel(BatchedArgs a) {
     constexpr int nb = kRouteN / QK;
+    static_assert(64 * (nb + 1) == 576, "a tail wave and a wave per fx block");
     const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave == 0) {
-        router_tail<false>(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, t);
-        __builtin_amdgcn_s_waitcnt(0);  // the selection is stored: read it back past L1
-        const int id = lane < a.k ? __hip_atomic_load(a.sel + (size_t)t * a.k + lane, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT)
-                                  : 0;
-        const int e = pair_expert(id, lane, a.k, a.n_ids);
+        const int id = router_tail<false>(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, t);
+        const int e = pair_expert(lane < a.k ? id : 0, lane, a.k, a.n_ids);
         const int kk = a.k + a.sh;  // pair (t, k): the shared expert, id n_ids
         if (lane < kk) a.pexp[(size_t)t * kk + lane] = lane < a.k ? e : a.n_ids;
+    } else {
+        const int b = wave - 1;
+        wave_quantize_q8l(a.fx + (size_t)t * kRouteN + b * QK, q8(a.q8x) + (size_t)t * nb + b);
     }
-    if (wave < nb) wave_quantize_q8l(a.fx + (size_t)t * kRouteN + wave * QK, q8(a.q8x) + (size_t)t * nb + wave);
 }
 
 // Caller ids of a prefill-sized batch, one token per workgroup of 512 threads:
@@ -910,7 +910,7 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
             hipLaunchKernelGGL(route_gemm_kernel<256>, rg, dim3(512), 0, s, a);
         else
             hipLaunchKernelGGL(route_gemm_kernel<512>, rg, dim3(512), 0, s, a);
-        hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(512), 0, s, a);
+        hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(576), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
     }

@@ -140,7 +140,8 @@ __device__ __forceinline__ void q4_fold(const Q4Raw &raw, Q4Fold &o) {
 // One super-block of the folded tile against the lane's token column (its Q8_K
 // block x): the integer sums from the three MFMA chains, then the per-token
 // path's fp32 block terms added in order.
-__device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const Q8L &x, float acc[4], float accm[4]) {
+template <class X>
+__device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const X &x, float acc[4], float accm[4]) {
     const int g = (threadIdx.x & 63) >> 4;
     v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0}, dn = {0, 0, 0, 0};
 #pragma unroll
@@ -170,12 +171,20 @@ __device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const Q8L &x, floa
 // super-block of its rows in registers; the gate waves hand their values to the
 // up waves through LDS, which form h and store it to hbuf[sorted pair][row].
 // Three workgroups share a CU.
-constexpr int kXGran = (int)sizeof(Q8L) / 16;                          // 16-byte granules per Q8_K block
+// The part of a Q8_K block the folded gate/up tiles read: the quants and the
+// scale (granules 0-15 and 18 of the block; its 16-element sums are not read).
+struct Q8S {
+    int32_t qs[64];
+    float d;
+    int32_t pad[3];
+};
+static_assert(sizeof(Q8S) == 272 && offsetof(Q8L, d) == 288, "Q8S: 17 granules, d from granule 18 of Q8L");
+constexpr int kXGran = (int)sizeof(Q8S) / 16;                          // 16-byte granules staged per token
 constexpr int kXChunksPerBlock = (kUnitTokens * kXGran + 63) / 64;     // 1 KB copies per unit block
 
 template <int NB>
 __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
-    __shared__ __align__(16) Q8L xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
+    __shared__ __align__(16) Q8S xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
     __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
 #pragma unroll
     for (int j = 0; j < kXJ; ++j) {
         const int p = 64 * (wave + 4 * j) + lane, tt = min(p / kXGran, kUnitTokens - 1), o = p % kXGran;
-        xsrc[j] = a.q8x + (size_t)a.ptok[w.p0 + min(tt, w.n - 1)] * NB * sizeof(Q8L) + 16 * o;
+        xsrc[j] = a.q8x + (size_t)a.ptok[w.p0 + min(tt, w.n - 1)] * NB * sizeof(Q8L) + 16 * (o < 16 ? o : 18);
     }
     auto stage_x = [&](int b, int buf) {
 #pragma unroll
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
             q4_raw_load(W, rb, b + 1, raw);
             stage_x(b + 1, (b + 1) & 1);
         }
-        const Q8L *xb = xs[b & 1];
+        const Q8S *xb = xs[b & 1];
 #pragma unroll
         for (int ch = 0; ch < kChunks; ++ch)
             if (ch < nch) q4_fold_step(t, xb[ch * 16 + c], acc[ch], accm[ch]);

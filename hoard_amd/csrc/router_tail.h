@@ -65,8 +65,8 @@ __device__ inline void softmax_nt(const float *lg, int E, float (&p)[NT]) {
 // workgroup's own use, or LDS).
 // NT: experts per lane the body is compiled for (E <= 64 NT, E <= 1024).
 template <bool AGENT, int NT, bool STORE_AGENT = AGENT>
-__device__ inline void router_tail_nt(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel,
-                                      int tok) {
+__device__ inline int router_tail_nt(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel,
+                                     int tok) {
     const int lane = threadIdx.x & 63;
     float p[NT];
     softmax_nt<AGENT, NT>(logits + (size_t)tok * E, E, p);
@@ -115,20 +115,22 @@ __device__ inline void router_tail_nt(const float *logits, int E, int k, int ren
             wsel[(size_t)tok * k + lane] = my_w;
         }
     }
+    return my_sel;
 }
 
+// Returns the selection of slot `lane` in lane `lane` (lanes < k).
 template <bool AGENT = false, bool STORE_AGENT = AGENT>
-__device__ inline void router_tail(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel, int tok) {
+__device__ inline int router_tail(const float *logits, int E, int k, int renorm, int32_t *sel, float *wsel, int tok) {
     if (E <= 64)
-        router_tail_nt<AGENT, 1, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
+        return router_tail_nt<AGENT, 1, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 128)
-        router_tail_nt<AGENT, 2, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
+        return router_tail_nt<AGENT, 2, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 256)
-        router_tail_nt<AGENT, 4, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
+        return router_tail_nt<AGENT, 4, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else if (E <= 512)
-        router_tail_nt<AGENT, 8, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
+        return router_tail_nt<AGENT, 8, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
     else
-        router_tail_nt<AGENT, kMaxExpertsPerLane, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
+        return router_tail_nt<AGENT, kMaxExpertsPerLane, STORE_AGENT>(logits, E, k, renorm, sel, wsel, tok);
 }
 
 }  // namespace hoard
