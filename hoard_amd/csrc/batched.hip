@@ -251,23 +251,36 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     __syncthreads();
     if (t < a.M) {
         const float *x = xl[wave];
-        // half-wave h takes rows rp + h, rp = 0, 2, ...
-#pragma unroll 1
-        for (int rp = 0; rp < R; rp += 2) {
-            const int row = r0 + rp + (lane >> 5);
-            const float *wr = wl[min(rp + (lane >> 5), nrows - 1)];
-            float acc = 0.0f;
-#pragma unroll 16
-            for (int i = 0; i < n; i += 32) acc = fmaf(wr[i + l], x[i + l], acc);
-            acc = acc + __shfl_xor(acc, 16);
-            acc = acc + __shfl_xor(acc, 8);
-            acc = acc + __shfl_xor(acc, 4);
-            acc = acc + __shfl_xor(acc, 1);
-            acc = acc + __shfl_xor(acc, 2);
+        // half-wave h takes rows rp + h, rp = 0, 2, ...; the R / 2 rows of a lane
+        // accumulate side by side, so their FMA chains overlap
+        static_assert(R % 2 == 0, "two rows a pass, one a half-wave");
+        constexpr int kP = R / 2;
+        const float *wr[kP];
+        float acc[kP];
+#pragma unroll
+        for (int j = 0; j < kP; ++j) {
+            wr[j] = wl[min(2 * j + (lane >> 5), nrows - 1)];
+            acc[j] = 0.0f;
+        }
+#pragma unroll 8
+        for (int i = 0; i < n; i += 32) {
+            const float xv = x[i + l];
+#pragma unroll
+            for (int j = 0; j < kP; ++j) acc[j] = fmaf(wr[j][i + l], xv, acc[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kP; ++j) {
+            float v = acc[j];
+            v = v + __shfl_xor(v, 16);
+            v = v + __shfl_xor(v, 8);
+            v = v + __shfl_xor(v, 4);
+            v = v + __shfl_xor(v, 1);
+            v = v + __shfl_xor(v, 2);
+            const int row = r0 + 2 * j + (lane >> 5);
             if (l == 0 && row < E)
-                __hip_atomic_store(a.logits + (size_t)t * E + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.logits + (size_t)t * E + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else if (l == 0 && row == E && a.sh)
-                a.sgl[t] = acc;
+                a.sgl[t] = v;
         }
         // Q8_K of fx: workgroup i of a token group quantises blocks i, i + gridDim.x, ...
         // of its tokens, so every block is formed whatever the expert count (grid width)
