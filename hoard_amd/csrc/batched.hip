@@ -130,6 +130,10 @@ __device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ys
         }
     }
     if (tid == 0) a.n_unique[0] = wave_total;
+    // the grid's group places past the used ones hold no expert, so a
+    // workgroup learns from its place alone whether it has work
+    const int umax = min(E, P) + a.sh;
+    for (int g = wave_total + a.sh + tid; g < umax; g += nt) a.uexp[g] = -1;
 }
 
 // Groups and units in ascending expert order from the per-expert pair counts
@@ -618,37 +622,25 @@ __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
 // Weight tiles are contiguous rows of the expert and are copied into LDS in
 // one burst.
 
-// A group's expert and size are read together with the group count (u < the
-// grid's umax keeps them in bounds): one latency rather than two.  Testing them
-// too keeps the compiler from moving their loads after the test (a group
-// always has an expert >= 0 and a token).
+// A group's expert and size, read together (u < the grid's umax keeps them in
+// bounds; the grouping leaves expert -1 at every place past the used groups):
+// one latency.  Testing both keeps the compiler from moving their loads after
+// the test (a group always has an expert >= 0 and a token).
 __device__ __forceinline__ bool load_group(const BatchedArgs &a, int u, int &e, int &m) {
-    const int nu = a.n_unique[0] + a.sh;  // the shared expert's group follows the routed ones
     e = a.uexp[u];
     m = min(a.ucount[u], kMaxTok);
-    return (u < nu) & (e >= 0) & (m >= 1);
+    return (e >= 0) & (m >= 1);
 }
 
-// Gather the Q8_K rows (nb blocks each) of tokens tok[c0 .. c0+mc) into LDS at
-// xs, 16-byte granules spread over the workgroup's nw waves (issued, not
-// waited for).
+// Gather the Q8_K row (nb blocks) of token tt into LDS at xs, 16-byte granules
+// spread over the workgroup's nw waves (issued, not waited for).
 template <int NBX>
-__device__ __forceinline__ void gather_tokens(uint8_t *xs, const uint8_t *q8base, const int *tok, int c0, int mc,
-                                              int m, int wave, int nw) {
+__device__ __forceinline__ void gather_token(uint8_t *xs, const uint8_t *q8base, int tt, int wave, int nw) {
     constexpr int kTokGran = NBX * (int)sizeof(Q8L) / 16;
-    int tk[kXChunk];  // uniform indices: scalar loads
-#pragma unroll
-    for (int i = 0; i < kXChunk; ++i) tk[i] = tok[min(c0 + i, m - 1)];
-    const int lane = threadIdx.x & 63, ng = mc * kTokGran;
-    for (int k = wave; 64 * k < ng; k += nw) {
+    const int lane = threadIdx.x & 63;
+    for (int k = wave; 64 * k < kTokGran; k += nw) {
         const int p = 64 * k + lane;
-        if (p < ng) {
-            const int t = p / kTokGran, o = p - t * kTokGran;
-            int tt = tk[0];
-#pragma unroll
-            for (int i = 1; i < kXChunk; ++i) tt = t == i ? tk[i] : tt;
-            dma_lanes(xs + 1024 * k, q8base + (size_t)tt * (NBX * sizeof(Q8L)) + 16 * o);
-        }
+        if (p < kTokGran) dma_lanes(xs + 1024 * k, q8base + (size_t)tt * (NBX * sizeof(Q8L)) + 16 * p);
     }
 }
 
@@ -665,14 +657,21 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     constexpr int kTileBytes = kRows * kRowBytes;
     static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
     const int u = blockIdx.y;
+    const int *tok = a.utok + u * kMaxTok;
+    // the group's first four tokens are read with its size and expert (the
+    // group's places are in the buffer whatever they turn out to be): one
+    // latency, not two
+    static_assert(kMaxTok % 4 == 0, "a group's token places are 16-byte aligned");
+    const int4 tok4 = *reinterpret_cast<const int4 *>(tok);
     int e, m;
-    if (!load_group(a, u, e, m)) return;
+    const bool has = load_group(a, u, e, m);
+    asm volatile("" ::"s"(tok4.x), "s"(tok4.y), "s"(tok4.z), "s"(tok4.w));  // loaded before the test, not after
+    if (!has) return;
     __shared__ __align__(16) uint8_t wt[2][kTileBytes];
     __shared__ __align__(16) uint8_t xs[kXChunk * NB * sizeof(Q8L)];
     __shared__ float gu[2][kRows][kCols];  // gate and up values of 16 token columns
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kRows;
-    const int *tok = a.utok + u * kMaxTok;
     const uint8_t *W = (wave ? batched_up(a, e) : batched_gate(a, e)) + (size_t)row0 * kRowBytes;
     // h = silu(gate) * up of columns c0 .. c0 + 15 from gu (128 threads: 8 rows x 16 columns)
     auto store_h = [&](int c0) {
@@ -708,7 +707,9 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     for (int c0 = 0; c0 < m; c0 += kXChunk) {
         const int mc = min(m - c0, kXChunk);
         if (c0 > 0) __syncthreads();  // both waves are done with the previous chunk
-        gather_tokens<NB>(xs, a.q8x, tok, c0, mc, m, wave, 2);
+        static_assert(kXChunk == 1, "one token a copy");
+        const int tt = c0 == 0 ? tok4.x : c0 == 1 ? tok4.y : c0 == 2 ? tok4.z : c0 == 3 ? tok4.w : tok[c0];
+        gather_token<NB>(xs, a.q8x, tt, wave, 2);
         if (c0 == 0) dma_wave_copy_nt(wt[wave], W, kTileBytes);
         lds_dma_wait();
         __syncthreads();
