@@ -137,8 +137,10 @@ __device__ void group_by_expert(const BatchedArgs &a, GroupLds &g, const int *ys
 }
 
 // Groups and units in ascending expert order from the per-expert pair counts
-// g.cnt (wave 0 of the grouping workgroup): uexp / ucount / goff / units / hist,
-// n_unique / n_units, and g.base[e], the first sorted place of expert e.
+// g.cnt (wave 0 of the grouping workgroup): uexp / ucount / goff / hist, the
+// unit records {expert, first sorted pair, pairs} (every place past the last
+// unit zeroed), n_unique / n_units, and g.base[e], the first sorted place of
+// expert e.
 __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
     const int tid = threadIdx.x, E = a.n_ids + a.sh;
     {
@@ -170,11 +172,8 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
                 a.uexp[gi] = e;
                 a.ucount[gi] = c;
                 a.goff[gi] = pi;
-                for (int s0 = 0; s0 < c; s0 += kUnitTokens, ++ui) {
-                    a.units[3 * ui] = gi;
-                    a.units[3 * ui + 1] = s0;
-                    a.units[3 * ui + 2] = min(kUnitTokens, c - s0);
-                }
+                for (int s0 = 0; s0 < c; s0 += kUnitTokens, ++ui)
+                    *reinterpret_cast<int4 *>(a.units + 4 * ui) = make_int4(e, pi + s0, min(kUnitTokens, c - s0), 0);
                 ++gi;
             }
             pi += c;
@@ -184,6 +183,10 @@ __device__ void group_units(const BatchedArgs &a, GroupLds &g) {
             a.n_units[0] = iu;
             g.total = ip;  // pairs in all groups
         }
+        // the grid's unit places past the last unit hold no pairs, so a workgroup
+        // learns from its own place alone whether it has work
+        for (int x = __shfl(iu, 63) + lane; x < a.max_units; x += 64)
+            *reinterpret_cast<int4 *>(a.units + 4 * x) = make_int4(0, 0, 0, 0);
     }
 }
 

@@ -1190,9 +1190,9 @@ BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
     L.hbuf = std::max(pairs_s, pairs) * c.n_ff * sizeof(float);
     L.ybuf = pairs * c.n_embd * sizeof(float);
     size_t o = 1;  // [0]: the group count
-    auto take = [&](size_t n) {
-        const size_t r = o;
-        o += n;
+    auto take = [&](size_t n) {  // every array starts 16-byte aligned (read in 16-byte words)
+        const size_t r = (o + 3) & ~(size_t)3;
+        o = r + n;
         return r;
     };
     L.o_slot_of = take(E);
@@ -1206,7 +1206,7 @@ BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
     L.o_ptok = take(pairs);
     L.o_pslot = take(pairs);
     L.o_pexp = take(pairs);
-    L.o_units = take((size_t)3 * L.max_units);
+    L.o_units = take((size_t)4 * L.max_units);
     L.o_nunits = take(1);
     L.o_sgl = take(T);  // floats
     L.n_ints = o;

@@ -42,17 +42,25 @@ static_assert(kChunks == 4, "four token chunks per unit");
 
 __device__ __forceinline__ const Q8L *q8c(const uint8_t *p) { return reinterpret_cast<const Q8L *>(p); }
 
-// A work unit: group u (expert uexp[u]), its pairs [p0, p0 + n) in sorted order.
+// A work unit: expert e, its pairs [p0, p0 + n) in sorted order; one 16-byte
+// record (a place past the last unit holds n = 0), so a workgroup knows its
+// work after one memory latency.
 struct Unit {
     int e, p0, n;
 };
 __device__ __forceinline__ bool load_unit(const BatchedArgs &a, int unit, Unit &w) {
-    if (unit >= a.n_units[0]) return false;
-    const int u = a.units[3 * unit];
-    w.e = a.uexp[u];
-    w.p0 = a.goff[u] + a.units[3 * unit + 1];
-    w.n = a.units[3 * unit + 2];
+    const int4 r = *reinterpret_cast<const int4 *>(a.units + 4 * unit);
+    w.e = r.x;
+    w.p0 = r.y;
+    w.n = r.z;
     return w.n > 0;
+}
+// The same after a test of the unit count: two latencies, but the Q4_K gate/up
+// kernel's registers stay within its three-wave budget with the early exit
+// (without it the compiler spills 24 bytes a lane).
+__device__ __forceinline__ bool load_unit_counted(const BatchedArgs &a, int unit, Unit &w) {
+    if (unit >= a.n_units[0]) return false;
+    return load_unit(a, unit, w);
 }
 
 __device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     __shared__ __align__(16) Q8S xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
     __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
     Unit w;
-    if (!load_unit(a, blockIdx.y, w)) return;
+    if (!load_unit_counted(a, blockIdx.y, w)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * kGuRows + rt * kWaveRows;
@@ -198,18 +206,21 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     // unit's token chunks are copied, token places past its end copy its last token
     constexpr int kXJ = (kXChunksPerBlock + 3) / 4;
     const int ngran = nch * 16 * kXGran;
-    const uint8_t *xsrc[kXJ];
+    // byte offsets into q8x (it holds at most 512 tokens' blocks): half the
+    // registers of pointers
+    uint32_t xoff[kXJ];
 #pragma unroll
     for (int j = 0; j < kXJ; ++j) {
         const int p = 64 * (wave + 4 * j) + lane, tt = min(p / kXGran, kUnitTokens - 1), o = p % kXGran;
-        xsrc[j] = a.q8x + (size_t)a.ptok[w.p0 + min(tt, w.n - 1)] * NB * sizeof(Q8L) + 16 * (o < 16 ? o : 18);
+        xoff[j] = (uint32_t)a.ptok[w.p0 + min(tt, w.n - 1)] * (uint32_t)(NB * sizeof(Q8L)) + 16u * (o < 16 ? o : 18);
     }
     auto stage_x = [&](int b, int buf) {
 #pragma unroll
         for (int j = 0; j < kXJ; ++j) {
             const int ck = wave + 4 * j;
             if (64 * ck < ngran && 64 * ck + lane < ngran)
-                dma_lanes(reinterpret_cast<uint8_t *>(&xs[buf][0]) + 1024 * ck, xsrc[j] + (size_t)b * sizeof(Q8L));
+                dma_lanes(reinterpret_cast<uint8_t *>(&xs[buf][0]) + 1024 * ck,
+                          a.q8x + (xoff[j] + (uint32_t)(b * sizeof(Q8L))));
         }
     };
     float acc[kChunks][4], accm[kChunks][4];
