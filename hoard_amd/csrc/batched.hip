@@ -39,7 +39,12 @@ __device__ __forceinline__ Q8L *q8(uint8_t *p) { return reinterpret_cast<Q8L *>(
 // copies of the tokens' fx): measured per layer, four rows against two took
 // 0.5 us off at 16 tokens and 2.8 at 32 (Qwen3-30B shape), 3.3 and 7.5 with
 // 512 experts (Qwen3-Next), and added 1.2 us at 4 tokens; eight rows were
-// slower than four everywhere.  The last
+// slower than four everywhere.  A remainder of one row (a shared expert's
+// gate row after a multiple of R routed rows) goes to the last workgroup of
+// the row range as an extra pass instead of a workgroup of its own: with 512
+// experts and four token groups the extra workgroups would not fit the two a
+// CU that the LDS allows, and a second round of workgroups would follow the
+// first.  The last
 // workgroup of a token group (device-scope counter) runs the tails of its
 // tokens; the last token group's tail workgroup then groups the (token, slot)
 // pairs by expert.  Waves with a spare slot quantise fx to Q8_K.
@@ -237,12 +242,12 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     const int t = tg * kRouteTok + wave;  // this wave's token; its half-waves take one row each
     // rows 0..E-1 are the router's; row E (with a shared expert) is its gate row
     const int r0 = blockIdx.x * R;
-    const int nrows = min(R, E + a.sh - r0);
+    const int nrows = blockIdx.x == gridDim.x - 1 ? E + a.sh - r0 : R;  // R + 1 with a one-row remainder
     // the workgroup's token rows and router rows go to LDS in one burst, so
     // that every load is in flight at once; the dot then reads them in the
     // per-lane order the accumulation needs
     __shared__ __align__(16) float xl[kRouteTok][kRouteN];
-    __shared__ __align__(16) float wl[R][kRouteN];
+    __shared__ __align__(16) float wl[R + 1][kRouteN];
     if (t < a.M) dma_wave_copy(reinterpret_cast<uint8_t *>(xl[wave]), reinterpret_cast<const uint8_t *>(a.fx + (size_t)t * n),
                                n * (int)sizeof(float));
     {
@@ -275,9 +280,18 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 #pragma unroll
             for (int j = 0; j < kP; ++j) acc[j] = fmaf(wr[j][i + l], xv, acc[j]);
         }
+        // the remainder row, on both half-waves (the second one's result is
+        // past the rows and not stored)
+        float acc_r = 0.0f;
+        if (nrows > R) {
+            const float *w = wl[R];
+#pragma unroll 8
+            for (int i = 0; i < n; i += 32) acc_r = fmaf(w[i + l], x[i + l], acc_r);
+        }
 #pragma unroll
-        for (int j = 0; j < kP; ++j) {
-            float v = acc[j];
+        for (int j = 0; j <= kP; ++j) {
+            if (j == kP && nrows <= R) break;
+            float v = j < kP ? acc[j] : acc_r;
             v = v + __shfl_xor(v, 16);
             v = v + __shfl_xor(v, 8);
             v = v + __shfl_xor(v, 4);
@@ -931,11 +945,13 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
     }
+    // row workgroups: a remainder of one row joins the last workgroup
     const int nr = a.E + a.sh, ntg = (a.M + kRouteTok - 1) / kRouteTok;
+    auto row_groups = [nr](int R) { return nr > R && nr % R == 1 ? nr / R : (nr + R - 1) / R; };
     if (a.M > 8)
-        hipLaunchKernelGGL(route_kernel<4>, dim3((nr + 3) / 4, ntg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(route_kernel<4>, dim3(row_groups(4), ntg), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(route_kernel<2>, dim3((nr + 1) / 2, ntg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(route_kernel<2>, dim3(row_groups(2), ntg), dim3(256), 0, s, a);
     return launch_groups(a, s);
 }
 
