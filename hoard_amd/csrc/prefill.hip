@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
     Unit w;
     if (!load_unit_counted(a, blockIdx.y, w)) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * kGuRows + rt * kWaveRows;
     constexpr size_t rb = (size_t)NB * kQ4KBytes;
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void pf_down_q4_kernel(BatchedArgs a) {
     __shared__ __align__(16) uint8_t tile[kTileBytes];
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
     // each wave copies its own 16 rows and waits for them alone
     constexpr int kWaveBytes = kWaveRows * kRowBytes;
@@ -598,7 +598,7 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     __shared__ float gx[2][kChunks][4][64];  // gate values: [row tile][chunk][row i][lane]
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * 2 * kWaveRows;
     // the lane's token of each chunk, read once, while the tile lands
@@ -669,7 +669,7 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     __shared__ int yrow[kUnitTokens];  // y row (token * slots + slot) of each of the unit's pairs
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
@@ -740,7 +740,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     if (!load_unit(a, blockIdx.y, w)) return;
     const bool shx = TS != kTypeQ5K && a.sh && w.e == a.n_ids;  // the shared expert's Q6_K rows
     const int rbytes = shx ? kRowBytesS : kRowBytesD;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+    const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int rt0 = blockIdx.x * kDnRows;
     // the pairs' places, read while the tile lands
     const int tid = threadIdx.x;

@@ -38,6 +38,10 @@ __device__ __forceinline__ double dpp_d(double v) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
+// The wave's index within its workgroup, in a scalar register: addresses
+// formed from it (LDS staging bases, row pointers) stay scalar instead of
+// being formed per lane.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 __device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
