@@ -237,7 +237,7 @@ template <int R>
 __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
     constexpr int n = kRouteN, nb = kRouteN / QK;
     const int E = a.E;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
+    const int wave = wave_index(), lane = threadIdx.x & 63, l = lane & 31;
     const int tg = blockIdx.y;
     const int t = tg * kRouteTok + wave;  // this wave's token; its half-waves take one row each
     // rows 0..E-1 are the router's; row E (with a shared expert) is its gate row
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
     constexpr int n = kRouteN, kSteps = n / kTileK;
     static_assert(kSteps >= kGemmBufs, "the ring is filled before the first step");
     constexpr int kRowsPerWave = (kTileE + kTileT) / 8 * (kTileK / 256);  // 1 KB copies each wave issues per step
-    const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = wave_index(), lane = tid & 63;
     const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
     const int re = (q & 3) * 4, rt = (q >> 2) * 4;  // this group's 4 experts and 4 tokens within the tile
     float acc[4][4];
@@ -478,7 +478,7 @@ __device__ __forceinline__ int pair_expert(int id, int j, int k, int n_ids) {
 __global__ __launch_bounds__(576) void route_tails_kernel(BatchedArgs a) {
     constexpr int nb = kRouteN / QK;
     static_assert(64 * (nb + 1) == 576, "a tail wave and a wave per fx block");
-    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x, wave = wave_index(), lane = threadIdx.x & 63;
     if (wave == 0) {
         const int id = router_tail<false>(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, t);
         const int e = pair_expert(lane < a.k ? id : 0, lane, a.k, a.n_ids);
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(576) void route_tails_kernel(BatchedArgs a) {
 // or a repeated id).
 __global__ __launch_bounds__(512) void prep_ids_large_kernel(BatchedArgs a) {
     constexpr int nb = kRouteN / QK;
-    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, k = a.k;
+    const int t = blockIdx.x, wave = wave_index(), lane = threadIdx.x & 63, k = a.k;
     if (wave == 0) {
         const int id = lane < k ? a.sel[(size_t)t * k + lane] : 0;
         const bool bad = __any(lane < k && (id < 0 || id >= a.n_ids));
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(1024) void group_kernel(BatchedArgs a) {
 // id with weight 0.
 __global__ __launch_bounds__(512) void prep_ids_kernel(BatchedArgs a) {
     constexpr int nb = kRouteN / QK;
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     if ((int)blockIdx.x < a.M) {
         const int t = blockIdx.x;
         for (int b = wave; b < nb; b += 8)
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
     __shared__ __align__(16) uint8_t wt[2][kTileBytes];
     __shared__ __align__(16) uint8_t xs[kXChunk * NB * sizeof(Q8L)];
     __shared__ float gu[2][kRows][kCols];  // gate and up values of 16 token columns
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
+    const int wave = wave_index(), lane = threadIdx.x & 63, t8 = lane & 7, grp = lane >> 3;
     const int row0 = blockIdx.x * kRows;
     const uint8_t *W = (wave ? batched_up(a, e) : batched_gate(a, e)) + (size_t)row0 * kRowBytes;
     // h = silu(gate) * up of columns c0 .. c0 + 15 from gu (128 threads: 8 rows x 16 columns)
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(128, 3) void gateup_kernel(BatchedArgs a) {
 // -- Q8_K of h per (expert, token) ---------------------------------------------
 // One workgroup per (group, token), a wave per 256-element block of h.
 __global__ __launch_bounds__(256) void quant_h_kernel(BatchedArgs a) {
-    const int u = blockIdx.y, c = blockIdx.x, b = threadIdx.x >> 6;
+    const int u = blockIdx.y, c = blockIdx.x, b = wave_index();
     const int nbh = a.n_ff / QK;
     const size_t uc = (size_t)u * kMaxTok + c;
     // h is loaded with the group count and size, not after them (its place

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void spread_kernel(SpreadArgs a) {
     __shared__ unsigned seq_s;
     __shared__ unsigned gu_done;  // waves 0-5 done with their gate/up rows, counted over layers
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = wave_index(), lane = tid & 63;
     const int grp = tid >> 3, t8 = tid & 7;
     const unsigned xcc = xcc_id();
     if (tid == 0) {

@@ -15,6 +15,7 @@
 // same activation.
 #include "kernels.h"
 #include "qblocks.h"
+#include "wave.h"
 
 namespace hoard {
 
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(GateUpArgs a, int R) {
     const int og = stage_issue(lds_g, gsrc, R * rbg);
     const int ou = stage_issue(lds_u, usrc, R * rbu);
 
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     for (int b = wave; b < nb; b += kThreads / 64) wave_quantize_q8k(a.fx + b * QK, &qx[b]);
     __syncthreads();
 
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(DownArgs a, int 
         if (threadIdx.x == 0) offs[s] = o;
     }
 
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     for (int q = wave; q < nq; q += kThreads / 64) {
         const int j = q < k * nbh ? q / nbh : k;
         const int b = q < k * nbh ? q - j * nbh : q - k * nbh;

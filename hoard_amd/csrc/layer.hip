@@ -57,7 +57,7 @@ __global__ __launch_bounds__(128) void layer_route_kernel(RouterArgs a) {
     __shared__ double red[2];
     __shared__ int last;
     const int E = a.E;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
+    const int wave = wave_index(), lane = threadIdx.x & 63, l = lane & 31;
     const int r0 = blockIdx.x * kRouteRows;
     const int nrows = min(kRouteRows, E - r0);
     // both copies in flight at once: x on wave 0, the rows split over the waves
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(512) void layer_gateup_kernel(GateUpArgs a) {
     const MatDesc &U = shared ? a.sh_up : a.up;
     const int r0 = blockIdx.x * kGuRows;
     if (r0 >= G.rows) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = wave_index(), lane = threadIdx.x & 63;
     float *hout = a.h + (size_t)j * a.hstride + r0;
     const uint8_t *gsrc = G.base, *usrc = U.base;
     if (!shared) {
@@ -190,7 +190,7 @@ template <int T, int NB, int NT>
 __device__ __forceinline__ void down_rows(const uint8_t *base, int n, int u0, const Q8L *q8h, float *ys) {
     static_assert(NT % 128 == 0, "whole wave pairs");
     constexpr int kRowBytes = NB * QType<T>::bytes;
-    const int wave = threadIdx.x >> 6, grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
+    const int wave = wave_index(), grp = threadIdx.x >> 3, t8 = threadIdx.x & 7;
     if constexpr (T == kTypeQ6K) {
         // 8 lanes per row; a wave takes rows of one parity so that its 2-byte
         // aligned rows share their 4-byte alignment
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(1024) void layer_down_kernel(DownArgs a) {
     const int nu = k + (has_sh ? 1 : 0);
     uint8_t *wd = smem;
     Q8L *q8h = reinterpret_cast<Q8L *>(smem + k * kSegBytes + (has_sh ? kSegBytesS : 0));
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     const int d0 = blockIdx.x * kDownRows;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
@@ -321,7 +321,7 @@ __device__ __forceinline__ unsigned long long ctr_add(unsigned long long *p) {
 // rms_norm scale of x (every thread takes part): mean of x*x in double,
 // 1/sqrtf(mean + eps), as the route kernel forms it.
 __device__ __forceinline__ float rms_scale(const float *x, int n, float eps, double *red) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = wave_index(), lane = threadIdx.x & 63;
     double ss = 0.0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const float v = x[i];
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(512) void fused_layer_kernel(FusedLayerArgs a) {
     __shared__ float w_s[16];
     __shared__ __align__(16) float ps[128];
     __shared__ float lg_s[1024];  // this launch's logits, gathered from the XCD's tagged copy
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = wave_index(), lane = tid & 63;
     const int E = a.E, k = a.k, nff = a.gate.rows;
     // The selection in the gate/up and down roles.  select_a (wave 0) waits
     // until every logit of this launch is stored; with E <= 128 it forms the

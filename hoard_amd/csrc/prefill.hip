@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
 // -- Q8_K of h per sorted pair --------------------------------------------------
 // grid (pairs), block 64 * NBH: wave b quantises block b of the pair's h.
 __global__ __launch_bounds__(256) void pf_quant_h_kernel(BatchedArgs a) {
-    const int pos = blockIdx.x, b = threadIdx.x >> 6;
+    const int pos = blockIdx.x, b = wave_index();
     const int nbh = a.n_ff / QK;
     if (b >= nbh) return;
     wave_quantize_q8l(a.hbuf + (size_t)pos * a.n_ff + (size_t)b * QK,

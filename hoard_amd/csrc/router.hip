@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void router_rows_m_kernel(RouterArgs a) {
     const float4 *src = reinterpret_cast<const float4 *>(a.xin + (size_t)t0 * n);
     for (int i = threadIdx.x; i < nt * n / 4; i += blockDim.x) reinterpret_cast<float4 *>(xs)[i] = src[i];
     __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l = lane & 31;
+    const int wave = wave_index(), lane = threadIdx.x & 63, l = lane & 31;
     const int row = blockIdx.x * kRowsPerWg + wave * 2 + (lane >> 5);
     if (row >= E) return;
     const float *wr = a.w + (size_t)row * n;
