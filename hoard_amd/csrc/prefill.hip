@@ -68,23 +68,28 @@ __device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
 }
 
 // One Q4_K super-block of a 16-row tile, folded for v_mfma_i32_16x16x64_i8.
-// Lane l supplies A[l % 16][16 g .. 16 g + 15] (g = l / 16) of each 64-element
-// chunk jc (the lane layout checked by a probe: B[16 g ..][l % 16] alike,
-// D[4 g + i][l % 16]).  Chunk jc holds sub-block 2 jc in the low nibbles of its
-// 32 quant bytes and sub-block 2 jc + 1 in the high ones, so lane group g takes
-// the low (g < 2) or high (g >= 2) nibbles of bytes 16 (g & 1) .. + 15:
-// sub-block s = 2 jc + g / 2.  The sub-block scale sc (6 bits) is folded into A
-// in two parts that keep every product an int8: hi = q * (sc >> 3) and
-// lo = q * (sc & 7), each <= 105, with sc * q = 8 hi + lo; a nibble times a
-// factor below 8 never carries into the next byte, so a whole word multiplies
-// at once.  The min term sum_s m_s * (sum of sub-block s's activation quants)
-// is a third MFMA with m_s broadcast over its sub-block.  The three chains give
-// exactly the per-token path's integer sums isum = 8 D_hi + D_lo and
-// msum = D_min.  Each 16-bit half of a word of four nibbles multiplies at once
-// (v_pk_mul_lo_u16, full rate, where a 32-bit multiply is quarter rate).
+// Lane l supplies A[l % 16][16 g .. 16 g + 15] (g = l / 16) of each of the four
+// MFMA steps (the lane layout checked by a probe: B[16 g ..][l % 16] alike,
+// D[4 g + i][l % 16]).  Quant byte i of chunk q (32 bytes) holds element
+// 64 q + i in its low nibble and 64 q + 32 + i in its high one (sub-blocks 2 q
+// and 2 q + 1), and a step's K index is only a summation index: lane group g
+// takes the whole of chunk g, as two 16-byte pieces p that each give two
+// steps, step j = 2 p + h taking nibble half h of piece p, i.e. elements
+// 64 g + 16 p + 32 h .. + 15 of sub-block 2 g + h.  Each quant byte is so
+// loaded once (two 16-byte loads a lane), and the lane's B operand of step j
+// is those 16 contiguous activation quants.  The sub-block scale sc (6 bits)
+// is folded into A in two parts that keep every product an int8:
+// hi = q * (sc >> 3) and lo = q * (sc & 7), each <= 105, with
+// sc * q = 8 hi + lo; a nibble times a factor below 8 never carries into the
+// next byte, so a whole word multiplies at once.  The min term
+// sum_s m_s * (sum of sub-block s's activation quants) is a third MFMA with
+// m_s broadcast over the step.  The three chains give exactly the per-token
+// path's integer sums isum = 8 D_hi + D_lo and msum = D_min.  Each 16-bit half
+// of a word of four nibbles multiplies at once (v_pk_mul_lo_u16, full rate,
+// where a 32-bit multiply is quarter rate).
 struct Q4Fold {
     v4i hi[4], lo[4];
-    uint32_t mn;          // byte jc: the min of the lane's sub-block in chunk jc
+    uint32_t mn;          // byte j: the min of step j's sub-block
     float d[4], dmin[4];  // factors of the four rows whose results the lane receives
 };
 
@@ -101,63 +106,64 @@ __device__ __forceinline__ int splat_byte_of(uint32_t w, int i) {
 }
 
 // The lane's raw bytes of one super-block of a 16-row tile: its row's header
-// and quants (16 bytes of each 64-element chunk) and the fp16 factors of the
-// four rows whose results it receives; loaded one super-block ahead.
+// and chunk g's 32 quant bytes; loaded one super-block ahead.  The fp16
+// factors of the four rows whose results the lane receives come from those
+// rows' lanes by a lane shuffle (four 4-byte gathers from global memory per
+// super-block cost more than the shuffles).
 struct Q4Raw {
     uint4 hd;
-    uint4 qv[4];
-    uint32_t dm[4];
+    uint4 qv[2];
 };
 
 __device__ __forceinline__ void q4_raw_load(const uint8_t *W, size_t rb, int b, Q4Raw &o) {
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const uint8_t *blk = W + (size_t)r * rb + (size_t)b * kQ4KBytes;
     o.hd = *reinterpret_cast<const uint4 *>(blk);
-#pragma unroll
-    for (int jc = 0; jc < 4; ++jc) o.qv[jc] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * jc + 16 * (g & 1));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        o.dm[i] = *reinterpret_cast<const uint32_t *>(W + (size_t)(4 * g + i) * rb + (size_t)b * kQ4KBytes);
+    o.qv[0] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * g);
+    o.qv[1] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * g);
 }
 
 __device__ __forceinline__ void q4_fold(const Q4Raw &raw, Q4Fold &o) {
     const int g = (threadIdx.x & 63) >> 4;
     uint32_t sc[2], mn[2];
     q4k_scales_packed(raw.hd, sc, mn);
-    const uint32_t nsh = 4u * (uint32_t)(g >> 1);
-    o.mn = 0u;
+    // the scales and mins of sub-blocks 2 g (low nibbles) and 2 g + 1 (high)
+    const int s0 = 2 * g;
+    const uint32_t sc0 = (uint32_t)byte_of(sc[s0 >> 2], s0 & 3), sc1 = (uint32_t)byte_of(sc[s0 >> 2], (s0 & 3) + 1);
+    const uint32_t mn0 = (uint32_t)byte_of(mn[s0 >> 2], s0 & 3), mn1 = (uint32_t)byte_of(mn[s0 >> 2], (s0 & 3) + 1);
+    o.mn = mn0 | mn1 << 8 | mn0 << 16 | mn1 << 24;
 #pragma unroll
-    for (int jc = 0; jc < 4; ++jc) {
-        const int s = 2 * jc + (g >> 1);
-        const uint32_t scs = (uint32_t)byte_of(sc[s >> 2], s & 3), mns = (uint32_t)byte_of(mn[s >> 2], s & 3);
-        const uint4 qv = raw.qv[jc];
+    for (int j = 0; j < 4; ++j) {
+        const uint4 qv = raw.qv[j >> 1];
+        const uint32_t nsh = 4u * (uint32_t)(j & 1), scs = (j & 1) ? sc1 : sc0;
         const uint32_t w[4] = {(qv.x >> nsh) & 0x0f0f0f0fu, (qv.y >> nsh) & 0x0f0f0f0fu, (qv.z >> nsh) & 0x0f0f0f0fu,
                                (qv.w >> nsh) & 0x0f0f0f0fu};
         const uint32_t h = scs >> 3, lw = scs & 7u;
-        o.hi[jc] = v4i{nib_mul(w[0], h), nib_mul(w[1], h), nib_mul(w[2], h), nib_mul(w[3], h)};
-        o.lo[jc] = v4i{nib_mul(w[0], lw), nib_mul(w[1], lw), nib_mul(w[2], lw), nib_mul(w[3], lw)};
-        o.mn |= mns << (8 * jc);
+        o.hi[j] = v4i{nib_mul(w[0], h), nib_mul(w[1], h), nib_mul(w[2], h), nib_mul(w[3], h)};
+        o.lo[j] = v4i{nib_mul(w[0], lw), nib_mul(w[1], lw), nib_mul(w[2], lw), nib_mul(w[3], lw)};
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        o.d[i] = half_bits_to_float(raw.dm[i] & 0xffffu);
-        o.dmin[i] = half_bits_to_float(raw.dm[i] >> 16);
+        const uint32_t dm = (uint32_t)__shfl((int)raw.hd.x, 4 * g + i);
+        o.d[i] = half_bits_to_float(dm & 0xffffu);
+        o.dmin[i] = half_bits_to_float(dm >> 16);
     }
 }
 
 // One super-block of the folded tile against the lane's token column (its Q8_K
 // block x): the integer sums from the three MFMA chains, then the per-token
-// path's fp32 block terms added in order.
+// path's fp32 block terms added in order.  Step j's B operand: activation
+// quants 64 g + 16 (j / 2) + 32 (j % 2) .. + 15.
 template <class X>
 __device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const X &x, float acc[4], float accm[4]) {
     const int g = (threadIdx.x & 63) >> 4;
     v4i dh = {0, 0, 0, 0}, dl = {0, 0, 0, 0}, dn = {0, 0, 0, 0};
 #pragma unroll
-    for (int jc = 0; jc < 4; ++jc) {
-        const v4i xv = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
-        dh = mfma_16x16x64(w.hi[jc], xv, dh);
-        dl = mfma_16x16x64(w.lo[jc], xv, dl);
-        const int m4 = splat_byte_of(w.mn, jc);
+    for (int j = 0; j < 4; ++j) {
+        const v4i xv = *reinterpret_cast<const v4i *>(&x.qs[16 * g + 4 * (j >> 1) + 8 * (j & 1)]);
+        dh = mfma_16x16x64(w.hi[j], xv, dh);
+        dl = mfma_16x16x64(w.lo[j], xv, dl);
+        const int m4 = splat_byte_of(w.mn, j);
         dn = mfma_16x16x64(v4i{m4, m4, m4, m4}, xv, dn);
     }
     const float xd = x.d;
