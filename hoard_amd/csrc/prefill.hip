@@ -55,13 +55,6 @@ __device__ __forceinline__ bool load_unit(const BatchedArgs &a, int unit, Unit &
     w.n = r.z;
     return w.n > 0;
 }
-// The same after a test of the unit count: two latencies, but the Q4_K gate/up
-// kernel's registers stay within its three-wave budget with the early exit
-// (without it the compiler spills 24 bytes a lane).
-__device__ __forceinline__ bool load_unit_counted(const BatchedArgs &a, int unit, Unit &w) {
-    if (unit >= a.n_units[0]) return false;
-    return load_unit(a, unit, w);
-}
 
 __device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -89,7 +82,7 @@ __device__ __forceinline__ v4i mfma_16x16x64(v4i a, v4i b, v4i c) {
 // where a 32-bit multiply is quarter rate).
 struct Q4Fold {
     v4i hi[4], lo[4];
-    uint32_t mn;          // byte j: the min of step j's sub-block
+    v4i mn[2];            // the min of sub-block 2 g + h in every byte (steps of nibble half h)
     float d[4], dmin[4];  // factors of the four rows whose results the lane receives
 };
 
@@ -130,8 +123,11 @@ __device__ __forceinline__ void q4_fold(const Q4Raw &raw, Q4Fold &o) {
     // the scales and mins of sub-blocks 2 g (low nibbles) and 2 g + 1 (high)
     const int s0 = 2 * g;
     const uint32_t sc0 = (uint32_t)byte_of(sc[s0 >> 2], s0 & 3), sc1 = (uint32_t)byte_of(sc[s0 >> 2], (s0 & 3) + 1);
-    const uint32_t mn0 = (uint32_t)byte_of(mn[s0 >> 2], s0 & 3), mn1 = (uint32_t)byte_of(mn[s0 >> 2], (s0 & 3) + 1);
-    o.mn = mn0 | mn1 << 8 | mn0 << 16 | mn1 << 24;
+    const int mw = (int)mn[s0 >> 2];
+    const int m0 = (int)__builtin_amdgcn_perm(mw, mw, 0x01010101u * (uint32_t)(s0 & 3));
+    const int m1 = (int)__builtin_amdgcn_perm(mw, mw, 0x01010101u * (uint32_t)((s0 & 3) + 1));
+    o.mn[0] = v4i{m0, m0, m0, m0};
+    o.mn[1] = v4i{m1, m1, m1, m1};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint4 qv = raw.qv[j >> 1];
@@ -163,8 +159,7 @@ __device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const X &x, float 
         const v4i xv = *reinterpret_cast<const v4i *>(&x.qs[16 * g + 4 * (j >> 1) + 8 * (j & 1)]);
         dh = mfma_16x16x64(w.hi[j], xv, dh);
         dl = mfma_16x16x64(w.lo[j], xv, dl);
-        const int m4 = splat_byte_of(w.mn, j);
-        dn = mfma_16x16x64(v4i{m4, m4, m4, m4}, xv, dn);
+        dn = mfma_16x16x64(w.mn[j & 1], xv, dn);
     }
     const float xd = x.d;
 #pragma unroll
@@ -201,7 +196,7 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     __shared__ __align__(16) Q8S xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
     __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
     Unit w;
-    if (!load_unit_counted(a, blockIdx.y, w)) return;
+    if (!load_unit(a, blockIdx.y, w)) return;
     const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
     const int m = wave >> 1, rt = wave & 1;
     const int row0 = blockIdx.x * kGuRows + rt * kWaveRows;
