@@ -378,13 +378,14 @@ __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
     // 32 rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
     // rows past the end repeat the last one (their results are not stored).  The
-    // next steps' rows are in flight while the current one is dotted.  Expert
-    // row E (with a shared expert) is the shared expert's gate row.
-    const int er = a.E + a.sh;
+    // next steps' rows are in flight while the current one is dotted.  A shared
+    // expert's gate row is not a row here: the tails kernel forms its logit,
+    // which keeps 512 (256) routed experts at a whole number of rounds of tiles.
+    const int er = a.E;
     auto issue = [&](int k0, int buf) {
         for (int r = wave; r < kTileE + kTileT; r += 8) {
             const int row = min(e0 + r, er - 1);
-            const float *src = r < kTileE ? (row < a.E ? a.router + (size_t)row * n : a.sh_gate_inp)
+            const float *src = r < kTileE ? a.router + (size_t)row * n
                                           : a.fx + (size_t)min(t0 + r - kTileE, a.M - 1) * n;
             float *dst = r < kTileE ? wl[buf][r] : xl[buf][r - kTileE];
 #pragma unroll
@@ -433,7 +434,6 @@ __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
             v = row16_ggml_fold(v);
             const int e = e0 + re + r, tok = t0 + rt + t;
             if (l == 0 && e < a.E && tok < a.M) a.logits[(size_t)tok * a.E + e] = v;
-            if (l == 0 && e == a.E && a.sh && tok < a.M) a.sgl[tok] = v;
         }
     (void)lane;
 }
@@ -454,9 +454,9 @@ __device__ __forceinline__ float router_order_dot(const float *w, const float *x
     return acc;
 }
 
-// One token per workgroup of 512 threads: wave 0 runs the router tail
-// (softmax, top-k, renorm) on the token's logits, and wave b forms Q8_K of
-// block b of its fx.
+// One token per workgroup of 640 threads: wave 0 runs the router tail
+// (softmax, top-k, renorm) on the token's logits, wave b + 1 forms Q8_K of
+// block b of its fx, and wave 9 the shared expert's gate logit.
 // The pair's expert for the grouping: its id clamped into range (an id out of
 // range counts as expert 0), or -1 where an earlier slot of the token holds the
 // same clamped id, so that a token joins a group once.  ids: the token's k ids
@@ -475,18 +475,21 @@ __device__ __forceinline__ int pair_expert(int id, int j, int k, int n_ids) {
 // (softmax, top-k, renorm) on the token's logits and writes the pairs' experts
 // for the grouping from the selection it holds; wave b + 1 forms Q8_K of block
 // b of its fx.
-__global__ __launch_bounds__(576) void route_tails_kernel(BatchedArgs a) {
+__global__ __launch_bounds__(640) void route_tails_kernel(BatchedArgs a) {
     constexpr int nb = kRouteN / QK;
-    static_assert(64 * (nb + 1) == 576, "a tail wave and a wave per fx block");
+    static_assert(64 * (nb + 2) == 640, "a tail wave, a wave per fx block and a shared-gate wave");
     const int t = blockIdx.x, wave = wave_index(), lane = threadIdx.x & 63;
     if (wave == 0) {
         const int id = router_tail<false>(a.logits, a.E, a.k, a.renorm, a.sel, a.wsel, t);
         const int e = pair_expert(lane < a.k ? id : 0, lane, a.k, a.n_ids);
         const int kk = a.k + a.sh;  // pair (t, k): the shared expert, id n_ids
         if (lane < kk) a.pexp[(size_t)t * kk + lane] = lane < a.k ? e : a.n_ids;
-    } else {
+    } else if (wave <= nb) {
         const int b = wave - 1;
         wave_quantize_q8l(a.fx + (size_t)t * kRouteN + b * QK, q8(a.q8x) + (size_t)t * nb + b);
+    } else if (a.sh) {
+        const float v = router_order_dot(a.sh_gate_inp, a.fx + (size_t)t * kRouteN);
+        if (lane == 0) a.sgl[t] = v;
     }
 }
 
@@ -936,12 +939,12 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
         return hipErrorInvalidValue;
     if (a.M > kMaxTok) {
-        const dim3 rg((a.E + a.sh + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT);
+        const dim3 rg((a.E + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT);
         if (rg.x * rg.y > 256)  // more tiles than CUs: two workgroups a CU
             hipLaunchKernelGGL(route_gemm_kernel<256>, rg, dim3(512), 0, s, a);
         else
             hipLaunchKernelGGL(route_gemm_kernel<512>, rg, dim3(512), 0, s, a);
-        hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(576), 0, s, a);
+        hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(640), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
     }
