@@ -245,9 +245,12 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
         asm volatile("" ::"v"(t.hi[0]), "v"(t.hi[1]), "v"(t.hi[2]), "v"(t.hi[3]), "v"(t.lo[0]), "v"(t.lo[1]),
                      "v"(t.lo[2]), "v"(t.lo[3])
                      : "memory");
+        // the next super-block's activation copies issue before its weight
+        // loads (both are waited for at the next super-block; copies first
+        // measured 3 % faster for the layer at 512 tokens)
         if (b + 1 < NB) {
-            q4_raw_load(W, rb, b + 1, raw);
             stage_x(b + 1, (b + 1) & 1);
+            q4_raw_load(W, rb, b + 1, raw);
         }
         const Q8S *xb = xs[b & 1];
 #pragma unroll
