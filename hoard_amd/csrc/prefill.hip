@@ -204,9 +204,10 @@ __global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
     const uint8_t *W = (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)row0 * rb;
     const int nch = (w.n + 15) >> 4;
     // this lane's granules of the x copy: chunks wave, wave + 4, ...; only the
-    // unit's token chunks are copied, token places past its end copy its last token
+    // unit's tokens are copied (the MFMA columns of the places past them read
+    // whatever the buffer holds, and their results are not stored)
     constexpr int kXJ = (kXChunksPerBlock + 3) / 4;
-    const int ngran = nch * 16 * kXGran;
+    const int ngran = w.n * kXGran;
     // byte offsets into q8x (it holds at most 512 tokens' blocks): half the
     // registers of pointers
     uint32_t xoff[kXJ];
