@@ -98,6 +98,7 @@ struct BatchedArgs {
     int *ptok, *pslot;      // [M*k] token and slot of each sorted pair
     int *pexp;              // [M*k] expert of each pair for the grouping, -1 for one that joins none
     int *units;             // [max_units][4] expert, first sorted pair, pairs (0: no unit), unused
+    float *q8hd;            // [pairs][4] the scales d of each sorted pair's Q8_K(h) blocks (prefill)
     int *n_units;           // [1]
     int max_units;
     // The gated shared expert (sh = 1): every token's pair (t, k) with the

@@ -1169,7 +1169,7 @@ namespace {
 struct BatchedLayout {
     int T, Ts, umax, umax_s, max_units;
     size_t q8x, q8h, hbuf, ybuf, n_ints, hist, counters;  // bytes (n_ints: ints)
-    size_t o_slot_of, o_uexp, o_ucount, o_utok, o_uslot, o_ysrc, o_bad, o_goff, o_ptok, o_pslot, o_pexp, o_units,
+    size_t o_slot_of, o_uexp, o_ucount, o_utok, o_uslot, o_ysrc, o_bad, o_goff, o_ptok, o_pslot, o_pexp, o_units, o_q8hd,
         o_nunits, o_sgl;
 };
 
@@ -1207,6 +1207,7 @@ BatchedLayout batched_layout(const hoard_moe_cfg &c, int T) {
     L.o_pslot = take(pairs);
     L.o_pexp = take(pairs);
     L.o_units = take((size_t)4 * L.max_units);
+    L.o_q8hd = take((size_t)4 * pairs);  // floats
     L.o_nunits = take(1);
     L.o_sgl = take(T);  // floats
     L.n_ints = o;
@@ -1234,6 +1235,7 @@ void bind_batched(hoard::BatchedArgs &a, const BatchedLayout &L, uint8_t *q8x, u
     a.pslot = ints + L.o_pslot;
     a.pexp = ints + L.o_pexp;
     a.units = ints + L.o_units;
+    a.q8hd = reinterpret_cast<float *>(ints + L.o_q8hd);
     a.n_units = ints + L.o_nunits;
     a.max_units = hoard::prefill_max_units(a.M, a.k + a.sh, a.n_ids + a.sh);
     a.sgl = reinterpret_cast<float *>(ints + L.o_sgl);

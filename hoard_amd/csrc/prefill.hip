@@ -288,8 +288,10 @@ __global__ __launch_bounds__(256) void pf_quant_h_kernel(BatchedArgs a) {
     const int pos = blockIdx.x, b = wave_index();
     const int nbh = a.n_ff / QK;
     if (b >= nbh) return;
-    wave_quantize_q8l(a.hbuf + (size_t)pos * a.n_ff + (size_t)b * QK,
-                      reinterpret_cast<Q8L *>(a.q8h) + (size_t)pos * nbh + b);
+    const float d = wave_quantize_q8l(a.hbuf + (size_t)pos * a.n_ff + (size_t)b * QK,
+                                      reinterpret_cast<Q8L *>(a.q8h) + (size_t)pos * nbh + b);
+    // the scales again, four to a pair: the down kernels copy a unit's in one 16-byte load a lane
+    if ((threadIdx.x & 63) == 0) a.q8hd[(size_t)pos * 4 + b] = d;
 }
 
 // -- down: 64 rows of the unit's expert, y to its (token, slot) place -----------
@@ -418,6 +420,12 @@ __device__ __forceinline__ void q6_load_xb(const Q8L &x, Q6XB &o) {
 #pragma unroll
     for (int jc = 0; jc < 4; ++jc) o.x[jc] = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
     o.xd = x.d;
+}
+// The quants alone, the scale coming from elsewhere.
+__device__ __forceinline__ void q6_load_xq(const Q8L &x, Q6XB &o) {
+    const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int jc = 0; jc < 4; ++jc) o.x[jc] = *reinterpret_cast<const v4i *>(&x.qs[16 * jc + 4 * g]);
 }
 
 __device__ __forceinline__ void q6_fold_step(const Q6Fold &w, const Q6XB &x, float acc[4]) {
@@ -672,6 +680,7 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     static_assert(kTileBytes % 16 == 0, "the tile copies in 16-byte units");
     __shared__ __align__(16) uint8_t tile[kTileBytes];
     __shared__ int yrow[kUnitTokens];  // y row (token * slots + slot) of each of the unit's pairs
+    __shared__ __align__(16) float xds[4][kUnitTokens][4];  // each wave's copy of the pairs' Q8_K(h) scales
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
@@ -680,6 +689,12 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
     auto x_of = [&](int ch, int b) -> const Q8L & {
         return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
+    };
+    // the pairs' block scales come from the wave's LDS copy, copied with the
+    // tile: a 4-byte load of a scale with every chunk's quants cost more
+    auto load_x = [&](int ch, int b, Q6XB &o) {
+        q6_load_xq(x_of(ch, b), o);
+        o.xd = xds[wave][min(ch * 16 + c, kUnitTokens - 1)][b];
     };
     // Chunk ch of a super-block takes its activation operands from x[ch % 2]:
     // chunk 0's are loaded before the fold, each later chunk's while the one
@@ -694,6 +709,8 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
     constexpr int kWaveBytes = kWaveRows * kRowBytes;
     static_assert(kWaveBytes % 16 == 0, "a wave's rows copy in 16-byte units");
     uint8_t *T = tile + wave * kWaveBytes;
+    dma_lanes(reinterpret_cast<uint8_t *>(&xds[wave][0][0]),
+              reinterpret_cast<const uint8_t *>(a.q8hd + (size_t)(w.p0 + min(lane, w.n - 1)) * 4));
     dma_wave_copy_nt(T, batched_down(a, w.e) + (size_t)(rt0 + wave * kWaveRows) * kRowBytes, kWaveBytes);
     lds_dma_wait();
     if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
@@ -704,16 +721,16 @@ __global__ __launch_bounds__(256, 3) void pf_down_q6_kernel(BatchedArgs a) {
         for (int i = 0; i < 4; ++i) acc[ch][i] = 0.0f;
 #pragma unroll 1
     for (int b = 0; b < NBH; ++b) {
-        q6_load_xb(x_of(0, b), x0);
+        load_x(0, b, x0);
         Q6Fold f;
         q6_fold(T, kRowBytes, b, f);
-        if (nch > 1) q6_load_xb(x_of(1, b), x1);
+        if (nch > 1) load_x(1, b, x1);
         q6_fold_step(f, x0, acc[0]);
         if (nch > 1) {
-            if (nch > 2) q6_load_xb(x_of(2, b), x0);
+            if (nch > 2) load_x(2, b, x0);
             q6_fold_step(f, x1, acc[1]);
             if (nch > 2) {
-                if (nch > 3) q6_load_xb(x_of(3, b), x1);
+                if (nch > 3) load_x(3, b, x1);
                 q6_fold_step(f, x0, acc[2]);
                 if (nch > 3) q6_fold_step(f, x1, acc[3]);
             }

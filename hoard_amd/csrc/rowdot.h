@@ -25,12 +25,13 @@ static_assert(sizeof(Q8L) == 304, "Q8L is 19 x 16 bytes");
 // Wave quantisation of 256 floats to Q8_K (ggml quantize_row_q8_K semantics:
 // largest |x| with its sign, first index on ties; iscale = -127/max;
 // q = min(127, nearest_int(iscale*x)); d = 1/iscale; all-zero block -> 0).
-__device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out);
-__device__ __forceinline__ void wave_quantize_q8l(const float *x, Q8L *out) {
+__device__ __forceinline__ float wave_quantize_q8l_regs(const float v[4], Q8L *out);
+// Returns the block's scale d (in every lane).
+__device__ __forceinline__ float wave_quantize_q8l(const float *x, Q8L *out) {
     const int lane = threadIdx.x & 63;
     const float4 v4 = *reinterpret_cast<const float4 *>(x + 4 * lane);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    wave_quantize_q8l_regs(v, out);
+    return wave_quantize_q8l_regs(v, out);
 }
 
 // One Q4_K row of nb super-blocks (16-byte aligned in LDS) dotted with x.
@@ -568,7 +569,7 @@ __device__ __forceinline__ unsigned wave_max_bits(unsigned u) {
 // patterns cleared to 0 first), which orders them as the values would be, so
 // the wave max is an integer max and the element that holds it is found with
 // one compare per element, one ballot and one read of its lane.
-__device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *out) {
+__device__ __forceinline__ float wave_quantize_q8l_regs(const float v[4], Q8L *out) {
     const int lane = threadIdx.x & 63;
     unsigned b[4];
 #pragma unroll
@@ -581,7 +582,7 @@ __device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *ou
         out->qs[lane] = 0;
         if (lane < 16) out->bsums[lane] = 0;
         if (lane == 0) out->d = 0.0f;
-        return;
+        return 0.0f;
     }
     const bool h0 = b[0] == am, h1 = b[1] == am, h2 = b[2] == am, h3 = b[3] == am;
     const float c = h0 ? v[0] : (h1 ? v[1] : (h2 ? v[2] : v[3]));
@@ -600,7 +601,9 @@ __device__ __forceinline__ void wave_quantize_q8l_regs(const float v[4], Q8L *ou
     out->qs[lane] = (int32_t)packed;
     s = group4_sum(s);
     if ((lane & 3) == 0) out->bsums[lane >> 2] = (int16_t)s;
-    if (lane == 0) out->d = 1.0f / iscale;
+    const float d = 1.0f / iscale;
+    if (lane == 0) out->d = d;
+    return d;
 }
 
 }  // namespace hoard
