@@ -758,6 +758,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     static_assert(TS == kTypeQ5K || TS == kTypeQ6K, "the shared expert's down rows are Q5_K or Q6_K");
     __shared__ __align__(16) uint8_t tile[kTileBytes];
     __shared__ int yrow[kUnitTokens];  // y row (token * slots + slot) of each of the unit's pairs
+    __shared__ __align__(16) float xds[4][kUnitTokens][4];  // each wave's copy of the pairs' Q8_K(h) scales
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const bool shx = TS != kTypeQ5K && a.sh && w.e == a.n_ids;  // the shared expert's Q6_K rows
@@ -770,6 +771,8 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     // each wave copies its own 16 rows and waits for them alone
     const int wbytes = kWaveRows * rbytes;  // a multiple of 16 for both row types
     uint8_t *T = tile + wave * wbytes;
+    dma_lanes(reinterpret_cast<uint8_t *>(&xds[wave][0][0]),
+              reinterpret_cast<const uint8_t *>(a.q8hd + (size_t)(w.p0 + min(lane, w.n - 1)) * 4));
     dma_wave_copy_nt(T, batched_down(a, w.e) + (size_t)(rt0 + wave * kWaveRows) * rbytes, wbytes);
     lds_dma_wait();
     if (tid < w.n) yrow[tid] = pt * (a.k + a.sh) + ps;
@@ -777,6 +780,11 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
     const Q8L *q8h = reinterpret_cast<const Q8L *>(a.q8h);
     auto x_of = [&](int ch, int b) -> const Q8L & {
         return q8h[(size_t)(w.p0 + min(ch * 16 + c, w.n - 1)) * NBH + b];
+    };
+    // the quants from memory, the pairs' block scales from the wave's LDS copy
+    auto load_x = [&](int ch, int b, Q6XB &o) {
+        q6_load_xq(x_of(ch, b), o);
+        o.xd = xds[wave][min(ch * 16 + c, kUnitTokens - 1)][b];
     };
     float acc[kChunks][4], accm[kChunks][4];
 #pragma unroll
@@ -790,7 +798,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
                 Q6XB xc[kChunks];
 #pragma unroll
                 for (int ch = 0; ch < kChunks; ++ch)
-                    if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
+                    if (ch < nch) load_x(ch, b, xc[ch]);
                 Q6Fold f;
                 q6_fold(T, kRowBytesS, b, f);
 #pragma unroll
@@ -804,7 +812,7 @@ __global__ __launch_bounds__(256, 2) void pf_down_q5_kernel(BatchedArgs a) {
             Q6XB xc[kChunks];
 #pragma unroll
             for (int ch = 0; ch < kChunks; ++ch)
-                if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
+                if (ch < nch) load_x(ch, b, xc[ch]);
             Q5Fold f;
             q5_fold(T, kRowBytesD, b, f);
 #pragma unroll
