@@ -26,6 +26,14 @@ __device__ __forceinline__ void dma_lanes(uint8_t *dst, const uint8_t *g) {
                  : "memory", "m0");
 }
 
+// The 4-byte form: lane l copies the 4 bytes at its own source address g to
+// dst[4 l, 4 l + 4); g 4-byte aligned, dst a 4-byte aligned LDS address.
+__device__ __forceinline__ void dma_lanes4(uint8_t *dst, const uint8_t *g) {
+    const lds_void *lp = (const lds_void *)dst;
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lp);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+
 // The contiguous form: lane l copies src[16 l, 16 l + 16).
 __device__ __forceinline__ void dma_chunk(uint8_t *dst, const uint8_t *src) {
     dma_lanes(dst, src + (threadIdx.x & 63) * 16);

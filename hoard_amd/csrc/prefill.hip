@@ -609,6 +609,7 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     static_assert(kRowBytes % 16 == 0, "Q3_K rows of 8 blocks are 880 bytes: tiles start 16-byte aligned");
     __shared__ __align__(16) uint8_t tile[2][kTileBytes];
     __shared__ float gx[2][kChunks][4][64];  // gate values: [row tile][chunk][row i][lane]
+    __shared__ float xds[4][kUnitTokens * NB];  // each wave's copy of the tokens' Q8_K block scales
     Unit w;
     if (!load_unit(a, blockIdx.y, w)) return;
     const int wave = wave_index(), lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
@@ -623,10 +624,26 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
     uint8_t *T = tile[m] + rt * kWaveBytes;
     dma_wave_copy_nt(T, (m ? batched_up(a, w.e) : batched_gate(a, w.e)) + (size_t)(row0 + rt * kWaveRows) * kRowBytes,
                      kWaveBytes);
+    // the block scales of the unit's token places, place-major, into the wave's
+    // LDS copy (NB 4-byte copies a lane; the lane's place comes from the lane
+    // that read its token): a 4-byte load of a scale with every chunk's quants
+    // in the loop cost more
+    static_assert(NB == 8, "eight blocks a token: a copy covers eight places");
+    const Q8L *q8xs = reinterpret_cast<const Q8L *>(a.q8x);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int tk = __shfl(tok[j >> 1], 8 * (j & 1) + (lane >> 3));
+        dma_lanes4(reinterpret_cast<uint8_t *>(&xds[wave][64 * j]),
+                   reinterpret_cast<const uint8_t *>(&q8xs[(size_t)tk * NB + (lane & 7)].d));
+    }
     lds_dma_wait();
     const int nch = (w.n + 15) >> 4;
     const Q8L *q8x = reinterpret_cast<const Q8L *>(a.q8x);
     auto x_of = [&](int ch, int b) -> const Q8L & { return q8x[(size_t)tok[ch] * NB + b]; };
+    auto load_x = [&](int ch, int b, Q6XB &o) {
+        q6_load_xq(x_of(ch, b), o);
+        o.xd = xds[wave][(ch * 16 + c) * NB + b];
+    };
     float acc[kChunks][4];
 #pragma unroll
     for (int ch = 0; ch < kChunks; ++ch)
@@ -638,7 +655,7 @@ __global__ __launch_bounds__(256, 2) void pf_gateup_q3_kernel(BatchedArgs a) {
         Q6XB xc[kChunks];
 #pragma unroll
         for (int ch = 0; ch < kChunks; ++ch)
-            if (ch < nch) q6_load_xb(x_of(ch, b), xc[ch]);
+            if (ch < nch) load_x(ch, b, xc[ch]);
         Q3Fold f;
         q3_fold(T, kRowBytes, b, f);
 #pragma unroll
