@@ -341,19 +341,21 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 }
 
 // -- prefill-sized routing: tiled router GEMM, then tails, then the grouping -----
-// Logits of 16 experts x 16 tokens per workgroup of 512 threads.  Thread
-// (group q = tid / 32, lane l = tid % 32) holds accumulator l of ggml's x86 f32
-// dot (elements 32 i + l, i ascending) for 4 experts x 4 tokens: the rows and
-// tokens pass through LDS 512 elements at a time, every element read once per
-// 16 dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
+// Logits of 16 experts x TT tokens per workgroup of 512 threads (TT = 16, or 8
+// where 16-token tiles would leave CUs idle).  Thread (group q = tid / 32, lane
+// l = tid % 32) holds accumulator l of ggml's x86 f32 dot (elements 32 i + l,
+// i ascending) for 4 experts x TT / 4 tokens: the rows and tokens pass through
+// LDS 512 elements at a time, every element read once per 16 (8) dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
 // which fold them in ggml's order, so every logit is the single-token router's.
 // One workgroup per CU: eight waves (two per SIMD) took 4 us less per launch
 // than four waves with 4 x 8 dots each, sixteen waves with 2 x 4 each 1 us
 // more than eight.  Each K step costs a wait and a barrier besides its dots:
 // 512-element steps (4 of them) took 3.5 us less per launch than 256-element
 // ones (8), and 1024-element ones without a second buffer 1.6 us more than
-// 512 at M = 512 (four waves).
-constexpr int kTileE = 16, kTileT = 16;
+// 512 at M = 512 (four waves).  8-token tiles where 16-token ones would fill
+// at most half the CUs: 2.5 us less per layer at 128 tokens of 128 experts
+// (2.2 more at 512, where 16-token tiles fill the CUs once).
+constexpr int kTileE = 16;
 
 // K steps in LDS: the current one and the next in flight (four buffers, three
 // steps in flight, measured the same: once one step is prefetched the dots and
@@ -361,8 +363,10 @@ constexpr int kTileE = 16, kTileT = 16;
 // workgroup per CU; 256: 64 KB, two a CU, for grids of more tiles than CUs
 // (512 experts at 128 and 512 tokens: 49.5 against 2 x 12 us per launch).
 constexpr int kGemmBufs = 2;
-template <int kTileK>
+template <int kTileK, int kTileT>
 __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
+    constexpr int kTQ = kTileT / 4;  // tokens per thread group
+    static_assert((kTileE + kTileT) % 8 == 0, "every wave copies as many rows");
     __shared__ __align__(16) float wl[kGemmBufs][kTileE][kTileK];
     __shared__ __align__(16) float xl[kGemmBufs][kTileT][kTileK];
     constexpr int n = kRouteN, kSteps = n / kTileK;
@@ -370,13 +374,13 @@ __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
     constexpr int kRowsPerWave = (kTileE + kTileT) / 8 * (kTileK / 256);  // 1 KB copies each wave issues per step
     const int tid = threadIdx.x, q = tid >> 5, l = tid & 31, wave = wave_index(), lane = tid & 63;
     const int e0 = blockIdx.x * kTileE, t0 = blockIdx.y * kTileT;
-    const int re = (q & 3) * 4, rt = (q >> 2) * 4;  // this group's 4 experts and 4 tokens within the tile
-    float acc[4][4];
+    const int re = (q & 3) * 4, rt = (q >> 2) * kTQ;  // this group's 4 experts and kTQ tokens within the tile
+    float acc[4][kTQ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-    // 32 rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
+        for (int j = 0; j < kTQ; ++j) acc[i][j] = 0.0f;
+    // 16 + TT rows of 1 KB per step: expert rows then token rows, one wave per 8 rows;
     // rows past the end repeat the last one (their results are not stored).  The
     // next steps' rows are in flight while the current one is dotted.  A shared
     // expert's gate row is not a row here: the tails kernel forms its logit,
@@ -413,22 +417,22 @@ __global__ __launch_bounds__(512) void route_gemm_kernel(BatchedArgs a) {
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < kTileK / 32; ++i) {
-            float wv[4], xv[4];
+            float wv[4], xv[kTQ];
 #pragma unroll
             for (int r = 0; r < 4; ++r) wv[r] = wl[buf][re + r][32 * i + l];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xv[t] = xl[buf][rt + t][32 * i + l];
+            for (int t = 0; t < kTQ; ++t) xv[t] = xl[buf][rt + t][32 * i + l];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int t = 0; t < 4; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
+                for (int t = 0; t < kTQ; ++t) acc[r][t] = fmaf(wv[r], xv[t], acc[r][t]);
         }
         __syncthreads();  // every wave is done with this buffer before it is refilled
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < kTQ; ++t) {
             float v = acc[r][t];
             v = v + __shfl_xor(v, 16);  // accumulators l and l + 16
             v = row16_ggml_fold(v);
@@ -939,11 +943,14 @@ hipError_t launch_batched(const BatchedArgs &a, hipStream_t s) {
     if (!args_ok(a) || a.ysrc || a.n_ids != a.E || (a.M + kRouteTok - 1) / kRouteTok > kBatchedCounters - 1)
         return hipErrorInvalidValue;
     if (a.M > kMaxTok) {
-        const dim3 rg((a.E + kTileE - 1) / kTileE, (a.M + kTileT - 1) / kTileT);
+        const unsigned et = (a.E + kTileE - 1) / kTileE;
+        const dim3 rg(et, (a.M + 15) / 16);
         if (rg.x * rg.y > 256)  // more tiles than CUs: two workgroups a CU
-            hipLaunchKernelGGL(route_gemm_kernel<256>, rg, dim3(512), 0, s, a);
-        else
-            hipLaunchKernelGGL(route_gemm_kernel<512>, rg, dim3(512), 0, s, a);
+            hipLaunchKernelGGL((route_gemm_kernel<256, 16>), rg, dim3(512), 0, s, a);
+        else if (rg.x * rg.y > 128)
+            hipLaunchKernelGGL((route_gemm_kernel<512, 16>), rg, dim3(512), 0, s, a);
+        else  // at most half the CUs with 16-token tiles: 8-token ones, at most one a CU
+            hipLaunchKernelGGL((route_gemm_kernel<512, 8>), dim3(et, (a.M + 7) / 8), dim3(512), 0, s, a);
         hipLaunchKernelGGL(route_tails_kernel, dim3(a.M), dim3(640), 0, s, a);
         hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, a);
         return launch_prefill_groups(a, s);
