@@ -345,8 +345,9 @@ __global__ __launch_bounds__(256) void route_kernel(BatchedArgs a) {
 // where 16-token tiles would leave CUs idle).  Thread (group q = tid / 32, lane
 // l = tid % 32) holds accumulator l of ggml's x86 f32 dot (elements 32 i + l,
 // i ascending) for 4 experts x TT / 4 tokens: the rows and tokens pass through
-// LDS 512 elements at a time, every element read once per 16 (8) dots.  The 32 accumulators of a dot sit in the 32 lanes of a half-wave,
-// which fold them in ggml's order, so every logit is the single-token router's.
+// LDS 512 elements at a time, 8 (6) reads for every 16 (8) dots.  The 32
+// accumulators of a dot sit in the 32 lanes of a half-wave, which fold them in
+// ggml's order, so every logit is the single-token router's.
 // One workgroup per CU: eight waves (two per SIMD) took 4 us less per launch
 // than four waves with 4 x 8 dots each, sixteen waves with 2 x 4 each 1 us
 // more than eight.  Each K step costs a wait and a barrier besides its dots:
