@@ -179,7 +179,11 @@ __device__ __forceinline__ void q4_fold_step(const Q4Fold &w, const X &x, float 
 // token chunks into LDS (one buffer ahead) while each wave holds the next
 // super-block of its rows in registers; the gate waves hand their values to the
 // up waves through LDS, which form h and store it to hbuf[sorted pair][row].
-// Three workgroups share a CU.
+// Three workgroups share a CU (43 KB of LDS each).  The kernel is compiled to
+// the 128 registers of four waves a SIMD all the same: that schedule measured
+// 1 % faster for the layer than the 146-register one at three waves (a fourth
+// workgroup a CU, with the gate values over an x buffer, spilled and measured
+// 12 % slower).
 // The part of a Q8_K block the folded gate/up tiles read: the quants and the
 // scale (granules 0-15 and 18 of the block; its 16-element sums are not read).
 struct Q8S {
@@ -192,7 +196,7 @@ constexpr int kXGran = (int)sizeof(Q8S) / 16;                          // 16-byt
 constexpr int kXChunksPerBlock = (kUnitTokens * kXGran + 63) / 64;     // 1 KB copies per unit block
 
 template <int NB>
-__global__ __launch_bounds__(256, 3) void pf_gateup_kernel(BatchedArgs a) {
+__global__ __launch_bounds__(256, 4) void pf_gateup_kernel(BatchedArgs a) {
     __shared__ __align__(16) Q8S xs[2][kUnitTokens];  // the unit's Q8_K block b (two buffers)
     __shared__ float gx[2][kChunks][4][64];            // gate values: [row tile][chunk][row i][lane]
     Unit w;
